@@ -1,0 +1,201 @@
+"""ctypes binding of libactune_hip.so (include/actune_hip.h).
+
+The library is the only compute path of this package: there is no Python or
+CPU fallback. Loading fails loudly when the library is missing, and every
+call raises on a non-zero status with the library's error message.
+
+The wrappers take torch tensors (device memory and the current stream come
+from PyTorch-ROCm) and reproduce the reference's argument checks and
+messages (actune/kernels/grouped_native.cu:92-105, grouped.py:118-119, 128).
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libactune_hip.so"
+_LIB = None
+
+DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+CONFIG_AUTO = -1
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -m actune_amd.build` "
+                "(the group-64 backend has no fallback path)")
+        so = ctypes.CDLL(str(LIB_PATH))
+        so.actune_version.restype = ctypes.c_char_p
+        so.actune_last_error.restype = ctypes.c_char_p
+        so.actune_quantize_groups.argtypes = [_P, _I, _P, _I64, _I64, _I, _P, _P, _P]
+        so.actune_grouped_linear.argtypes = [_P, _P, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I, _I, _I, _P]
+        so.actune_grouped_forward.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _I64, _I64,
+                                              _I, _I, _I, _P]
+        so.actune_grouped_dots_i32.argtypes = [_P, _P, _I64, _I64, _I64, _I, _I, _I, _P, _P]
+        so.actune_config_valid.argtypes = [_I, _I64]
+        so.actune_default_config.argtypes = [_I64, _I64, _I64, _I, _I]
+        _LIB = so
+    return _LIB
+
+
+def _check(rc: int) -> None:
+    if rc:
+        msg = lib().actune_last_error().decode()
+        raise RuntimeError(msg) if rc == 2 else ValueError(msg)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype not in DTYPE_CODES:
+        raise ValueError(f"unsupported dtype {t.dtype}")
+    return DTYPE_CODES[t.dtype]
+
+
+def version() -> str:
+    return lib().actune_version().decode()
+
+
+def num_configs() -> int:
+    return lib().actune_num_configs()
+
+
+def config_valid(config: int, m: int) -> bool:
+    return bool(lib().actune_config_valid(config, m))
+
+
+def default_config(m: int, n: int, k: int, w: int, a: int) -> int:
+    return lib().actune_default_config(m, n, k, w, a)
+
+
+def _require_cuda(*tensors):
+    if not all(t.is_cuda for t in tensors if t is not None):
+        raise RuntimeError("CUDA required")
+    dev = tensors[0].device
+    if any(t is not None and t.device != dev for t in tensors):
+        raise RuntimeError("device mismatch")
+
+
+def quantize_groups(x: torch.Tensor, a: int, input_scale: torch.Tensor | None = None,
+                    packed: torch.Tensor | None = None, scales: torch.Tensor | None = None):
+    """Group-64 quantize a contiguous [M, K] tensor; returns (packed, scales)."""
+    _require_cuda(x, input_scale)
+    if x.dim() != 2 or not x.is_contiguous():
+        raise RuntimeError("contiguous [M, K] input required")
+    m, k = x.shape
+    if input_scale is not None and (input_scale.dtype != x.dtype or input_scale.numel() != k
+                                    or not input_scale.is_contiguous()):
+        raise RuntimeError("input_scale must be a contiguous [K] tensor of the input dtype")
+    if packed is None:
+        packed = torch.empty((m, k * a // 8), device=x.device, dtype=torch.uint8)
+    if scales is None:
+        scales = torch.empty((m, k // 64), device=x.device, dtype=torch.float32)
+    _check(lib().actune_quantize_groups(_ptr(x), _dtype_code(x), _ptr(input_scale), m, k, a,
+                                        _ptr(packed), _ptr(scales), _stream(x.device)))
+    return packed, scales
+
+
+def _check_linear_operands(a, as_, w, ws, bias, m, k, n, W, A):
+    if a.dtype != torch.uint8 or w.dtype != torch.uint8:
+        raise RuntimeError("packed uint8 required")
+    if as_.dtype != torch.float32 or ws.dtype != torch.float32:
+        raise RuntimeError("float scales/bias required")
+    if not (a.is_contiguous() and as_.is_contiguous() and w.is_contiguous() and ws.is_contiguous()
+            and (bias is None or bias.is_contiguous())):
+        raise RuntimeError("contiguous operands required")
+    if a.dim() != 2 or w.dim() != 2 or as_.dim() != 2:
+        raise RuntimeError("rank mismatch")
+    if not (m >= 0 and n > 0 and k > 0 and k % 64 == 0):
+        raise RuntimeError("invalid dimensions")
+    if a.size(0) != m or a.size(1) != k * A // 8 or w.size(1) != k * W // 8:
+        raise RuntimeError("packed shape mismatch")
+    if as_.size(0) != m or as_.size(1) != k // 64 or ws.numel() != n:
+        raise RuntimeError("scale shape mismatch")
+    if bias is not None and bias.numel() not in (0, n):
+        raise RuntimeError("bias shape mismatch")
+
+
+def grouped_linear(a, as_, w, ws, bias, source_or_shape, W, A, config=CONFIG_AUTO, out=None,
+                   out_dtype=None):
+    """The native op of grouped_native.cu:90-115 / grouped_big_m.cu:92-135:
+    packed activations + scales x packed weights -> [M, N] in source.dtype.
+    ``source_or_shape`` is the [M, K] source tensor (its dtype and shape
+    define the output), as in the reference op signature."""
+    _require_cuda(a, as_, w, ws, bias)
+    if isinstance(source_or_shape, torch.Tensor):
+        m, k = source_or_shape.shape
+        dtype = source_or_shape.dtype
+    else:
+        m, k = source_or_shape
+        dtype = out_dtype or torch.bfloat16
+    n = w.size(0)
+    if W not in (2, 4, 8) or A not in (2, 4, 8):
+        raise ValueError("Unsupported integer width")
+    _check_linear_operands(a, as_, w, ws, bias, m, k, n, W, A)
+    if bias is not None and bias.numel() == 0:
+        bias = None
+    if out is None:
+        out = torch.empty((m, n), device=a.device, dtype=dtype)
+    _check(lib().actune_grouped_linear(
+        _ptr(a), _ptr(as_), _ptr(w), _ptr(ws), _ptr(bias), DTYPE_CODES.get(bias.dtype, 2) if bias is not None else 2,
+        _ptr(out), _dtype_code(out), m, n, k, W, A, config, _stream(a.device)))
+    return out
+
+
+def grouped_forward(flat, w, ws, bias, W, A, input_scale=None, config=CONFIG_AUTO, out=None):
+    """Quantize + GEMM for a contiguous [M, K] input (GroupedLinear.forward's
+    device work, grouped.py:127-143); returns [M, N] in flat.dtype."""
+    _require_cuda(flat, w, ws, bias, input_scale)
+    m, k = flat.shape
+    n = w.size(0)
+    if w.size(1) != k * W // 8:
+        raise RuntimeError("packed shape mismatch")
+    packed = torch.empty((m, k * A // 8), device=flat.device, dtype=torch.uint8)
+    scales = torch.empty((m, k // 64), device=flat.device, dtype=torch.float32)
+    if out is None:
+        out = torch.empty((m, n), device=flat.device, dtype=flat.dtype)
+    bias_dt = 2 if bias is None else _dtype_code(bias)
+    _check(lib().actune_grouped_forward(
+        _ptr(flat), _dtype_code(flat), _ptr(input_scale), _ptr(packed), _ptr(scales), _ptr(w), _ptr(ws),
+        _ptr(bias), bias_dt, _ptr(out), m, n, k, W, A, config, _stream(flat.device)))
+    return out
+
+
+def grouped_dots(a, w, m, k, W, A, config=CONFIG_AUTO):
+    """Exact int32 per-group dots [M, N, K/64] through kernel ``config``."""
+    _require_cuda(a, w)
+    n = w.size(0)
+    dots = torch.empty((m, n, k // 64), device=a.device, dtype=torch.int32)
+    _check(lib().actune_grouped_dots_i32(_ptr(a), _ptr(w), m, n, k, W, A, config, _ptr(dots),
+                                         _stream(a.device)))
+    return dots
+
+
+class Extension:
+    """Object form of the reference's JIT extension (grouped.py:97-105): its
+    ``linear`` has the reference op signature plus an optional config."""
+
+    @staticmethod
+    def linear(a, as_, w, ws, bias, source, W, A, config=CONFIG_AUTO):
+        return grouped_linear(a, as_, w, ws, bias, source, W, A, config)
+
+
+def extension() -> Extension:
+    lib()
+    return Extension()

@@ -1,0 +1,134 @@
+"""Group-64 packed W{2,4,8} x A{2,4,8} linear modules on the HIP backend.
+
+Same module surface as actune/kernels/grouped.py:108-167: ``pack_rows``,
+``GroupedLinear`` (install-time weight codes + packed rows, forward = group-64
+quantize + packed GEMM) and ``GroupedPaddedLinear`` (K padded to 128, one
+backend per mode, dispatch on the active precision profile, per-call
+counters). Buffers, dtypes and byte counts match the reference exactly, so
+``install_bank``'s storage check and state dicts carry over unchanged.
+
+The forward makes one library call, ``actune_grouped_forward``: the group-64
+quantizer (with the channel-scale division fused in when a ResidentLinear
+passes one) and the packed GEMM, both launched on the current HIP stream.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _native
+from ..precision import active_precision_profile
+from .quantizers import weight_codes
+
+CONFIG_AUTO = _native.CONFIG_AUTO
+
+
+def extension():
+    """The native op object (reference: the JIT extension, grouped.py:97-105)."""
+    return _native.extension()
+
+
+def pack_rows(q, bits):
+    """Pack int8 codes [N, K] into u8 [N, K*bits/8]: code k of a row sits in
+    byte k*bits/8 at bit (k % (8/bits))*bits (grouped.py:108-111 layout)."""
+    per = 8 // bits
+    mask = (1 << bits) - 1
+    fields = (q.to(torch.int32) & mask).reshape(q.shape[0], -1, per)
+    packed = torch.zeros(fields.shape[:2], dtype=torch.int32, device=q.device)
+    for j in range(per):
+        packed |= fields[..., j] << (j * bits)
+    return packed.to(torch.uint8).contiguous()
+
+
+class GroupedLinear(torch.nn.Module):
+    """One (W, A) version of a linear layer: packed weight codes + per-row
+    scale (+ bias), forward through the HIP library."""
+
+    def __init__(self, linear, w, a, ratios):
+        super().__init__()
+        self.in_features = linear.in_features
+        self.out_features = linear.out_features
+        self.w, self.a = w, a
+        if self.in_features % 64:
+            raise ValueError("Grouped backend requires K divisible by 64")
+        if w not in (2, 4, 8) or a not in (2, 4, 8):
+            raise ValueError("Unsupported integer width")
+        codes, scale = weight_codes(linear.weight, w, a, clip_ratios=ratios)
+        self.register_buffer("packed_weight", pack_rows(codes, w))
+        self.register_buffer("weight_scale", scale.contiguous())
+        bias = None
+        if linear.bias is not None:
+            bias = linear.bias.detach().clone()
+            if a == 4:
+                bias = bias.float()
+        self.register_buffer("bias", bias)
+        # kernel configuration id (ACTUNE_CONFIG_AUTO or a tuned id); not a buffer
+        self.config = CONFIG_AUTO
+
+    def forward(self, x, input_scale=None):
+        """y = grouped linear of x (optionally x / input_scale, rounded to
+        x's dtype, fused into the quantizer)."""
+        if not x.is_cuda:
+            raise ValueError("Grouped integer backend requires CUDA")
+        flat = x.reshape(-1, self.in_features).contiguous()
+        if input_scale is not None and input_scale.dtype != flat.dtype:
+            flat = (flat / input_scale).contiguous()
+            input_scale = None
+        out = _native.grouped_forward(flat, self.packed_weight, self.weight_scale, self.bias,
+                                      self.w, self.a, input_scale=input_scale, config=self.config)
+        return out.reshape(*x.shape[:-1], self.out_features)
+
+
+class GroupedPaddedLinear(torch.nn.Module):
+    """Resident set of GroupedLinear versions of one layer; the active
+    precision profile picks the version for each call."""
+
+    def __init__(self, linear, assignments, initial, clips):
+        super().__init__()
+        logical = linear.in_features
+        padded = -(-logical // 128) * 128
+        if padded != logical:
+            linear = _zero_padded(linear, padded)
+        self.in_features = logical
+        self.out_features = linear.out_features
+        self.padding = padded - logical
+        self.assignments = dict(assignments)
+        self.default_profile = initial
+        modes = sorted(set(self.assignments.values()))
+        self.backends = torch.nn.ModuleDict(
+            {mode: GroupedLinear(linear, int(mode[1]), int(mode[3]), clips[mode]) for mode in modes})
+        self.register_buffer("_weight_dtype", torch.empty(0, device=linear.weight.device,
+                                                          dtype=linear.weight.dtype))
+        self.calls = 0
+        self.input_elements = 0
+
+    @property
+    def weight(self):
+        """Empty tensor of the weight dtype, for callers that sniff .weight.dtype."""
+        return self._weight_dtype
+
+    def active_backend(self):
+        return self.backends[self.assignments[active_precision_profile() or self.default_profile]]
+
+    def forward(self, x):
+        return self._dispatch(x, None)
+
+    def _dispatch(self, x, input_scale):
+        self.calls += 1
+        self.input_elements += x.numel()
+        if self.padding:
+            x = torch.nn.functional.pad(x, (0, self.padding))
+            if input_scale is not None:
+                input_scale = torch.nn.functional.pad(input_scale, (0, self.padding), value=1.0)
+        return self.active_backend()(x, input_scale)
+
+
+def _zero_padded(linear, padded):
+    """Copy of `linear` with zero weight columns up to `padded` inputs."""
+    fc = torch.nn.Linear(padded, linear.out_features, bias=linear.bias is not None,
+                         device=linear.weight.device, dtype=linear.weight.dtype)
+    with torch.no_grad():
+        fc.weight.zero_()
+        fc.weight[:, :linear.in_features].copy_(linear.weight)
+        if fc.bias is not None:
+            fc.bias.copy_(linear.bias)
+    return fc

@@ -1,0 +1,95 @@
+"""Bit-exact kernel-configuration selection for the grouped backend.
+
+Same contract as actune/kernels/tuning.py:16-70: for each call signature
+(W, A, M, K, N, dtype, bias) the first call runs the default configuration
+and every candidate, discards candidates whose output is not bit-identical
+to the default's, times the rest with a 10-launch graph replayed 5 times
+(median), adopts the fastest if it beats the default by >= 5 %, caches the
+choice process-wide in TUNINGS and refuses to tune during graph capture.
+
+Candidates are the library's configuration ids valid for M (small-M split-K
+variants and MFMA tile shapes). All of them reduce in the same fixed order,
+so every candidate is expected to pass the bit-identity check.
+"""
+from __future__ import annotations
+
+import statistics
+
+import torch
+
+from .. import _native
+
+TUNINGS = {}
+
+
+def _time_graph(launch, config, repeats=5, launches=10):
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            launch(config)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(launches):
+            launch(config)
+    times = []
+    for _ in range(repeats):
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        stop.record()
+        stop.synchronize()
+        times.append(start.elapsed_time(stop) / launches)
+    del graph
+    return statistics.median(times)
+
+
+def select(key, launch, configurations, default):
+    """Pick the fastest configuration whose output equals the default's."""
+    if key in TUNINGS:
+        return TUNINGS[key]["selected"]
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("Kernel geometry must be warmed before graph capture")
+    expected = launch(default)
+    torch.cuda.synchronize()
+    candidates = []
+    for config in configurations:
+        result = launch(config)
+        torch.cuda.synchronize()
+        if not torch.equal(expected, result):
+            candidates.append(dict(config=config, exact=False))
+            continue
+        candidates.append(dict(config=config, exact=True, ms=_time_graph(launch, config)))
+    exact = [c for c in candidates if c["exact"]]
+    base = next(c for c in exact if c["config"] == default)
+    best = min(exact, key=lambda c: c["ms"])
+    chosen = best["config"] if best["ms"] < 0.95 * base["ms"] else default
+    TUNINGS[key] = dict(selected=chosen, candidates=candidates)
+    print("geometry", key, "selected", chosen, "baseline_ms", base["ms"], "best_ms", best["ms"], flush=True)
+    return chosen
+
+
+def grouped_forward(self, x, input_scale=None):
+    """GroupedLinear.forward with per-signature configuration selection
+    (installed by install_bank(tune=True))."""
+    if not x.is_cuda:
+        raise ValueError("Grouped integer backend requires CUDA")
+    flat = x.reshape(-1, self.in_features).contiguous()
+    if input_scale is not None and input_scale.dtype != flat.dtype:
+        flat = (flat / input_scale).contiguous()
+        input_scale = None
+    m, k = flat.shape
+    n = self.out_features
+    packed, scales = _native.quantize_groups(flat, self.a, input_scale)
+
+    def launch(config):
+        return _native.grouped_linear(packed, scales, self.packed_weight, self.weight_scale, self.bias,
+                                      flat, self.w, self.a, config)
+
+    configs = [c for c in range(_native.num_configs()) if _native.config_valid(c, m)]
+    default = _native.default_config(m, n, k, self.w, self.a)
+    key = ("grouped", self.w, self.a, m, k, n, str(x.dtype), self.bias is not None)
+    config = select(key, launch, configs, default)
+    return launch(config).reshape(*x.shape[:-1], n)

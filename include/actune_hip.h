@@ -1,0 +1,104 @@
+/*
+ * actune_hip.h - C ABI of the MI355X (gfx950) group-64 packed-integer linear
+ * backend, libactune_hip.so.
+ *
+ * Plain pointers, sizes and a hipStream_t passed as void*. No allocation, no
+ * host synchronisation, no exceptions: every entry point is legal inside
+ * hipStreamBeginCapture and returns a status; on failure
+ * actune_last_error() holds a message for the calling thread.
+ *
+ * Data formats are the reference's (zanehpn/Actune):
+ *   packed activations  u8  [M, K*A/8]  code k at byte k*A/8, bit (k%(8/A))*A
+ *   activation scales   f32 [M, K/64]
+ *   packed weights      u8  [N, K*W/8]  same little-endian field order
+ *   weight scale        f32 [N]
+ *   output              [M, N] in bf16 / f16 / f32 (row-major)
+ * Pointers to packed data and to x must be 16-byte aligned.
+ */
+#ifndef ACTUNE_HIP_H
+#define ACTUNE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ACTUNE_OK = 0, ACTUNE_ERR_INVALID = 1, ACTUNE_ERR_DEVICE = 2 };
+enum { ACTUNE_DTYPE_BF16 = 0, ACTUNE_DTYPE_F16 = 1, ACTUNE_DTYPE_F32 = 2 };
+#define ACTUNE_CONFIG_AUTO (-1)
+
+/* Library version string. */
+const char* actune_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* actune_last_error(void);
+
+/*
+ * Group-64 activation quantizer. Replaces the _quantize_groups Triton launch,
+ * actune/kernels/grouped.py:55-71 (launched at :132-133), with the
+ * channel-scale division of actune/layers.py:41-42 fused in when input_scale
+ * is non-NULL (input_scale has x's dtype and K entries; the quotient is
+ * rounded to that dtype before quantization).
+ * x: [M, K] in x_dtype; packed: [M, K*A/8]; scales: [M, K/64].
+ */
+int actune_quantize_groups(const void* x, int x_dtype, const void* input_scale, int64_t M, int64_t K,
+                           int A, uint8_t* packed, float* scales, void* stream);
+
+/*
+ * Packed grouped linear. Replaces the native op `linear(a, as, w, ws, bias,
+ * source, W, A[, config])` of actune/kernels/grouped_native.cu:90-115 and
+ * grouped_big_m.cu:92-135, and the _group_gemm Triton launch of
+ * actune/kernels/grouped.py:74-94, 138-142, for all nine W{2,4,8} x A{2,4,8}
+ * pairs. bias may be NULL; bias_dtype gives its element type (the reference
+ * keeps it in the weight dtype, or f32 when A == 4, grouped.py:123-125).
+ * config: ACTUNE_CONFIG_AUTO or an id below actune_num_configs(); every
+ * config gives bit-identical results (fixed chunked fp32 reduction order).
+ */
+int actune_grouped_linear(const uint8_t* a, const float* a_scales, const uint8_t* w,
+                          const float* w_scale, const void* bias, int bias_dtype, void* out,
+                          int out_dtype, int64_t M, int64_t N, int64_t K, int W, int A, int config,
+                          void* stream);
+
+/*
+ * Quantize + linear in one call (two launches): the whole per-call device
+ * work of GroupedLinear.forward, actune/kernels/grouped.py:127-143.
+ * a_buf [M, K*A/8] and scale_buf [M, K/64] are caller-owned scratch that
+ * receive the packed activations and their scales.
+ */
+int actune_grouped_forward(const void* x, int x_dtype, const void* input_scale, uint8_t* a_buf,
+                           float* scale_buf, const uint8_t* w, const float* w_scale, const void* bias,
+                           int bias_dtype, void* out, int64_t M, int64_t N, int64_t K, int W, int A,
+                           int config, void* stream);
+
+/*
+ * Exact per-group int32 dots dots[m][n][g] = sum_{k in g} a[m,k] * w[n,k]
+ * computed by the integer path of kernel config `config` (test/debug; the
+ * reference has no counterpart, it checks dots only through its float
+ * output, tests/test_kernels.py:28-49). dots: [M, N, K/64].
+ */
+int actune_grouped_dots_i32(const uint8_t* a, const uint8_t* w, int64_t M, int64_t N, int64_t K,
+                            int W, int A, int config, int32_t* dots, void* stream);
+
+/*
+ * Kernel configurations, the counterpart of the 13 tile geometries of
+ * actune/kernels/grouped_big_m.cu:115-130 selected by tuning.py:16-45.
+ * actune_config_valid: 1 if `config` can run a call with M rows.
+ * actune_default_config: the config ACTUNE_CONFIG_AUTO resolves to.
+ */
+int actune_num_configs(void);
+int actune_config_valid(int config, int64_t M);
+int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A);
+
+/*
+ * Host-only check of the operand element orders the kernels rely on
+ * (sub-byte unpack and cross-width reorder for every (W, A) pair). Returns 0
+ * when all orders agree; touches no GPU. No reference counterpart.
+ */
+int actune_layout_selftest(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ACTUNE_HIP_H */

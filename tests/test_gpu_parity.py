@@ -1,0 +1,183 @@
+"""GPU parity of the HIP path against the CPU oracle, through the C ABI.
+
+Bar: packed activation codes, activation scales and int32 group dots are
+bit-exact; the output is bit-exact against the oracle evaluated in the
+library's canonical fp32 order (16 quad-aligned K-chunks); against the
+reference's own float criterion (dequantize-then-matmul,
+tests/test_kernels.py:42-48) it is within rtol = atol = 0.02; the max
+abs/rel deviation from the reference's sequential fp32 order is reported and
+bounded by 2 bf16 ulps (2 * 2^-8 relative) plus 1e-3 absolute.
+"""
+import numpy as np
+import pytest
+import torch
+
+from actune_amd import _native
+from oracle import oracle as O
+from tests.helpers import PAIRS, bits, canonical_bounds, dtype_name, oracle_activation, oracle_weight, rel_err, seeded_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _packed_weight(w, W, A, ratios=None):
+    codes, scale = oracle_weight(w, W, A, ratios)
+    return codes, scale, torch.from_numpy(O.pack_rows(codes, W)).to(DEV), torch.from_numpy(scale).to(DEV)
+
+
+# ---------------------------------------------------------------- quantizer
+@pytest.mark.parametrize("A", [2, 4, 8])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("shape", [(1, 64), (17, 128), (3, 4096), (50, 1024), (64, 11008)])
+def test_quantizer_bit_exact(A, dtype, shape):
+    m, k = shape
+    x, _, _ = seeded_inputs(m, k, 1, seed=m * 7 + k + A, dtype=dtype)
+    x[0, :64] = 0  # an all-zero group
+    packed, scales = _native.quantize_groups(x.to(DEV), A)
+    want_p, want_s, _ = oracle_activation(x, A)
+    np.testing.assert_array_equal(packed.cpu().numpy(), want_p)
+    np.testing.assert_array_equal(scales.cpu().numpy(), want_s)
+
+
+@pytest.mark.parametrize("A", [2, 4, 8])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_quantizer_fused_input_scale_bit_exact(A, dtype):
+    x, _, _ = seeded_inputs(9, 384, 1, seed=A, dtype=dtype)
+    scale = torch.linspace(0.3, 3.0, 384).to(dtype)
+    packed, scales = _native.quantize_groups(x.to(DEV), A, scale.to(DEV))
+    want_p, want_s, _ = oracle_activation(x, A, scale)
+    np.testing.assert_array_equal(packed.cpu().numpy(), want_p)
+    np.testing.assert_array_equal(scales.cpu().numpy(), want_s)
+    # and it equals quantizing torch's own x / scale (layers.py:41-42)
+    p2, s2 = _native.quantize_groups((x.to(DEV) / scale.to(DEV)).contiguous(), A)
+    assert torch.equal(p2, packed) and torch.equal(s2, scales)
+
+
+# ---------------------------------------------------------------- int32 dots
+SHAPES = [(1, 64, 32), (17, 128, 96), (5, 320, 48), (16, 1024, 80), (3, 192, 16), (40, 256, 72)]
+
+
+@pytest.mark.parametrize("W,A", PAIRS)
+@pytest.mark.parametrize("shape", SHAPES)
+def test_int32_group_dots_bit_exact_every_config(W, A, shape):
+    m, k, n = shape
+    x, w, _ = seeded_inputs(m, k, n, seed=W * 100 + A + m)
+    a_packed, _, a_codes = oracle_activation(x, A)
+    w_codes, _, w_dev, _ = _packed_weight(w, W, A)
+    want = O.group_dots(a_codes, w_codes)
+    a_dev = torch.from_numpy(a_packed).to(DEV)
+    for config in range(_native.num_configs()):
+        if not _native.config_valid(config, m):
+            continue
+        got = _native.grouped_dots(a_dev, w_dev, m, k, W, A, config).cpu().numpy()
+        np.testing.assert_array_equal(got, want, err_msg=f"config {config}")
+
+
+# ---------------------------------------------------------------- outputs
+def _run_linear(x, w, b, W, A, config, out_dtype=None):
+    a_packed, a_scales, a_codes = oracle_activation(x, A)
+    w_codes, w_scale, w_dev, ws_dev = _packed_weight(w, W, A)
+    a_dev = torch.from_numpy(a_packed).to(DEV)
+    s_dev = torch.from_numpy(a_scales).to(DEV)
+    bias = None
+    if b is not None:
+        bias = b.float() if A == 4 else b  # the reference's bias storage rule
+    out = _native.grouped_linear(a_dev, s_dev, w_dev, ws_dev, None if bias is None else bias.to(DEV),
+                                 (x.shape[0], x.shape[1]), W, A, config, out_dtype=out_dtype or x.dtype)
+    return out, (a_codes, a_scales, w_codes, w_scale, None if bias is None else bias.float().numpy())
+
+
+@pytest.mark.parametrize("W,A", PAIRS)
+@pytest.mark.parametrize("shape", [(1, 64, 32), (17, 128, 96), (8, 4096, 64), (50, 1024, 48)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_output_bit_exact_in_canonical_order(W, A, shape, with_bias):
+    m, k, n = shape
+    x, w, b = seeded_inputs(m, k, n, seed=W + 10 * A + m, bias=with_bias)
+    G = k // 64
+    outs = {}
+    for config in range(_native.num_configs()):
+        if not _native.config_valid(config, m):
+            continue
+        out, (ac, asc, wc, wsc, bf) = _run_linear(x, w, b, W, A, config)
+        outs[config] = out
+        want = O.linear(ac, asc, wc, wsc, bf, bounds=canonical_bounds(G))
+        np.testing.assert_array_equal(bits(out), O.round_out(want, "bf16"), err_msg=f"config {config}")
+    first = next(iter(outs.values()))
+    assert all(torch.equal(first, o) for o in outs.values())  # every config bit-identical
+
+
+@pytest.mark.parametrize("W,A", PAIRS)
+@pytest.mark.parametrize("shape", [(1, 64, 32), (17, 128, 96)])
+def test_reference_float_criterion(W, A, shape):
+    """tests/test_kernels.py:28-49 restated: nn.Linear init with bias, x ~ randn,
+    output vs F.linear(activation_reference(x), q.float() * scale, bias)."""
+    m, k, n = shape
+    torch.manual_seed(7)
+    lin = torch.nn.Linear(k, n, bias=True, dtype=torch.bfloat16)
+    x = torch.randn(m, k, dtype=torch.bfloat16)
+    out, (ac, asc, wc, wsc, bf) = _run_linear(x, lin.weight.detach(), lin.bias.detach(), W, A, _native.CONFIG_AUTO)
+    exp = O.reference_float_linear(x.float().numpy(), A, wc, wsc, bf)
+    exp_bf16 = O.bf16_bits_to_f32(O.f32_to_bf16_bits(exp))
+    got = out.float().cpu().numpy()
+    np.testing.assert_allclose(got, exp_bf16, rtol=0.02, atol=0.02)
+    assert out.shape == (m, n)
+
+
+@pytest.mark.parametrize("W,A", PAIRS)
+def test_deviation_from_sequential_order_is_bounded(W, A):
+    m, k, n = 8, 4096, 256
+    x, w, _ = seeded_inputs(m, k, n, seed=3 * W + A)
+    out, (ac, asc, wc, wsc, _) = _run_linear(x, w, None, W, A, _native.CONFIG_AUTO)
+    seq = O.linear(ac, asc, wc, wsc)  # the reference kernels' sequential order
+    got = out.float().cpu().numpy()
+    abs_e, rel_e = rel_err(got, seq)
+    print(f"W{W}A{A}: max abs {abs_e:.3e} max rel {rel_e:.3e} vs sequential fp32 order")
+    assert np.all(np.abs(got - seq) <= 2 * 2.0**-8 * np.abs(seq) + 1e-3)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("W,A", [(4, 8), (2, 4), (8, 2)])
+def test_output_dtypes(out_dtype, W, A):
+    m, k, n = 5, 256, 40
+    x, w, b = seeded_inputs(m, k, n, seed=5, bias=True)
+    out, (ac, asc, wc, wsc, bf) = _run_linear(x, w, b, W, A, _native.CONFIG_AUTO, out_dtype=out_dtype)
+    want = O.linear(ac, asc, wc, wsc, bf, bounds=canonical_bounds(k // 64))
+    np.testing.assert_array_equal(bits(out), O.round_out(want, dtype_name(out_dtype)))
+
+
+def test_grouped_forward_matches_two_step_path():
+    m, k, n, W, A = 6, 512, 64, 4, 8
+    x, w, b = seeded_inputs(m, k, n, seed=9, bias=True)
+    _, _, w_dev, ws_dev = _packed_weight(w, W, A)
+    xd = x.to(DEV)
+    one = _native.grouped_forward(xd, w_dev, ws_dev, b.to(DEV), W, A)
+    p, s = _native.quantize_groups(xd, A)
+    two = _native.grouped_linear(p, s, w_dev, ws_dev, b.to(DEV), xd, W, A)
+    assert torch.equal(one, two)
+
+
+# ---------------------------------------------------------------- full sizes
+@pytest.mark.parametrize("m,n,k,W,A", [
+    (1, 4096, 4096, 4, 8), (8, 11008, 4096, 4, 8), (1, 4096, 11008, 4, 8),
+    (512, 4096, 4096, 8, 8), (512, 11008, 4096, 4, 8), (256, 2048, 2048, 4, 4),
+    (50, 4096, 1024, 2, 4), (1, 256, 2048, 4, 4), (256, 2048, 16384, 4, 4),
+])
+def test_full_size_sampled_parity(m, n, k, W, A):
+    """BASELINE shapes: every output row against the oracle on 64 sampled
+    columns (bit-exact, canonical order), plus the quantizer on all of x."""
+    x, w, _ = seeded_inputs(m, k, n, seed=m + n + k)
+    xd = x.to(DEV)
+    codes, scale = O.weight_codes(w.float().numpy(), W, A)
+    w_dev = torch.from_numpy(O.pack_rows(codes, W)).to(DEV)
+    ws_dev = torch.from_numpy(scale).to(DEV)
+    out = _native.grouped_forward(xd, w_dev, ws_dev, None, W, A)
+    p, s = _native.quantize_groups(xd, A)
+    want_p, want_s, a_codes = oracle_activation(x, A)
+    np.testing.assert_array_equal(p.cpu().numpy(), want_p)
+    np.testing.assert_array_equal(s.cpu().numpy(), want_s)
+    cols = np.random.default_rng(0).choice(n, size=min(64, n), replace=False)
+    rows = np.arange(m) if m <= 64 else np.random.default_rng(1).choice(m, size=64, replace=False)
+    want = O.linear(a_codes, want_s, codes, scale, None, bounds=canonical_bounds(k // 64), rows=rows, cols=cols)
+    got = bits(out)[rows][:, cols]
+    np.testing.assert_array_equal(got, O.round_out(want, "bf16"))

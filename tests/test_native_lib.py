@@ -1,0 +1,84 @@
+"""CPU checks of the C ABI library: it loads without a GPU, exports every
+symbol include/actune_hip.h declares, passes its host layout self-test and
+rejects bad arguments before launching anything."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from actune_amd import _native
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "actune_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    names = re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(actune_[a-z_0-9]+)\s*\(", text, re.M)
+    assert names, "no declarations found"
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_native.LIB_PATH))
+    names = declared_functions()
+    assert {"actune_quantize_groups", "actune_grouped_linear", "actune_grouped_forward",
+            "actune_grouped_dots_i32", "actune_version", "actune_last_error"} <= set(names)
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_version_and_layout_selftest():
+    assert "gfx950" in _native.version()
+    assert _native.lib().actune_layout_selftest() == 0
+
+
+def test_config_table():
+    n = _native.num_configs()
+    assert n == 7
+    assert _native.config_valid(0, 16) and not _native.config_valid(0, 17)
+    assert all(_native.config_valid(c, 4096) for c in range(3, n))
+    assert not _native.config_valid(n, 1) and not _native.config_valid(-2, 1)
+    for m in (1, 8, 16, 17, 50, 512):
+        c = _native.default_config(m, 4096, 4096, 4, 8)
+        assert _native.config_valid(c, m)
+
+
+def _err():
+    return _native.lib().actune_last_error().decode()
+
+
+@pytest.mark.parametrize("args,msg", [
+    (dict(A=3), "Unsupported integer width"),
+    (dict(K=100), "K divisible by 64"),
+    (dict(dt=7), "dtype"),
+])
+def test_quantize_rejects_bad_arguments(args, msg):
+    p = dict(x=None, dt=0, sc=None, M=4, K=128, A=8)
+    p.update(args)
+    rc = _native.lib().actune_quantize_groups(p["x"], p["dt"], p["sc"], p["M"], p["K"], p["A"], None, None, None)
+    assert rc == 1 and msg in _err()
+
+
+@pytest.mark.parametrize("args,msg", [
+    (dict(W=5), "Unsupported integer width"),
+    (dict(K=96), "invalid dimensions"),
+    (dict(N=0), "invalid dimensions"),
+    (dict(config=0, M=17), "M <= 16"),
+    (dict(config=99), "invalid configuration"),
+    (dict(out_dt=9), "dtype"),
+    (dict(M=4), "null pointer"),
+])
+def test_linear_rejects_bad_arguments(args, msg):
+    p = dict(M=4, N=32, K=128, W=4, A=8, config=3, out_dt=0)
+    p.update(args)
+    rc = _native.lib().actune_grouped_linear(None, None, None, None, None, 2, None, p["out_dt"],
+                                             p["M"], p["N"], p["K"], p["W"], p["A"], p["config"], None)
+    assert rc == 1 and msg in _err()
+
+
+def test_zero_rows_is_a_no_op_without_a_gpu():
+    lib = _native.lib()
+    assert lib.actune_grouped_linear(None, None, None, None, None, 2, None, 0, 0, 32, 128, 4, 8, -1, None) == 0
+    assert lib.actune_quantize_groups(None, 0, None, 0, 128, 8, None, None, None) == 0
