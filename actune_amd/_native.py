@@ -158,16 +158,20 @@ def grouped_linear(a, as_, w, ws, bias, source_or_shape, W, A, config=CONFIG_AUT
     return out
 
 
-def grouped_forward(flat, w, ws, bias, W, A, input_scale=None, config=CONFIG_AUTO, out=None):
+def grouped_forward(flat, w, ws, bias, W, A, input_scale=None, config=CONFIG_AUTO, out=None,
+                    packed=None, scales=None):
     """Quantize + GEMM for a contiguous [M, K] input (GroupedLinear.forward's
-    device work, grouped.py:127-143); returns [M, N] in flat.dtype."""
+    device work, grouped.py:127-143); returns [M, N] in flat.dtype.
+    packed [M, K*A/8] / scales [M, K/64] / out may be preallocated."""
     _require_cuda(flat, w, ws, bias, input_scale)
     m, k = flat.shape
     n = w.size(0)
     if w.size(1) != k * W // 8:
         raise RuntimeError("packed shape mismatch")
-    packed = torch.empty((m, k * A // 8), device=flat.device, dtype=torch.uint8)
-    scales = torch.empty((m, k // 64), device=flat.device, dtype=torch.float32)
+    if packed is None:
+        packed = torch.empty((m, k * A // 8), device=flat.device, dtype=torch.uint8)
+    if scales is None:
+        scales = torch.empty((m, k // 64), device=flat.device, dtype=torch.float32)
     if out is None:
         out = torch.empty((m, n), device=flat.device, dtype=flat.dtype)
     bias_dt = 2 if bias is None else _dtype_code(bias)

@@ -81,7 +81,7 @@ int actune_config_valid(int config, int64_t M) {
 
 int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
   (void)K; (void)W; (void)A;
-  if (M <= 16) return N >= 4096 ? 1 : 2;
+  if (M <= 16) return 2;
   return M <= 64 ? 3 : 6;
 }
 

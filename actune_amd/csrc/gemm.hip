@@ -94,6 +94,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(
     const float* __restrict__ ws, const void* __restrict__ bias, int bias_dt, void* __restrict__ out,
     int out_dt, int32_t* __restrict__ dots, int M, int N, int K) {
   constexpr int GS = 8 / W;       // groups covered by one 16-byte weight load per lane
+  constexpr int DG = 8;           // groups per load batch
+  constexpr int DS = DG / GS;     // 16-byte weight loads per lane per batch
   constexpr int CPW = kChunks / NW;
   constexpr int T = shift_of(W) + shift_of(A);
   const float fold = __builtin_ldexpf(1.0f, -T);
@@ -115,30 +117,48 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(
     const int c = wave * CPW + cc;
     const int gb = chunk_begin(c, G), ge = chunk_begin(c + 1, G);
     float p[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int g = gb; g < ge; g += GS) {
-      const long off = (long)g * 8 * W + kb * 16;
-      uint32_t wv[4];
-      load_slot<8>(wrow + off, row_ok && off < wrow_bytes, wv);
-      exchange<W>(wv);
+    // Batches of DG groups: every weight, activation and scale load of the
+    // batch is issued before any of them is consumed, so a wave keeps
+    // DS x 16 B of weights per lane in flight instead of one load at a time.
+    for (int g0 = gb; g0 < ge; g0 += DG) {
+      uint32_t wv[DS][4];
+      uint32_t ap[DG][4];
+      float sc[DG];
 #pragma unroll
-      for (int j = 0; j < GS; ++j) {
-        const int gg = g + j;
-        if (gg >= ge) break;
-        uint32_t wd[4];
-        unpack_slot<W>(&wv[j * W / 2], wd);
-        uint32_t ad[4];
-        act_slot<W, A>(arow, m_ok, gg * kGroup + slot_k, ad);
-        const v4i D = mfma16x16x64(wd, ad, v4i{0, 0, 0, 0});
-        if constexpr (DOTS) {
+      for (int t = 0; t < DS; ++t) {
+        const int g = g0 + t * GS;
+        const long off = (long)g * 8 * W + kb * 16;
+        load_slot<8>(wrow + off, row_ok && g < ge && off < wrow_bytes, wv[t]);
+      }
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int n = n0 + 4 * kb + r;
-            if (n < N && m_ok) dots[((long)i * N + n) * G + gg] = D[r] >> T;
+      for (int j = 0; j < DG; ++j) {
+        const int gg = g0 + j;
+        const bool ok = m_ok && gg < ge;
+        load_slot<A>(arow + ((gg * kGroup + slot_k) * A) / 8, ok, ap[j]);
+        if constexpr (!DOTS) sc[j] = ok ? srow[gg] * fold : 0.0f;
+      }
+#pragma unroll
+      for (int t = 0; t < DS; ++t) {
+        exchange<W>(wv[t]);
+#pragma unroll
+        for (int j = 0; j < GS; ++j) {
+          const int gg = g0 + t * GS + j;
+          if (gg >= ge) break;
+          uint32_t wd[4], ad[4];
+          unpack_slot<W>(&wv[t][j * W / 2], wd);
+          unpack_slot<A>(ap[t * GS + j], ad);
+          reorder_slot<A, W>(ad);
+          const v4i D = mfma16x16x64(wd, ad, v4i{0, 0, 0, 0});
+          if constexpr (DOTS) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int n = n0 + 4 * kb + r;
+              if (n < N && m_ok) dots[((long)i * N + n) * G + gg] = D[r] >> T;
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) p[r] = __builtin_fmaf((float)D[r], sc[t * GS + j], p[r]);
           }
-        } else {
-          const float s = m_ok ? srow[gg] * fold : 0.0f;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) p[r] = __builtin_fmaf((float)D[r], s, p[r]);
         }
       }
     }
