@@ -24,6 +24,12 @@ CONFIG_AUTO = -1
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I = ctypes.c_int
+MAX_TARGETS = 4
+
+
+class _Target(ctypes.Structure):
+    """actune_linear_target"""
+    _fields_ = [("w", _P), ("w_scale", _P), ("bias", _P), ("out", _P), ("N", _I64)]
 
 
 def lib():
@@ -41,6 +47,8 @@ def lib():
         so.actune_grouped_linear.argtypes = [_P, _P, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I, _I, _I, _P]
         so.actune_grouped_forward.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _I64, _I64,
                                               _I, _I, _I, _P]
+        so.actune_grouped_forward_multi.argtypes = [_P, _I, _P, _P, _P, ctypes.POINTER(_Target), _I, _I,
+                                                    _I64, _I64, _I, _I, _I, _P]
         so.actune_grouped_dots_i32.argtypes = [_P, _P, _I64, _I64, _I64, _I, _I, _I, _P, _P]
         so.actune_config_valid.argtypes = [_I, _I64]
         so.actune_default_config.argtypes = [_I64, _I64, _I64, _I, _I]
@@ -179,6 +187,39 @@ def grouped_forward(flat, w, ws, bias, W, A, input_scale=None, config=CONFIG_AUT
         _ptr(flat), _dtype_code(flat), _ptr(input_scale), _ptr(packed), _ptr(scales), _ptr(w), _ptr(ws),
         _ptr(bias), bias_dt, _ptr(out), m, n, k, W, A, config, _stream(flat.device)))
     return out
+
+
+def grouped_forward_multi(flat, targets, W, A, input_scale=None, config=CONFIG_AUTO, packed=None,
+                          scales=None):
+    """Quantize + GEMM of one [M, K] input against up to 4 linears in one
+    launch. targets: sequence of (w, ws, bias, out) with out [M, N_t] (None
+    to allocate). Returns the list of outputs."""
+    if not 1 <= len(targets) <= MAX_TARGETS:
+        raise ValueError("between 1 and 4 targets required")
+    m, k = flat.shape
+    _require_cuda(flat, input_scale, *[t for tgt in targets for t in tgt[:3]])
+    biases = [t[2] for t in targets]
+    if any(b is not None for b in biases) and len({(b.dtype if b is not None else None) for b in biases}) != 1:
+        raise ValueError("all targets must share one bias dtype (or none)")
+    bias_dt = 2 if biases[0] is None else _dtype_code(biases[0])
+    arr = (_Target * len(targets))()
+    outs = []
+    for j, (w, ws, bias, out) in enumerate(targets):
+        if w.size(1) != k * W // 8:
+            raise RuntimeError("packed shape mismatch")
+        if out is None:
+            out = torch.empty((m, w.size(0)), device=flat.device, dtype=flat.dtype)
+        outs.append(out)
+        arr[j] = _Target(w.data_ptr(), ws.data_ptr(), None if bias is None else bias.data_ptr(), out.data_ptr(),
+                         w.size(0))
+    if packed is None:
+        packed = torch.empty((m, k * A // 8), device=flat.device, dtype=torch.uint8)
+    if scales is None:
+        scales = torch.empty((m, k // 64), device=flat.device, dtype=torch.float32)
+    _check(lib().actune_grouped_forward_multi(_ptr(flat), _dtype_code(flat), _ptr(input_scale), _ptr(packed),
+                                              _ptr(scales), arr, len(targets), bias_dt, m, k, W, A, config,
+                                              _stream(flat.device)))
+    return outs
 
 
 def grouped_dots(a, w, m, k, W, A, config=CONFIG_AUTO):

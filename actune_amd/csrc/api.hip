@@ -13,9 +13,18 @@ using namespace actune;
 
 namespace {
 
-constexpr int kNumConfigs = 7;
-constexpr int kSmallMConfigs = 3;  // ids 0..2 need M <= 16
+constexpr int kNumConfigs = 10;
+constexpr int kSmallMConfigs = 3;  // ids 0..2: small-M kernel, M <= kSmallMMax
+constexpr int kSmallMMax = 64;
+constexpr int kTiledConfigs = 4;   // ids 3..6: MFMA-tiled kernel, any M
+constexpr int kStreamFirst = kSmallMConfigs + kTiledConfigs;  // ids 7..9: streaming kernel, M <= 16
+constexpr int kStreamMax = 16;
+constexpr int kFusedMaxM = 4;      // small-M calls up to this M quantize inside the GEMM
+constexpr int kSmallMWaves[kSmallMConfigs] = {4, 8, 16};
 thread_local char g_err[512];
+// Kernels address every operand through 32-bit buffer offsets and use
+// 2^31 as the "no load" offset, so each operand buffer must stay below 2 GiB.
+constexpr int64_t kMaxBufferBytes = (int64_t)1 << 31;
 
 int fail(int code, const char* fmt, const char* detail = "") {
   snprintf(g_err, sizeof g_err, fmt, detail);
@@ -37,7 +46,7 @@ int check_quantize(const void* x, int dt, const void* sc, int64_t M, int64_t K, 
   if (!width_ok(A)) return fail(ACTUNE_ERR_INVALID, "Unsupported integer width");
   if (!dtype_ok(dt)) return fail(ACTUNE_ERR_INVALID, "unsupported activation dtype");
   if (M < 0 || K <= 0 || K % 64) return fail(ACTUNE_ERR_INVALID, "Grouped backend requires K divisible by 64");
-  if (M * (K / 64) / 32 >= INT_MAX) return fail(ACTUNE_ERR_INVALID, "activation too large");
+  if (M * (K / 64) / 32 >= INT_MAX || K > INT_MAX / 8) return fail(ACTUNE_ERR_INVALID, "activation too large");
   if (M == 0) return ACTUNE_OK;
   if (!x || !packed || !scales) return fail(ACTUNE_ERR_INVALID, "null pointer");
   if (!aligned(x, 16) || (sc && !aligned(sc, 16)) || !aligned(packed, 8) || !aligned(scales, 4))
@@ -45,18 +54,25 @@ int check_quantize(const void* x, int dt, const void* sc, int64_t M, int64_t K, 
   return ACTUNE_OK;
 }
 
-int check_linear(const uint8_t* a, const float* as, const uint8_t* w, const float* ws, int bias_dt,
-                 const void* out, int out_dt, int64_t M, int64_t N, int64_t K, int W, int A, int config) {
+int check_shape(int64_t M, int64_t K, int W, int A, int out_dt, int bias_dt, int config) {
   if (!width_ok(W) || !width_ok(A)) return fail(ACTUNE_ERR_INVALID, "Unsupported integer width");
-  if (M < 0 || N <= 0 || K <= 0 || K % 64) return fail(ACTUNE_ERR_INVALID, "invalid dimensions");
-  if (M > INT_MAX || N > INT_MAX - 64 || K > INT_MAX / 8) return fail(ACTUNE_ERR_INVALID, "dimensions too large");
+  if (M < 0 || K <= 0 || K % 64) return fail(ACTUNE_ERR_INVALID, "invalid dimensions");
+  if (M > INT_MAX || K > INT_MAX / 8) return fail(ACTUNE_ERR_INVALID, "dimensions too large");
+  if (M * K * 4 >= kMaxBufferBytes) return fail(ACTUNE_ERR_INVALID, "operand too large (each buffer must stay below 2 GiB)");
   if (!dtype_ok(out_dt) || !dtype_ok(bias_dt)) return fail(ACTUNE_ERR_INVALID, "unsupported output/bias dtype");
   if (config < 0 || config >= kNumConfigs) return fail(ACTUNE_ERR_INVALID, "invalid configuration");
-  if (config < kSmallMConfigs && M > 16) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 16");
+  if (config < kSmallMConfigs && M > kSmallMMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
+  if (config >= kStreamFirst && M > kStreamMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 16");
+  return ACTUNE_OK;
+}
+
+int check_target(const uint8_t* w, const float* ws, const void* out, int64_t N, int64_t M, int64_t K, int W) {
+  if (N <= 0 || N > INT_MAX / 2) return fail(ACTUNE_ERR_INVALID, "invalid dimensions");
+  if (N * K * W / 8 >= kMaxBufferBytes || M * N * 4 >= kMaxBufferBytes)
+    return fail(ACTUNE_ERR_INVALID, "operand too large (each buffer must stay below 2 GiB)");
   if (M == 0) return ACTUNE_OK;
-  if (!a || !as || !w || !ws || !out) return fail(ACTUNE_ERR_INVALID, "null pointer");
-  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(as, 4) || !aligned(ws, 4))
-    return fail(ACTUNE_ERR_INVALID, "misaligned operand (packed data needs 16 B)");
+  if (!w || !ws || !out) return fail(ACTUNE_ERR_INVALID, "null pointer");
+  if (!aligned(w, 16) || !aligned(ws, 4)) return fail(ACTUNE_ERR_INVALID, "misaligned operand (packed data needs 16 B)");
   return ACTUNE_OK;
 }
 
@@ -64,11 +80,53 @@ int resolve(int config, int64_t M, int64_t N, int64_t K, int W, int A) {
   return config == ACTUNE_CONFIG_AUTO ? actune_default_config(M, N, K, W, A) : config;
 }
 
+// Fill the problem table of a launch; returns the number of 16-row tiles.
+int add_problem(LinearArgs& g, const uint8_t* w, const float* ws, const void* bias, void* out, int64_t N) {
+  Problem& p = g.prob[g.nprob++];
+  p = Problem{w, ws, bias, out, (int)N, g.tiles};
+  g.tiles += (int)((N + 15) / 16);
+  return g.tiles;
+}
+
+// Launch the GEMM of `g` (all problems) with kernel config `config`. A
+// streaming config whose LDS staging would not fit (or the dots mode) runs
+// the small-M kernel with the same wave count; results are identical.
+void run_gemm(int W, int A, int config, int mode, const LinearArgs& g, hipStream_t st) {
+  if (config >= kStreamFirst) {
+    const int nw = kSmallMWaves[config - kStreamFirst];
+    if (mode != kModeDots && stream_lds_bytes(g.K, g.M, nw) <= kStreamLdsMax) {
+      launch_stream(W, A, nw, mode, g, st);
+      return;
+    }
+    config -= kStreamFirst;
+  }
+  if (config < kSmallMConfigs) {
+    launch_smallm(W, A, kSmallMWaves[config], mode, g, st);
+    return;
+  }
+  for (int p = 0; p < g.nprob; ++p) {
+    LinearArgs one = g;
+    one.prob[0] = g.prob[p];
+    one.prob[0].tile0 = 0;
+    one.nprob = 1;
+    launch_tiled(W, A, config - kSmallMConfigs, mode == kModeDots, one, st);
+  }
+}
+
+LinearArgs base_args(int64_t M, int64_t K, int bias_dt, int out_dt) {
+  LinearArgs g{};
+  g.M = (int)M;
+  g.K = (int)K;
+  g.bias_dt = bias_dt;
+  g.out_dt = out_dt;
+  return g;
+}
+
 }  // namespace
 
 extern "C" {
 
-const char* actune_version(void) { return "actune_hip 0.1.0 gfx950"; }
+const char* actune_version(void) { return "actune_hip 0.2.0 gfx950"; }
 
 const char* actune_last_error(void) { return g_err; }
 
@@ -76,13 +134,23 @@ int actune_num_configs(void) { return kNumConfigs; }
 
 int actune_config_valid(int config, int64_t M) {
   if (config < 0 || config >= kNumConfigs) return 0;
-  return config >= kSmallMConfigs || M <= 16;
+  if (config < kSmallMConfigs) return M <= kSmallMMax;
+  if (config >= kStreamFirst) return M <= kStreamMax;
+  return 1;
 }
 
 int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
-  (void)K; (void)W; (void)A;
-  if (M <= 16) return 2;
-  return M <= 64 ? 3 : 6;
+  (void)W; (void)A;
+  // Measured on MI355X (W4A8, Llama/Gemma shapes): the one-tile-per-CU
+  // small-M kernel with 16 waves is fastest for decode shapes of up to ~768
+  // row tiles; beyond that, and for M > 4, the persistent streaming kernel
+  // with 8 waves wins (it keeps the next tile's weights in flight and
+  // quantizes once per workgroup).
+  const int64_t tiles = (N + 15) / 16;
+  if (M <= kFusedMaxM) return tiles >= 768 ? kStreamFirst + 1 : 2;
+  if (M <= kStreamMax) return tiles >= 512 ? kStreamFirst + 1 : kStreamFirst + 2;
+  if (M <= kSmallMMax) return 1;
+  return M <= 128 ? 3 : 4;
 }
 
 int actune_quantize_groups(const void* x, int x_dtype, const void* input_scale, int64_t M, int64_t K,
@@ -100,10 +168,54 @@ int actune_grouped_linear(const uint8_t* a, const float* a_scales, const uint8_t
                           void* stream) {
   g_err[0] = 0;
   config = resolve(config, M, N, K, W, A);
-  int rc = check_linear(a, a_scales, w, w_scale, bias_dtype, out, out_dtype, M, N, K, W, A, config);
+  int rc = check_shape(M, K, W, A, out_dtype, bias_dtype, config);
+  if (!rc) rc = check_target(w, w_scale, out, N, M, K, W);
   if (rc || M == 0) return rc;
-  GemmArgs g{a, a_scales, w, w_scale, bias, bias_dtype, out, out_dtype, nullptr, (int)M, (int)N, (int)K};
-  launch_gemm(W, A, config, g, (hipStream_t)stream);
+  if (!a || !a_scales) return fail(ACTUNE_ERR_INVALID, "null pointer");
+  if (!aligned(a, 16) || !aligned(a_scales, 4)) return fail(ACTUNE_ERR_INVALID, "misaligned operand (packed data needs 16 B)");
+  LinearArgs g = base_args(M, K, bias_dtype, out_dtype);
+  g.a = a;
+  g.as = a_scales;
+  add_problem(g, w, w_scale, bias, out, N);
+  run_gemm(W, A, config, kModePacked, g, (hipStream_t)stream);
+  return check_launch();
+}
+
+int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_scale, uint8_t* a_buf,
+                                 float* scale_buf, const actune_linear_target* targets, int ntargets,
+                                 int bias_dtype, int64_t M, int64_t K, int W, int A, int config,
+                                 void* stream) {
+  g_err[0] = 0;
+  if (ntargets < 1 || ntargets > ACTUNE_MAX_TARGETS || !targets)
+    return fail(ACTUNE_ERR_INVALID, "between 1 and 4 targets required");
+  int64_t n_total = 0;
+  for (int t = 0; t < ntargets; ++t) n_total += targets[t].N;
+  config = resolve(config, M, n_total, K, W, A);
+  int rc = check_shape(M, K, W, A, x_dtype, bias_dtype, config);
+  if (!rc) rc = check_quantize(x, x_dtype, input_scale, M, K, A, a_buf, scale_buf);
+  for (int t = 0; t < ntargets && !rc; ++t)
+    rc = check_target(targets[t].w, targets[t].w_scale, targets[t].out, targets[t].N, M, K, W);
+  if (!rc && n_total / 16 >= INT_MAX / 2) rc = fail(ACTUNE_ERR_INVALID, "dimensions too large");
+  if (rc || M == 0) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  LinearArgs g = base_args(M, K, bias_dtype, x_dtype);
+  for (int t = 0; t < ntargets; ++t)
+    add_problem(g, targets[t].w, targets[t].w_scale, targets[t].bias, targets[t].out, targets[t].N);
+  // The quantizer is fused into the GEMM for M <= 4 on the small-M and
+  // streaming kernels (for larger M its per-workgroup cost is no longer
+  // hidden under the weight loads; measured on MI355X).
+  const bool fused = M <= kFusedMaxM && (config < kSmallMConfigs || config >= kStreamFirst);
+  if (fused) {
+    g.x = x;
+    g.xscale = input_scale;
+    g.x_dt = x_dtype;
+    run_gemm(W, A, config, kModeFused, g, st);
+  } else {
+    launch_quantize(x, x_dtype, input_scale, M, K, A, a_buf, scale_buf, st);
+    g.a = a_buf;
+    g.as = scale_buf;
+    run_gemm(W, A, config, kModePacked, g, st);
+  }
   return check_launch();
 }
 
@@ -111,27 +223,26 @@ int actune_grouped_forward(const void* x, int x_dtype, const void* input_scale, 
                            float* scale_buf, const uint8_t* w, const float* w_scale, const void* bias,
                            int bias_dtype, void* out, int64_t M, int64_t N, int64_t K, int W, int A,
                            int config, void* stream) {
-  g_err[0] = 0;
-  config = resolve(config, M, N, K, W, A);
-  int rc = check_quantize(x, x_dtype, input_scale, M, K, A, a_buf, scale_buf);
-  if (!rc) rc = check_linear(a_buf, scale_buf, w, w_scale, bias_dtype, out, x_dtype, M, N, K, W, A, config);
-  if (rc || M == 0) return rc;
-  launch_quantize(x, x_dtype, input_scale, M, K, A, a_buf, scale_buf, (hipStream_t)stream);
-  GemmArgs g{a_buf, scale_buf, w, w_scale, bias, bias_dtype, out, x_dtype, nullptr, (int)M, (int)N, (int)K};
-  launch_gemm(W, A, config, g, (hipStream_t)stream);
-  return check_launch();
+  const actune_linear_target t{w, w_scale, bias, out, N};
+  return actune_grouped_forward_multi(x, x_dtype, input_scale, a_buf, scale_buf, &t, 1, bias_dtype, M, K,
+                                      W, A, config, stream);
 }
 
 int actune_grouped_dots_i32(const uint8_t* a, const uint8_t* w, int64_t M, int64_t N, int64_t K,
                             int W, int A, int config, int32_t* dots, void* stream) {
   g_err[0] = 0;
   config = resolve(config, M, N, K, W, A);
-  // scales/out are unused in the dots mode; pass a and w to satisfy the null checks
-  int rc = check_linear(a, (const float*)w, w, (const float*)w, kF32, dots, kF32, M, N, K, W, A, config);
+  int rc = check_shape(M, K, W, A, kF32, kF32, config);
+  if (!rc && (N <= 0 || N > INT_MAX / 2)) rc = fail(ACTUNE_ERR_INVALID, "invalid dimensions");
+  if (!rc && N * K * W / 8 >= kMaxBufferBytes) rc = fail(ACTUNE_ERR_INVALID, "operand too large (each buffer must stay below 2 GiB)");
   if (rc || M == 0) return rc;
-  if (!aligned(dots, 4)) return fail(ACTUNE_ERR_INVALID, "misaligned dots buffer");
-  GemmArgs g{a, nullptr, w, nullptr, nullptr, kF32, nullptr, kF32, dots, (int)M, (int)N, (int)K};
-  launch_dots(W, A, config, g, (hipStream_t)stream);
+  if (!a || !w || !dots) return fail(ACTUNE_ERR_INVALID, "null pointer");
+  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(dots, 4)) return fail(ACTUNE_ERR_INVALID, "misaligned operand");
+  LinearArgs g = base_args(M, K, kF32, kF32);
+  g.a = a;
+  g.dots = dots;
+  add_problem(g, w, nullptr, nullptr, nullptr, N);
+  run_gemm(W, A, config, kModeDots, g, (hipStream_t)stream);
   return check_launch();
 }
 

@@ -1,0 +1,265 @@
+// Small-M packed group-64 GEMM for gfx950 (decode and action-chunk shapes,
+// M <= 64): HBM-bound on the packed weights.
+//
+// Restates the per-call math of actune/kernels/grouped.py:74-94 and
+// actune/kernels/grouped_native.cu:42-88 (exact int32 dot per 64-group,
+// fp32 rescale by the activation scale, weight-scale epilogue), reduced in
+// the canonical chunked order of common.hpp.
+//
+// Structure:
+//  * One workgroup owns 16 output channels of one problem (a problem is one
+//    linear; up to kMaxProblems linears that share the same input run in one
+//    launch) over all of K, and NW waves split K along the 16 canonical
+//    chunks (split-K inside the workgroup, no global scratch).
+//  * Each lane streams 16-byte weight loads (global_load_dwordx4): lanes
+//    kb = 0..3 of a row fetch 64 consecutive bytes = 8/W groups, and
+//    v_permlane32/16_swap turn them into MFMA slots without LDS.
+//  * Loads are batched: every weight, activation and scale load of DG groups
+//    is issued before the batch is consumed.
+//  * v_mfma_i32_16x16x64_i8 with the weight rows as the A operand and up to
+//    16 tokens per column tile (MT tiles) as the B operand; one fp32 FMA per
+//    (row, token, group).
+//  * MODE_FUSED (M <= 4): each wave quantizes the activation groups of its
+//    own K-range straight from x (the group-64 quantizer of
+//    grouped.py:55-71, optionally dividing by the channel scale of
+//    layers.py:41-42) into a per-wave LDS slab laid out as MFMA B slots, while
+//    its weight loads are in flight; no separate quantizer launch.
+//  * Chunk partials meet in LDS and are added in chunk order.
+#include "common.hpp"
+#include "launch.hpp"
+#include "operands.hpp"
+
+namespace actune {
+
+// The problem owning row tile `tile`, selected field by field with constant
+// indices so the by-value kernel arguments stay in scalar kernarg loads.
+__device__ __forceinline__ Problem select_problem(const LinearArgs& args, int tile) {
+  Problem pr;
+  pr.w = args.prob[0].w; pr.ws = args.prob[0].ws; pr.bias = args.prob[0].bias;
+  pr.out = args.prob[0].out; pr.N = args.prob[0].N; pr.tile0 = args.prob[0].tile0;
+#pragma unroll
+  for (int q = 1; q < kMaxProblems; ++q) {
+    if (q < args.nprob && tile >= args.prob[q].tile0) {
+      pr.w = args.prob[q].w; pr.ws = args.prob[q].ws; pr.bias = args.prob[q].bias;
+      pr.out = args.prob[q].out; pr.N = args.prob[q].N; pr.tile0 = args.prob[q].tile0;
+    }
+  }
+  return pr;
+}
+
+template <int W, int A, int NW, int MT, int MODE, int DT, bool SCALE>
+__global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
+  constexpr int GS = 8 / W;                        // groups per 16-byte weight load per lane
+  constexpr int DG = (8 / MT) > GS ? (8 / MT) : GS;  // groups per load batch
+  constexpr int DS = DG / GS;                      // weight loads per lane per batch
+  constexpr int CPW = kChunks / NW;                // canonical chunks per wave
+  constexpr int T = shift_of(W) + shift_of(A);
+  constexpr bool FUSED = MODE == kModeFused;
+  constexpr bool DOTS = MODE == kModeDots;
+  constexpr int COLS = 16 * MT;
+  static_assert(!FUSED || (MT == 1 && DG == 8), "fused quantization serves M <= 4");
+
+  __shared__ float red[DOTS ? 1 : kChunks][16][COLS + 1];
+  __shared__ __align__(16) uint8_t slab[FUSED ? NW : 1][FUSED ? DG * 4 * kGroup : 16];
+  __shared__ float sslab[FUSED ? NW : 1][FUSED ? DG * 4 : 1];
+
+  const float fold = __builtin_ldexpf(1.0f, -T);
+  const Problem pr = select_problem(args, blockIdx.x);
+  const int M = args.M, K = args.K, N = pr.N;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = lane & 15, kb = lane >> 4;
+  const int G = K / kGroup;
+  const int n0 = ((int)blockIdx.x - pr.tile0) * 16;
+  const uint32_t wrow_bytes = (uint32_t)K * W / 8;
+  const bool row_ok = n0 + i < N;
+  const Rsrc wres = make_rsrc(pr.w, (uint32_t)N * wrow_bytes);
+  const uint32_t wrow = (uint32_t)(n0 + i) * wrow_bytes;
+  const int slot_k = smallm_slot_k<W>(kb);
+
+  // activation row offsets (bytes) of this lane's tokens, kOff when m >= M
+  const uint32_t arow_bytes = (uint32_t)K * A / 8;
+  Rsrc ares, sres, xres, xsres;
+  if constexpr (FUSED) {
+    xres = make_rsrc(args.x, (uint32_t)M * K * (DT == kF32 ? 4 : 2));
+    xsres = make_rsrc(SCALE ? args.xscale : args.x, (uint32_t)K * (DT == kF32 ? 4 : 2));
+  } else {
+    ares = make_rsrc(args.a, (uint32_t)M * arow_bytes);
+    sres = make_rsrc(args.as, (uint32_t)M * G * 4);
+  }
+  uint32_t arow[MT];
+  bool aok[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = 16 * t + i;
+    aok[t] = m < M;
+    arow[t] = (uint32_t)m;
+  }
+
+  for (int cc = 0; cc < CPW; ++cc) {
+    const int c = wave * CPW + cc;
+    const int gb = chunk_begin(c, G), ge = chunk_begin(c + 1, G);
+    float p[MT][4];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[t][r] = 0.f;
+
+    for (int g0 = gb; g0 < ge; g0 += DG) {
+      uint32_t wv[DS][4];
+#pragma unroll
+      for (int s = 0; s < DS; ++s) {
+        const int g = g0 + s * GS;
+        const uint32_t off = (uint32_t)g * 8 * W + kb * 16;
+        buffer_slot<8>(wres, row_ok && g < ge && off < wrow_bytes ? wrow + off : kOff, wv[s]);
+      }
+      uint32_t ap[FUSED ? 1 : DG][MT][4];
+      float sc[FUSED ? 1 : DG][MT];
+      if constexpr (FUSED) {
+        // Quantize groups [g0, g0+8) of the M <= 4 rows: group-row idx = m*8 + j,
+        // 8 lanes per group-row, each lane 8 consecutive elements.
+        uint8_t* my_slab = slab[wave];
+        for (int base = 0; base < M * DG; base += 8) {
+          const int idx = base + (lane >> 3), seg = lane & 7;
+          const int m = idx >> 3, j = idx & 7, g = g0 + j;
+          const bool live = m < M && g < ge;
+          constexpr uint32_t esz = DT == kF32 ? 4 : 2;
+          const uint32_t k0 = (uint32_t)(g * kGroup + seg * 8);
+          float v[8];
+          buffer_load8<DT>(xres, live ? ((uint32_t)m * K + k0) * esz : kOff, v);
+          if constexpr (SCALE) {
+            float d[8];
+            buffer_load8<DT>(xsres, live ? k0 * esz : kOff, d);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = live ? round_to_dtype<DT>(v[e] / d[e]) : 0.0f;
+          }
+          int cq[8];
+          const float s = group_codes<A, DT>(v, cq);
+          if (live) {
+            store_half_slot<W, A>(my_slab + (j * 4 + m) * kGroup + (seg >> 1) * 16, seg & 1, cq);
+            if (seg == 0) sslab[wave][j * 4 + m] = s * fold;
+          }
+        }
+        // LDS operations of one wave complete in order; keep the compiler from
+        // moving the slab reads above the writes.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      } else {
+#pragma unroll
+        for (int j = 0; j < DG; ++j) {
+          const int gg = g0 + j;
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            const bool ok = aok[t] && gg < ge;
+            const uint32_t aoff = arow[t] * arow_bytes + (uint32_t)((gg * kGroup + slot_k) * A) / 8;
+            buffer_slot<A>(ares, ok ? aoff : kOff, ap[j][t]);
+            if constexpr (!DOTS) sc[j][t] = buffer_f32(sres, ok ? (arow[t] * G + gg) * 4u : kOff) * fold;
+          }
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < DS; ++s) {
+        exchange<W>(wv[s]);
+#pragma unroll
+        for (int jj = 0; jj < GS; ++jj) {
+          const int j = s * GS + jj, gg = g0 + j;
+          if (gg >= ge) break;
+          uint32_t wd[4];
+          unpack_slot<W>(&wv[s][jj * W / 2], wd);
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            uint32_t bd[4];
+            float scale;
+            if constexpr (FUSED) {
+              const bool ok = i < M;
+              v4u q = v4u{0u, 0u, 0u, 0u};
+              if (ok) q = *reinterpret_cast<const v4u*>(slab[wave] + (j * 4 + i) * kGroup + slot_k);
+              bd[0] = q[0]; bd[1] = q[1]; bd[2] = q[2]; bd[3] = q[3];
+              scale = ok ? sslab[wave][j * 4 + i] : 0.0f;
+            } else {
+              unpack_slot<A>(ap[j][t], bd);
+              reorder_slot<A, W>(bd);
+              scale = DOTS ? 0.0f : sc[j][t];
+            }
+            const v4i D = mfma16x16x64(wd, bd, v4i{0, 0, 0, 0});
+            if constexpr (DOTS) {
+              const int m = 16 * t + i;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int n = n0 + 4 * kb + r;
+                if (n < N && m < M) args.dots[((long)m * N + n) * G + gg] = D[r] >> T;
+              }
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) p[t][r] = __builtin_fmaf((float)D[r], scale, p[t][r]);
+            }
+          }
+        }
+      }
+    }
+    if constexpr (!DOTS) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[c][4 * kb + r][16 * t + i] = p[t][r];
+    }
+  }
+  if constexpr (DOTS) return;
+  __syncthreads();
+  for (int e = threadIdx.x; e < 16 * COLS; e += NW * 64) {
+    const int nl = e / COLS, m = e % COLS, n = n0 + nl;
+    float acc = red[0][nl][m];
+#pragma unroll
+    for (int c = 1; c < kChunks; ++c) acc = acc + red[c][nl][m];
+    if (n < N && m < M) {
+      const float y = finish(acc, pr.ws[n], pr.bias, args.bias_dt, n);
+      const long o = (long)m * N + n;
+      if (args.out_dt == kBF16) store_out<kBF16>(pr.out, o, y);
+      else if (args.out_dt == kF16) store_out<kF16>(pr.out, o, y);
+      else store_out<kF32>(pr.out, o, y);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <int W, int A, int NW, int MT>
+static void launch_nw_mt(int mode, const LinearArgs& g, hipStream_t st) {
+  const dim3 grid((unsigned)g.tiles), block(NW * 64);
+  if (mode == kModeDots) {
+    gemm_smallm<W, A, NW, MT, kModeDots, kBF16, false><<<grid, block, 0, st>>>(g);
+  } else if (mode == kModePacked) {
+    gemm_smallm<W, A, NW, MT, kModePacked, kBF16, false><<<grid, block, 0, st>>>(g);
+  } else if constexpr (MT == 1) {
+#define FUSED_DT(DTV)                                                                               \
+  if (g.xscale) gemm_smallm<W, A, NW, 1, kModeFused, DTV, true><<<grid, block, 0, st>>>(g);        \
+  else gemm_smallm<W, A, NW, 1, kModeFused, DTV, false><<<grid, block, 0, st>>>(g)
+    if (g.x_dt == kBF16) { FUSED_DT(kBF16); }
+    else if (g.x_dt == kF16) { FUSED_DT(kF16); }
+    else { FUSED_DT(kF32); }
+#undef FUSED_DT
+  }
+}
+
+template <int W, int A, int NW>
+static void launch_nw(int mode, const LinearArgs& g, hipStream_t st) {
+  if (g.M <= 16) launch_nw_mt<W, A, NW, 1>(mode, g, st);
+  else if (g.M <= 32) launch_nw_mt<W, A, NW, 2>(mode, g, st);
+  else launch_nw_mt<W, A, NW, 4>(mode, g, st);
+}
+
+template <int W, int A>
+static void launch_wa(int nw, int mode, const LinearArgs& g, hipStream_t st) {
+  if (nw == 4) launch_nw<W, A, 4>(mode, g, st);
+  else if (nw == 8) launch_nw<W, A, 8>(mode, g, st);
+  else launch_nw<W, A, 16>(mode, g, st);
+}
+
+void launch_smallm(int W, int A, int nw, int mode, const LinearArgs& g, hipStream_t st) {
+#define CASE(WB, AB) if (W == WB && A == AB) return launch_wa<WB, AB>(nw, mode, g, st)
+  CASE(8, 8); CASE(8, 4); CASE(8, 2);
+  CASE(4, 8); CASE(4, 4); CASE(4, 2);
+  CASE(2, 8); CASE(2, 4); CASE(2, 2);
+#undef CASE
+}
+
+}  // namespace actune

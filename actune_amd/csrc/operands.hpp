@@ -1,0 +1,219 @@
+// Operand fetch / exchange helpers and the exact group-64 code computation
+// shared by the quantizer and the GEMM kernels.
+#pragma once
+#include "common.hpp"
+
+namespace actune {
+
+// ---------------------------------------------------------------------------
+// Raw buffer loads. A buffer resource covers `bytes` bytes from `base`; a
+// lane whose 32-bit offset is at or beyond that range reads zeros, so
+// predicated operand loads need no branch and a wave can keep all of its
+// loads in flight (a predicated global load would be wrapped in an exec
+// branch with its own wait). kOff marks a lane's load as switched off; the
+// C ABI keeps every operand buffer below 2 GiB so kOff is always outside.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr uint32_t kOff = 0x80000000u;
+
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
+  // word 3 = 0x00020000: 32-bit data format, the gfx9-family raw buffer setting
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 2B bytes (one 16-element slot of width B) at byte offset off; zeros if off
+// is out of range.
+template <int B>
+__device__ __forceinline__ void buffer_slot(Rsrc r, uint32_t off, uint32_t out[4]) {
+  if constexpr (B == 8) {
+    const v4u q = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    out[0] = q[0]; out[1] = q[1]; out[2] = q[2]; out[3] = q[3];
+  } else if constexpr (B == 4) {
+    const v2u q = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    out[0] = q[0]; out[1] = q[1]; out[2] = 0u; out[3] = 0u;
+  } else {
+    out[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    out[1] = out[2] = out[3] = 0u;
+  }
+}
+
+__device__ __forceinline__ float buffer_f32(Rsrc r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+// Eight consecutive elements of dtype DT at byte offset off as fp32 (zeros
+// when off is out of range).
+template <int DT>
+__device__ __forceinline__ void buffer_load8(Rsrc r, uint32_t off, float v[8]) {
+  if constexpr (DT == kF32) {
+    const v4u a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const v4u b = __builtin_amdgcn_raw_buffer_load_b128(r, off == kOff ? kOff : off + 16, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[e] = __uint_as_float(a[e]); v[e + 4] = __uint_as_float(b[e]); }
+  } else {
+    const v4u q = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t lo = (uint16_t)(q[e] & 0xffffu), hi = (uint16_t)(q[e] >> 16);
+      if constexpr (DT == kBF16) { v[2 * e] = bf16_to_f32(lo); v[2 * e + 1] = bf16_to_f32(hi); }
+      else { v[2 * e] = f16_to_f32(lo); v[2 * e + 1] = f16_to_f32(hi); }
+    }
+  }
+}
+
+// Eight consecutive elements of dtype DT held in q0 (and q1 for fp32) as fp32.
+template <int DT>
+__device__ __forceinline__ void unpack8(const v4u& q0, const v4u& q1, float v[8]) {
+  if constexpr (DT == kF32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[e] = __uint_as_float(q0[e]); v[e + 4] = __uint_as_float(q1[e]); }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t lo = (uint16_t)(q0[e] & 0xffffu), hi = (uint16_t)(q0[e] >> 16);
+      if constexpr (DT == kBF16) { v[2 * e] = bf16_to_f32(lo); v[2 * e + 1] = bf16_to_f32(hi); }
+      else { v[2 * e] = f16_to_f32(lo); v[2 * e + 1] = f16_to_f32(hi); }
+    }
+  }
+}
+
+// Packed bytes of one 16-element slot of width B (2B bytes) at p; zeros
+// when !ok (nothing is read).
+template <int B>
+__device__ __forceinline__ void load_slot(const uint8_t* p, bool ok, uint32_t out[4]) {
+  out[0] = out[1] = out[2] = out[3] = 0u;
+  if (!ok) return;
+  if constexpr (B == 8) {
+    const v4u q = *reinterpret_cast<const v4u*>(p);
+    out[0] = q[0]; out[1] = q[1]; out[2] = q[2]; out[3] = q[3];
+  } else if constexpr (B == 4) {
+    const v2u q = *reinterpret_cast<const v2u*>(p);
+    out[0] = q[0]; out[1] = q[1];
+  } else {
+    out[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+}
+
+// Eight consecutive elements starting at element i (i % 8 == 0) as fp32,
+// with 16-byte vector loads.
+template <int DT>
+__device__ __forceinline__ void load8(const void* p, long i, float v[8]) {
+  if constexpr (DT == kF32) {
+    const v4u a = reinterpret_cast<const v4u*>(p)[i / 4];
+    const v4u b = reinterpret_cast<const v4u*>(p)[i / 4 + 1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[e] = __uint_as_float(a[e]); v[e + 4] = __uint_as_float(b[e]); }
+  } else {
+    const v4u q = reinterpret_cast<const v4u*>(p)[i / 8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t lo = (uint16_t)(q[e] & 0xffffu), hi = (uint16_t)(q[e] >> 16);
+      if constexpr (DT == kBF16) { v[2 * e] = bf16_to_f32(lo); v[2 * e + 1] = bf16_to_f32(hi); }
+      else { v[2 * e] = f16_to_f32(lo); v[2 * e + 1] = f16_to_f32(hi); }
+    }
+  }
+}
+
+// Group-64 codes of 8 elements held by one lane of an 8-lane segment group:
+// amax over the group (xor-shuffles inside the 8 lanes), s = fl(max(amax,
+// 1e-8) / P) and c = clamp(rint(fl(v / s)), -P-1, P). For 16-bit inputs the
+// quotient is x * y with y = fl(1/s) plus one FMA correction (Markstein),
+// which gives the IEEE codes for every bf16 and f16 input (proved
+// exhaustively by tests/exhaustive_division.c); fp32 inputs use the IEEE
+// division itself. All 64 lanes of the wave must call this together.
+template <int A, int DT>
+__device__ __forceinline__ float group_codes(const float v[8], int c[8]) {
+  constexpr int P = (1 << (A - 1)) - 1;
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+  amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+  amax = fmaxf(amax, 1e-8f);
+  const float s = amax / (float)P;
+  const float y = 1.0f / s;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float q;
+    if constexpr (DT == kF32) {
+      q = v[e] / s;
+    } else {
+      const float q0 = v[e] * y;
+      const float r = __builtin_fmaf(-q0, s, v[e]);
+      q = __builtin_fmaf(r, y, q0);
+    }
+    q = fminf(fmaxf(__builtin_rintf(q), (float)(-P - 1)), (float)P);
+    c[e] = (int)q;
+  }
+  return s;
+}
+
+// Byte offset of k-slot kb (16 elements) inside a group, after the weight
+// exchange of gemm_smallm. W4 loads give each lane 32 consecutive k; the
+// swap leaves lanes kb = 0..3 with slots 0, 2, 1, 3 (k offsets 0, 32, 16, 48).
+template <int W>
+__device__ __forceinline__ int smallm_slot_k(int kb) {
+  if constexpr (W == 4) return ((kb & 1) << 5) | ((kb >> 1) << 4);
+  else return kb << 4;
+}
+
+// Turn one 16-byte weight load per lane (lanes kb = 0..3 of a row hold 64
+// consecutive bytes = 8/W groups) into one 16-element slot per group:
+//   W8: no exchange, slot = the 4 dwords;
+//   W4: lanes 0-31 hold group g, lanes 32-63 group g+1; swapping dwords 2,3
+//       of the low half with dwords 0,1 of the high half leaves dwords 0,1 =
+//       slot of g and dwords 2,3 = slot of g+1 in every lane;
+//   W2: lane kb holds group g+kb; a 4x4 transpose of dwords across the four
+//       lane rows (permlane32 then permlane16 swaps) leaves dword j = slot kb
+//       of group g+j.
+template <int W>
+__device__ __forceinline__ void exchange(uint32_t v[4]) {
+  if constexpr (W == 4) {
+    auto r0 = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+    auto r1 = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+    v[0] = r0[0]; v[2] = r0[1]; v[1] = r1[0]; v[3] = r1[1];
+  } else if constexpr (W == 2) {
+    auto r0 = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+    auto r1 = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+    v[0] = r0[0]; v[2] = r0[1]; v[1] = r1[0]; v[3] = r1[1];
+    auto r2 = __builtin_amdgcn_permlane16_swap(v[0], v[1], false, false);
+    auto r3 = __builtin_amdgcn_permlane16_swap(v[2], v[3], false, false);
+    v[0] = r2[0]; v[1] = r2[1]; v[2] = r3[0]; v[3] = r3[1];
+  }
+}
+
+// Activation B-operand slot for token row arow at k offset koff, reordered to
+// the weight width's element order.
+template <int W, int A>
+__device__ __forceinline__ void act_slot(const uint8_t* arow, bool ok, int koff, uint32_t d[4]) {
+  uint32_t p[4];
+  load_slot<A>(arow + (koff * A) / 8, ok, p);
+  unpack_slot<A>(p, d);
+  reorder_slot<A, W>(d);
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+         ((uint32_t)(d & 0xff) << 24);
+}
+
+// Store 8 consecutive codes (elements 8h..8h+7 of a 16-element slot, shifted
+// to the top of their byte for width A) into the slot at `slot` in the
+// element order of weight width W (common.hpp, unpack_slot).
+template <int W, int A>
+__device__ __forceinline__ void store_half_slot(uint8_t* slot, int h, const int c[8]) {
+  int b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = c[e] * (1 << shift_of(A));
+  if constexpr (W == 8) {
+    *reinterpret_cast<v2u*>(slot + 8 * h) = v2u{pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7])};
+  } else if constexpr (W == 4) {
+    *reinterpret_cast<v2u*>(slot + 8 * h) = v2u{pack4(b[0], b[2], b[4], b[6]), pack4(b[1], b[3], b[5], b[7])};
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<uint16_t*>(slot + 4 * r + 2 * h) = (uint16_t)((b[r] & 0xff) | ((b[4 + r] & 0xff) << 8));
+  }
+}
+
+}  // namespace actune

@@ -5,7 +5,7 @@
 // of actune/layers.py:41-42 fused in front:
 //   v = x (or dtype_round(x / input_scale)), p = 2^(A-1)-1,
 //   s = fl32(max(max|v|, f32(1e-8)) / p)          (IEEE division)
-//   c = clamp(rint_half_even(fl32(v / s)), -p-1, p)
+//   c = clamp(rint_half_even(fl32(v / s)), -p-1, p)  (exact; see group_codes)
 //   code k of row m -> byte m*(K*A/8) + k*A/8, bit (k % (8/A))*A.
 //
 // Layout: groups are 64 contiguous elements, and the M*K/64 groups of the
@@ -16,28 +16,9 @@
 // A8 writes 8 B/lane, A4 4 B/lane, A2 2 B/lane.
 #include "common.hpp"
 #include "launch.hpp"
+#include "operands.hpp"
 
 namespace actune {
-
-// Eight consecutive elements starting at i (i % 8 == 0) as fp32, with 16-byte
-// vector loads.
-template <int DT>
-__device__ __forceinline__ void load8(const void* p, long i, float v[8]) {
-  if constexpr (DT == kF32) {
-    const v4u a = reinterpret_cast<const v4u*>(p)[i / 4];
-    const v4u b = reinterpret_cast<const v4u*>(p)[i / 4 + 1];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) { v[e] = __uint_as_float(a[e]); v[e + 4] = __uint_as_float(b[e]); }
-  } else {
-    const v4u q = reinterpret_cast<const v4u*>(p)[i / 8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint16_t lo = (uint16_t)(q[e] & 0xffffu), hi = (uint16_t)(q[e] >> 16);
-      if constexpr (DT == kBF16) { v[2 * e] = bf16_to_f32(lo); v[2 * e + 1] = bf16_to_f32(hi); }
-      else { v[2 * e] = f16_to_f32(lo); v[2 * e + 1] = f16_to_f32(hi); }
-    }
-  }
-}
 
 template <int A, int DT, bool SCALE>
 __global__ __launch_bounds__(256) void quantize_groups_kernel(const void* __restrict__ x,
@@ -45,7 +26,6 @@ __global__ __launch_bounds__(256) void quantize_groups_kernel(const void* __rest
                                                               long groups, int G,
                                                               uint8_t* __restrict__ packed,
                                                               float* __restrict__ scales) {
-  constexpr int P = (1 << (A - 1)) - 1;
   const long gi = (long)blockIdx.x * 32 + (threadIdx.x >> 3);  // global group index m*G + g
   const int seg = threadIdx.x & 7;                               // 8-element segment in the group
   const bool live = gi < groups;
@@ -61,21 +41,12 @@ __global__ __launch_bounds__(256) void quantize_groups_kernel(const void* __rest
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = round_to_dtype<DT>(v[e] / d[e]);
   }
-  float amax = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
-  amax = fmaxf(amax, 1e-8f);
-  const float s = amax / (float)P;
-
+  int c[8];
+  const float s = group_codes<A, DT>(v, c);
   uint32_t bits[2] = {0u, 0u};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    float c = __builtin_rintf(v[e] / s);
-    c = fminf(fmaxf(c, (float)(-P - 1)), (float)P);
-    const uint32_t field = (uint32_t)(int)c & ((1u << A) - 1u);
+    const uint32_t field = (uint32_t)c[e] & ((1u << A) - 1u);
     const int bit = e * A;  // bit position inside this lane's 8*A-bit run
     bits[bit >> 5] |= field << (bit & 31);
   }

@@ -25,6 +25,16 @@ extern "C" {
 #endif
 
 enum { ACTUNE_OK = 0, ACTUNE_ERR_INVALID = 1, ACTUNE_ERR_DEVICE = 2 };
+#define ACTUNE_MAX_TARGETS 4
+
+/* One linear of a multi-target call (all targets share x, K, W and A). */
+typedef struct actune_linear_target {
+  const uint8_t* w;      /* packed weights [N, K*W/8] */
+  const float* w_scale;  /* [N] */
+  const void* bias;      /* [N] in the call's bias dtype, or NULL */
+  void* out;             /* [M, N] in x's dtype */
+  int64_t N;
+} actune_linear_target;
 enum { ACTUNE_DTYPE_BF16 = 0, ACTUNE_DTYPE_F16 = 1, ACTUNE_DTYPE_F32 = 2 };
 #define ACTUNE_CONFIG_AUTO (-1)
 
@@ -63,13 +73,30 @@ int actune_grouped_linear(const uint8_t* a, const float* a_scales, const uint8_t
 /*
  * Quantize + linear in one call (two launches): the whole per-call device
  * work of GroupedLinear.forward, actune/kernels/grouped.py:127-143.
- * a_buf [M, K*A/8] and scale_buf [M, K/64] are caller-owned scratch that
- * receive the packed activations and their scales.
+ * a_buf [M, K*A/8] and scale_buf [M, K/64] are caller-owned scratch (not
+ * written when the quantizer is fused into the GEMM, see below).
  */
 int actune_grouped_forward(const void* x, int x_dtype, const void* input_scale, uint8_t* a_buf,
                            float* scale_buf, const uint8_t* w, const float* w_scale, const void* bias,
                            int bias_dtype, void* out, int64_t M, int64_t N, int64_t K, int W, int A,
                            int config, void* stream);
+
+/*
+ * Quantize + linear for up to ACTUNE_MAX_TARGETS linears that read the same
+ * input x (sibling projections such as q/k/v or gate/up): one quantization
+ * and one GEMM launch for all of them. Each target is the computation of
+ * GroupedLinear.forward (grouped.py:127-143); results equal separate
+ * actune_grouped_forward calls bit for bit. No reference counterpart for the
+ * group-64 path; it mirrors the sibling-projection grouping of the
+ * reference's tokenwise decode path (actune/kernels/decode_w4a8_triton.py:152-239).
+ * The quantizer runs inside the GEMM (a_buf / scale_buf are then not
+ * written) for M <= 4 on the small-M and streaming configs; otherwise
+ * a_buf / scale_buf receive the packed activations and scales.
+ */
+int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_scale, uint8_t* a_buf,
+                                 float* scale_buf, const actune_linear_target* targets, int ntargets,
+                                 int bias_dtype, int64_t M, int64_t K, int W, int A, int config,
+                                 void* stream);
 
 /*
  * Exact per-group int32 dots dots[m][n][g] = sum_{k in g} a[m,k] * w[n,k]
@@ -83,6 +110,9 @@ int actune_grouped_dots_i32(const uint8_t* a, const uint8_t* w, int64_t M, int64
 /*
  * Kernel configurations, the counterpart of the 13 tile geometries of
  * actune/kernels/grouped_big_m.cu:115-130 selected by tuning.py:16-45.
+ *   0, 1, 2  small-M split-K kernel with 4, 8, 16 waves (M <= 64)
+ *   3 .. 6   MFMA-tiled kernel shapes (any M)
+ *   7, 8, 9  persistent streaming kernel with 4, 8, 16 waves (M <= 16)
  * actune_config_valid: 1 if `config` can run a call with M rows.
  * actune_default_config: the config ACTUNE_CONFIG_AUTO resolves to.
  */

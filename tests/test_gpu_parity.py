@@ -181,3 +181,67 @@ def test_full_size_sampled_parity(m, n, k, W, A):
     want = O.linear(a_codes, want_s, codes, scale, None, bounds=canonical_bounds(k // 64), rows=rows, cols=cols)
     got = bits(out)[rows][:, cols]
     np.testing.assert_array_equal(got, O.round_out(want, "bf16"))
+
+
+# ---------------------------------------------------------------- fused / siblings
+@pytest.mark.parametrize("W,A", PAIRS)
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_fused_small_m_equals_two_step(W, A, m, dtype):
+    """M <= 4 quantizes inside the GEMM; it must equal quantize + GEMM and the
+    oracle bit for bit, with and without the fused channel scale."""
+    k, n = 704, 80  # G = 11: ragged chunks and a partial weight step
+    x, w, b = seeded_inputs(m, k, n, seed=W * A + m, dtype=dtype, bias=True)
+    _, _, w_dev, ws_dev = _packed_weight(w, W, A)
+    xd, bd = x.to(DEV), b.to(DEV)
+    for scale in (None, torch.linspace(0.5, 2.0, k).to(dtype)):
+        sd = None if scale is None else scale.to(DEV)
+        for config in range(3):
+            fused = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, input_scale=sd, config=config)
+            p, s = _native.quantize_groups(xd, A, sd)
+            two = _native.grouped_linear(p, s, w_dev, ws_dev, bd, xd, W, A, config)
+            assert torch.equal(fused, two), (config, scale is None)
+        a_packed, a_scales, a_codes = oracle_activation(x, A, scale)
+        wc, wsc = oracle_weight(w, W, A)
+        want = O.linear(a_codes, a_scales, wc, wsc, b.float().numpy(), bounds=canonical_bounds(k // 64))
+        np.testing.assert_array_equal(bits(fused), O.round_out(want, dtype_name(dtype)))
+
+
+@pytest.mark.parametrize("m", [1, 4, 8, 50, 100])
+@pytest.mark.parametrize("W,A", [(4, 8), (2, 4), (8, 2)])
+def test_multi_target_equals_separate_calls(m, W, A):
+    k = 512
+    x, _, _ = seeded_inputs(m, k, 1, seed=m)
+    xd = x.to(DEV)
+    targets = []
+    for j, n in enumerate((96, 32, 160)):
+        _, w, b = seeded_inputs(1, k, n, seed=100 + j, bias=True)
+        _, _, w_dev, ws_dev = _packed_weight(w, W, A)
+        targets.append((w_dev, ws_dev, b.to(DEV), None))
+    outs = _native.grouped_forward_multi(xd, targets, W, A)
+    for (w_dev, ws_dev, bd, _), out in zip(targets, outs):
+        assert torch.equal(out, _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A))
+
+
+@pytest.mark.parametrize("W,A", PAIRS)
+@pytest.mark.parametrize("m", [1, 3, 8, 13, 16])
+def test_streaming_fused_equals_two_step(W, A, m):
+    """Streaming configs (fused quantizer for M <= 4, LDS-staged packed
+    activations above) equal quantize + GEMM and the oracle bit for bit
+    (bf16 and f16, with and without the channel scale)."""
+    k, n = 1344, 200  # G = 21: uneven wave ranges; N not a multiple of 16
+    for dtype in (torch.bfloat16, torch.float16):
+        x, w, b = seeded_inputs(m, k, n, seed=W * 11 + A + m, dtype=dtype, bias=True)
+        _, _, w_dev, ws_dev = _packed_weight(w, W, A)
+        xd, bd = x.to(DEV), b.to(DEV)
+        scale = torch.linspace(0.5, 2.0, k).to(dtype)
+        for sd in (None, scale.to(DEV)):
+            p, s = _native.quantize_groups(xd, A, sd)
+            ref = _native.grouped_linear(p, s, w_dev, ws_dev, bd, xd, W, A, 3)
+            for config in (7, 8, 9):
+                out = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, input_scale=sd, config=config)
+                assert torch.equal(out, ref), (dtype, config, sd is None)
+        a_packed, a_scales, a_codes = oracle_activation(x, A, scale)
+        wc, wsc = oracle_weight(w, W, A)
+        want = O.linear(a_codes, a_scales, wc, wsc, b.float().numpy(), bounds=canonical_bounds(k // 64))
+        np.testing.assert_array_equal(bits(out), O.round_out(want, dtype_name(dtype)))

@@ -36,9 +36,10 @@ def test_version_and_layout_selftest():
 
 def test_config_table():
     n = _native.num_configs()
-    assert n == 7
-    assert _native.config_valid(0, 16) and not _native.config_valid(0, 17)
-    assert all(_native.config_valid(c, 4096) for c in range(3, n))
+    assert n == 10
+    assert _native.config_valid(0, 64) and not _native.config_valid(0, 65)
+    assert all(_native.config_valid(c, 4096) for c in range(3, 7))
+    assert _native.config_valid(9, 16) and not _native.config_valid(9, 17)
     assert not _native.config_valid(n, 1) and not _native.config_valid(-2, 1)
     for m in (1, 8, 16, 17, 50, 512):
         c = _native.default_config(m, 4096, 4096, 4, 8)
@@ -65,7 +66,7 @@ def test_quantize_rejects_bad_arguments(args, msg):
     (dict(W=5), "Unsupported integer width"),
     (dict(K=96), "invalid dimensions"),
     (dict(N=0), "invalid dimensions"),
-    (dict(config=0, M=17), "M <= 16"),
+    (dict(config=0, M=65), "M <= 64"),
     (dict(config=99), "invalid configuration"),
     (dict(out_dt=9), "dtype"),
     (dict(M=4), "null pointer"),
