@@ -35,6 +35,9 @@ def flags() -> list[str]:
         "-ffp-contract=off",
         # packed fp32 VALU ops are kept out of the generated code
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA results in VGPRs: the fp32 epilogue reads them without
+        # v_accvgpr_read copies
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-Wall", "-Wno-unused-function", "-Wno-unused-command-line-argument",
     ]
 
