@@ -132,3 +132,45 @@ def _zero_padded(linear, padded):
         if fc.bias is not None:
             fc.bias.copy_(linear.bias)
     return fc
+
+
+def grouped_sibling_forward(x, modules):
+    """Run GroupedPaddedLinear (or ResidentLinear) modules that read the same
+    input x — sibling projections such as q/k/v or gate/up — and return their
+    outputs in order.
+
+    When every module's active backend has the same (W, A), K, padding, bias
+    dtype and input scale, all of them run in ONE quantize + GEMM launch
+    (actune_grouped_forward_multi, up to 4 targets); otherwise each module
+    runs on its own. Either way the outputs are bit-identical to calling the
+    modules one by one, and each module's calls / input_elements counters
+    advance exactly as for a separate call (BankRuntime.audit relies on them).
+    """
+    modules = list(modules)
+    if not modules:
+        return []
+    backends = [m.active_backend() for m in modules]
+    first, fb = modules[0], backends[0]
+    scale = getattr(first, "input_scale", None)
+    fusable = (
+        x.is_cuda and 1 < len(modules) <= _native.MAX_TARGETS
+        and all(getattr(b.forward, "__func__", None) is GroupedLinear.forward for b in backends)
+        and all(m.in_features == first.in_features and m.padding == first.padding for m in modules)
+        and all((b.w, b.a) == (fb.w, fb.a) for b in backends)
+        and len({None if b.bias is None else b.bias.dtype for b in backends}) == 1
+        and all(getattr(m, "input_scale", None) is scale for m in modules)
+        and (scale is None or scale.dtype == x.dtype)
+    )
+    if not fusable:
+        return [m(x) for m in modules]
+    for m in modules:
+        m.calls += 1
+        m.input_elements += x.numel()
+    if first.padding:
+        x = torch.nn.functional.pad(x, (0, first.padding))
+        if scale is not None:
+            scale = torch.nn.functional.pad(scale, (0, first.padding), value=1.0)
+    flat = x.reshape(-1, fb.in_features).contiguous()
+    targets = [(b.packed_weight, b.weight_scale, b.bias, None) for b in backends]
+    outs = _native.grouped_forward_multi(flat, targets, fb.w, fb.a, input_scale=scale, config=fb.config)
+    return [o.reshape(*x.shape[:-1], m.out_features) for o, m in zip(outs, modules)]

@@ -5,19 +5,26 @@ decoder layer (q/k/v/o 4096x4096, gate/up 4096->11008, down 11008->4096),
 W4A8 group-64, synthetic activations N(0,1) with 1 % outlier channels x10
 and synthetic packed W4 codes + per-channel scales, over `--layers` layers
 of distinct weights (1.2 GB at the default 12 layers, well above the 256 MB
-Infinity Cache). One step = one pass over the stack at M=1 token: for every
-linear the group-64 quantizer and the packed GEMM (actune_grouped_forward),
-all captured in one hipGraph. Inputs are resident in HBM; `value` is the
-packed-weight bytes streamed per second over the whole step.
+Infinity Cache). One step = one pass over the stack at M=1 token: every
+linear's group-64 quantization and packed GEMM. Inputs are resident in HBM.
+
+Two schedules of the same work, each captured in one hipGraph:
+  siblings   q/k/v and gate/up (which read the same input) in one launch
+             each (actune_grouped_forward_multi): 4 launches per layer;
+  per-linear one actune_grouped_forward call per linear: 7 per layer.
+Both give bit-identical outputs. At M=1 every launch is the fused
+quantize+GEMM small-M kernel (no separate quantizer launch). `value` is the
+packed-weight bytes streamed per second over the siblings step.
 
 Printed JSON line: the driver's contract fields plus
-  roofline      the dominant kernel (small-M packed GEMM, gemm_smallm) timed
-                with HIP events on its own stream over a GEMM-only graph of
-                the same stack: algorithmic bytes / average launch duration
-                vs 8 TB/s;
+  roofline      the dominant kernel (the fused small-M quantize+GEMM, every
+                launch of the M=1 step): algorithmic bytes per step / step
+                time (HIP events on the replay stream) vs 8 TB/s, and the
+                average launch duration; traffic from the committed
+                rocprofv3 PMC summary (profiles/), if present;
   cpu_baseline  the reference's dequantize-then-matmul path in torch-CPU
                 (oracle/cpu_path.py) on a bounded sample (rank 0, N=1);
-  detail        M=8 pass, per-shape us/launch, quantizer share.
+  detail        per-linear schedule, M=8, per-shape us/launch.
 """
 from __future__ import annotations
 
@@ -136,6 +143,46 @@ def cpu_baseline(seconds, W, A):
                        f"{dt:.1f} s, {dt / passes / 7 * 1e6:.0f} us/linear")
 
 
+def run_schedule(torch, _native, stack, W, A, siblings, steps, warmup):
+    """Capture one pass over the stack and time it; returns ms/step, launches."""
+    groups = []
+    if siblings:
+        by_layer = [stack[i:i + len(SHAPES)] for i in range(0, len(stack), len(SHAPES))]
+        for layer in by_layer:
+            names = {e["name"]: e for e in layer}
+            groups += [[names["q"], names["k"], names["v"]], [names["o"]],
+                       [names["gate"], names["up"]], [names["down"]]]
+    else:
+        groups = [[e] for e in stack]
+
+    def step():
+        for grp in groups:
+            e0 = grp[0]
+            if len(grp) == 1:
+                _native.grouped_forward(e0["x"], e0["w"], e0["ws"], None, W, A, out=e0["out"],
+                                        packed=e0["a"], scales=e0["s"])
+            else:
+                _native.grouped_forward_multi(e0["x"], [(e["w"], e["ws"], None, e["out"]) for e in grp], W, A,
+                                              packed=e0["a"], scales=e0["s"])
+
+    graph = capture(torch, step)
+    ms = time_graph(torch, graph, steps, warmup)
+    del graph
+    return ms, len(groups)
+
+
+def load_traffic(m):
+    """Per-launch HBM bytes of the M=m step measured with rocprofv3 PMC
+    counters (FETCH_SIZE / WRITE_SIZE scaled by a copy-kernel calibration),
+    committed as profiles/traffic_c2.json; None when absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_c2.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(f"M={m}")
+    except (OSError, ValueError):
+        return None
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -161,53 +208,36 @@ def main():
     results = {}
     for m in (1, 8):
         stack = build_stack(torch, m, args.layers, W, A)
-        cfg = _native.default_config(m, 4096, 4096, W, A)
-
-        def forward_pass():
-            for e in stack:
-                _native.grouped_forward(e["x"], e["w"], e["ws"], None, W, A, config=cfg, out=e["out"],
-                                        packed=e["a"], scales=e["s"])
-
-        def quant_pass():
-            for e in stack:
-                _native.quantize_groups(e["x"], A, packed=e["a"], scales=e["s"])
-
-        def gemm_pass():
-            for e in stack:
-                _native.grouped_linear(e["a"], e["s"], e["w"], e["ws"], None, e["x"], W, A, cfg, out=e["out"])
-
-        full = capture(torch, forward_pass)
-        quant = capture(torch, quant_pass)
-        gemm = capture(torch, gemm_pass)
-        torch.cuda.synchronize()
-        ms_full = time_graph(torch, full, args.steps, args.warmup)
-        ms_gemm = time_graph(torch, gemm, args.steps, args.warmup)
-        ms_quant = time_graph(torch, quant, args.steps, args.warmup)
+        r = {}
+        r["ms_sib"], r["launches_sib"] = run_schedule(torch, _native, stack, W, A, True, args.steps, args.warmup)
+        r["ms_lin"], r["launches_lin"] = run_schedule(torch, _native, stack, W, A, False, args.steps, args.warmup)
         per_shape = {}
         for name, n, k in (SHAPES[0], SHAPES[4], SHAPES[6]):
             subset = [e for e in stack if e["name"] == name]
 
             def one_shape(subset=subset):
                 for e in subset:
-                    _native.grouped_linear(e["a"], e["s"], e["w"], e["ws"], None, e["x"], W, A, cfg, out=e["out"])
+                    _native.grouped_forward(e["x"], e["w"], e["ws"], None, W, A, out=e["out"],
+                                            packed=e["a"], scales=e["s"])
 
             gph = capture(torch, one_shape)
             us = time_graph(torch, gph, args.steps, args.warmup) * 1e3 / len(subset)
-            per_shape[f"{n}x{k}"] = dict(us_per_launch=round(us, 3),
-                                         weight_GBps=round(n * k * W / 8 / us / 1e3, 1))
+            per_shape[f"{n}x{k}"] = dict(us_per_launch=round(us, 3), weight_GBps=round(n * k * W / 8 / us / 1e3, 1),
+                                         config=_native.default_config(m, n, k, W, A))
             del gph
-        wbytes = sum(e["n"] * e["k"] * W // 8 for e in stack)
-        abytes = sum(gemm_bytes(e["n"], e["k"], m, W, A) for e in stack)
-        ops = sum(2 * m * e["n"] * e["k"] for e in stack)
-        results[m] = dict(ms_full=ms_full, ms_gemm=ms_gemm, ms_quant=ms_quant, wbytes=wbytes, abytes=abytes,
-                          ops=ops, launches=len(stack), per_shape=per_shape, config=cfg)
-        del full, quant, gemm, stack
+        r["per_shape"] = per_shape
+        r["wbytes"] = sum(e["n"] * e["k"] * W // 8 for e in stack)
+        r["abytes"] = sum(gemm_bytes(e["n"], e["k"], m, W, A) for e in stack)
+        r["ops"] = sum(2 * m * e["n"] * e["k"] for e in stack)
+        r["linears"] = len(stack)
+        results[m] = r
+        del stack
         torch.cuda.synchronize()
 
     r1 = results[1]
-    value = r1["wbytes"] / (r1["ms_full"] * 1e-3) / 1e9
-    gemm_us = r1["ms_gemm"] * 1e3 / r1["launches"]
-    achieved = r1["abytes"] / (r1["ms_gemm"] * 1e-3) / 1e9
+    value = r1["wbytes"] / (r1["ms_sib"] * 1e-3) / 1e9
+    achieved = r1["abytes"] / (r1["ms_sib"] * 1e-3) / 1e9
+    traffic = load_traffic(1)
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -215,32 +245,35 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(r1["ms_full"], 4),
+        "ms_per_step": round(r1["ms_sib"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (random packed W4 codes + scales; N(0,1) activations with 1% outlier channels x10)",
-        "config": {"workload": "Llama-2-7B decoder linear stack (q,k,v,o,gate,up,down), batch 1, M=1 token",
+        "config": {"workload": "Llama-2-7B decoder linear stack (q,k,v,o,gate,up,down), batch 1, M=1 token, "
+                               "sibling projections fused",
                    "layers": args.layers, "W": W, "A": A, "group": 64, "M": 1,
-                   "weight_bytes_per_step": r1["wbytes"], "launches_per_step": 2 * r1["launches"],
-                   "gemm_config": r1["config"]},
-        "us_per_linear": round(r1["ms_full"] * 1e3 / r1["launches"], 3),
+                   "weight_bytes_per_step": r1["wbytes"], "launches_per_step": r1["launches_sib"]},
+        "us_per_linear": round(r1["ms_sib"] * 1e3 / r1["linears"], 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "gemm_smallm (packed W4A8 GEMM, M=1)",
-                     "avg_launch_us": round(gemm_us, 3)},
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": None if traffic is None else traffic.get("bytes_per_launch"),
+                     "kernel": "fused group-64 quantize + packed W4A8 GEMM, small-M (gemm_smallm / gemm_stream)",
+                     "avg_launch_us": round(r1["ms_sib"] * 1e3 / r1["launches_sib"], 3),
+                     "algorithmic_bytes_per_launch": round(r1["abytes"] / r1["launches_sib"])},
         "detail": {},
     }
     for m, r in results.items():
         line["detail"][f"M={m}"] = {
-            "us_per_linear": round(r["ms_full"] * 1e3 / r["launches"], 3),
-            "gemm_us_per_launch": round(r["ms_gemm"] * 1e3 / r["launches"], 3),
-            "quant_us_per_launch": round(r["ms_quant"] * 1e3 / r["launches"], 3),
-            "weight_GBps_whole_step": round(r["wbytes"] / (r["ms_full"] * 1e-3) / 1e9, 1),
-            "weight_GBps_gemm_only": round(r["wbytes"] / (r["ms_gemm"] * 1e-3) / 1e9, 1),
-            "int8_TOPS_gemm_only": round(r["ops"] / (r["ms_gemm"] * 1e-3) / 1e12, 3),
-            "per_shape_gemm": r["per_shape"],
+            "siblings": {"ms_per_step": round(r["ms_sib"], 4), "launches": r["launches_sib"],
+                         "us_per_linear": round(r["ms_sib"] * 1e3 / r["linears"], 3),
+                         "weight_GBps": round(r["wbytes"] / (r["ms_sib"] * 1e-3) / 1e9, 1),
+                         "int8_TOPS": round(r["ops"] / (r["ms_sib"] * 1e-3) / 1e12, 3)},
+            "per_linear": {"ms_per_step": round(r["ms_lin"], 4), "launches": r["launches_lin"],
+                           "us_per_linear": round(r["ms_lin"] * 1e3 / r["linears"], 3),
+                           "weight_GBps": round(r["wbytes"] / (r["ms_lin"] * 1e-3) / 1e9, 1)},
+            "per_shape": r["per_shape"],
         }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, W, A)
