@@ -52,7 +52,36 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 1 GiB device copy (for PMC byte-counter calibration)")
+    p.add_argument("--only", choices=sorted(ONLY_SHAPES),
+                   help="only launch one shape 24 times over distinct weights (for rocprofv3 counter runs)")
     return p.parse_args()
+
+
+# --only: (M, [(N, K) per target], kernel config) — M=1 decode launches of the C2 step and one C3 prefill
+ONLY_SHAPES = {
+    "q": (1, [(4096, 4096)], -1), "gate": (1, [(11008, 4096)], -1), "down": (1, [(4096, 11008)], -1),
+    "qkv": (1, [(4096, 4096)] * 3, -1), "gateup": (1, [(11008, 4096)] * 2, -1),
+    "prefill512": (512, [(4096, 4096)], -1),
+}
+
+
+def run_only(torch, _native, name, W, A):
+    m, spec, cfg = ONLY_SHAPES[name]
+    k = spec[0][1]
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(m, k, device="cuda").to(torch.bfloat16)
+    sets = [[(torch.randint(0, 256, (n, k * W // 8), generator=g, device="cuda", dtype=torch.uint8),
+              torch.rand(n, device="cuda") * 0.01, None, torch.empty(m, n, device="cuda", dtype=torch.bfloat16))
+             for n, _ in spec] for _ in range(24)]
+    torch.cuda.synchronize()
+    for t in sets:
+        if len(t) == 1:
+            w, ws, _, out = t[0]
+            _native.grouped_forward(x, w, ws, None, W, A, config=cfg, out=out)
+        else:
+            _native.grouped_forward_multi(x, t, W, A, config=cfg)
+    torch.cuda.synchronize()
+    print(json.dumps(dict(only=name, M=m, targets=spec, launches=len(sets))))
 
 
 def build_stack(torch, m, layers, W, A, seed=0):
@@ -202,6 +231,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps(dict(copy_bytes=1 << 30, launches=5)))
+        return 0
+    if args.only:
+        run_only(torch, _native, args.only, args.W, args.A)
         return 0
 
     W, A = args.W, args.A
