@@ -1,0 +1,335 @@
+"""GPU tests of the Python module surface on the HIP path.
+
+The modules (GroupedLinear, GroupedPaddedLinear, ResidentLinear, install_bank,
+GraphReplay, the bit-exact tuner and sibling launches) are checked against the
+CPU oracle (bit-exact bf16 in the library's canonical order) and against their
+own eager execution. Shapes follow the reference's module tests
+(tests/test_kernels.py:28-49, tests/test_method.py:92-124) and the
+Gemma-300M-shaped action expert: width 1024, MLP 1024->4096->1024, 50-token
+action chunks, q00/q01/q11/q10 switching under graph replay.
+"""
+import numpy as np
+import pytest
+import torch
+
+from actune_amd import _native
+from actune_amd.graph import GraphReplay
+from actune_amd.kernels import tuning
+from actune_amd.kernels.grouped import GroupedLinear, GroupedPaddedLinear, grouped_sibling_forward
+from actune_amd.layers import ResidentLinear, install_bank, tensor_storage_bytes
+from actune_amd.precision import CONFIGURATIONS, SharedBank, precision_profile
+from oracle import oracle as O
+from tests.helpers import PAIRS, bits, canonical_bounds, dtype_name, oracle_activation, seeded_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _linear(k, n, bias, seed, dtype=torch.bfloat16):
+    _, w, b = seeded_inputs(1, k, n, seed=seed, dtype=dtype, bias=bias)
+    lin = torch.nn.Linear(k, n, bias=bias, dtype=dtype)
+    with torch.no_grad():
+        lin.weight.copy_(w)
+        if bias:
+            lin.bias.copy_(b)
+    return lin
+
+
+def _oracle_module(backend, x_flat, input_scale=None):
+    """Oracle output of one GroupedLinear on x_flat [M, K] (cpu)."""
+    k = backend.in_features
+    wc = O.unpack_rows(backend.packed_weight.cpu().numpy(), backend.w, k)
+    ws = backend.weight_scale.cpu().numpy()
+    bias = None if backend.bias is None else backend.bias.float().cpu().numpy()
+    _, a_scales, a_codes = oracle_activation(x_flat, backend.a, input_scale)
+    want = O.linear(a_codes, a_scales, wc, ws, bias, bounds=canonical_bounds(k // 64))
+    return O.round_out(want, dtype_name(x_flat.dtype))
+
+
+# ---------------------------------------------------------------- modules
+@pytest.mark.parametrize("W,A", PAIRS)
+@pytest.mark.parametrize("lead", [(1,), (2, 3), (4, 16)])
+def test_grouped_linear_forward_matches_oracle(W, A, lead):
+    k, n = 320, 72
+    lin = _linear(k, n, True, seed=W * 3 + A)
+    mod = GroupedLinear(lin, W, A, None).to(DEV)
+    assert mod.bias.dtype == (torch.float32 if A == 4 else torch.bfloat16)
+    g = torch.Generator().manual_seed(len(lead))
+    x = torch.randn(*lead, k, generator=g).to(torch.bfloat16)
+    out = mod(x.to(DEV))
+    assert out.shape == (*lead, n) and out.dtype == torch.bfloat16
+    want = _oracle_module(mod, x.reshape(-1, k))
+    np.testing.assert_array_equal(bits(out.reshape(-1, n)), want)
+
+
+def test_grouped_linear_rejects_host_input():
+    mod = GroupedLinear(_linear(64, 16, False, 1), 4, 8, None).to(DEV)
+    with pytest.raises(ValueError, match="requires CUDA"):
+        mod(torch.zeros(1, 64, dtype=torch.bfloat16))
+
+
+def test_padded_linear_dispatch_on_gpu():
+    """K = 100 pads to 128 with zero weight columns; each profile runs its own
+    backend; counters count logical input elements."""
+    lin = _linear(100, 40, True, seed=5)
+    assign = {"q00": "w2a4", "q01": "w4a2", "q11": "w4a8", "q10": "w8a8"}
+    clips = {"w2a4": None, "w4a2": 0.9, "w4a8": None, "w8a8": None}
+    p = GroupedPaddedLinear(lin, assign, "q11", clips).to(DEV)
+    x = torch.randn(7, 100, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+    xp = torch.nn.functional.pad(x, (0, 28))
+    for q in (None, *CONFIGURATIONS):
+        mode = assign[q or "q11"]
+        if q is None:
+            out = p(x.to(DEV))
+        else:
+            with precision_profile(q):
+                out = p(x.to(DEV))
+        np.testing.assert_array_equal(bits(out), _oracle_module(p.backends[mode], xp), err_msg=str(q))
+    assert p.calls == 5 and p.input_elements == 5 * 700
+
+
+@pytest.mark.parametrize("m", [1, 3, 4, 5, 50])
+@pytest.mark.parametrize("A", [2, 4, 8])
+def test_resident_linear_fused_scale_equals_torch_division(m, A):
+    """layers.py:41-42: forward quantizes x / input_scale rounded to x's
+    dtype. The fused quantizer (M <= 4 inside the GEMM, standalone above)
+    must equal quantizing torch's own division, and the oracle."""
+    k, n = 256, 48
+    lin = _linear(k, n, False, seed=m + A)
+    scale = torch.linspace(0.25, 4.0, k).to(torch.bfloat16)
+    r = ResidentLinear(lin, {q: f"w4a{A}" for q in CONFIGURATIONS}, {f"w4a{A}": None}, scale).to(DEV)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    out = r(x.to(DEV))
+    divided = (x.to(DEV) / scale.to(DEV)).contiguous()
+    plain = r.backends[f"w4a{A}"](divided)
+    assert torch.equal(out, plain)
+    np.testing.assert_array_equal(bits(out), _oracle_module(r.backends[f"w4a{A}"], x, scale))
+
+
+def test_resident_linear_float_input_with_bf16_scale():
+    """x in fp32 with a bf16 channel scale: the module divides in torch
+    (fp32 result) and the fp32 quantizer path runs."""
+    k, n = 128, 32
+    lin = _linear(k, n, False, seed=2)
+    scale = torch.linspace(0.5, 2.0, k).to(torch.bfloat16)
+    r = ResidentLinear(lin, {q: "w8a8" for q in CONFIGURATIONS}, {"w8a8": None}, scale).to(DEV)
+    x = torch.randn(3, k, generator=torch.Generator().manual_seed(3))
+    out = r(x.to(DEV))
+    assert out.dtype == torch.float32
+    divided = (x.to(DEV) / scale.to(DEV)).cpu()  # the module's own torch division
+    np.testing.assert_array_equal(bits(out), _oracle_module(r.backends["w8a8"], divided))
+
+
+# ---------------------------------------------------------------- the expert bank
+EXPERT = {  # Gemma-300M-shaped action expert, one block
+    "q": (1024, 1024, True), "k": (256, 1024, True), "v": (256, 1024, True), "o": (1024, 1024, False),
+    "gate": (4096, 1024, False), "up": (4096, 1024, False), "down": (1024, 4096, False),
+}
+FIXED = {"q": "w4a4", "k": "w8a4", "v": "w4a4", "o": "w2a4", "down": "w4a4"}
+SWITCH = {"q00": ("w4a4", "w4a4"), "q01": ("w4a4", "w4a2"), "q11": ("w2a4", "w4a2"), "q10": ("w2a4", "w4a4")}
+
+
+class Expert(torch.nn.Module):
+    def __init__(self, seed=0):
+        super().__init__()
+        for i, (name, (n, k, bias)) in enumerate(EXPERT.items()):
+            setattr(self, name, _linear(k, n, bias, seed=seed * 100 + i))
+
+    def forward(self, x, fused_siblings=False):
+        if fused_siblings:
+            k, v = grouped_sibling_forward(x, [self.k, self.v])
+            gate, up = grouped_sibling_forward(x, [self.gate, self.up])
+        else:
+            k, v = self.k(x), self.v(x)
+            gate, up = self.gate(x), self.up(x)
+        q = self.q(x)
+        h = x + self.o(q * 0.5)
+        h = h + self.down(torch.nn.functional.silu(gate) * up)
+        return h, k, v
+
+
+def _version_bytes(n, k, bias, mode):
+    w, a = int(mode[1]), int(mode[3])
+    return n * k * w // 8 + 4 * n + (0 if not bias else (4 * n if a == 4 else 2 * n))
+
+
+def expert_bank(limit=1 << 30):
+    configs = {}
+    for q, (g, u) in SWITCH.items():
+        configs[q] = dict(FIXED, gate=g, up=u)
+    modes = [f"w{w}a{a}" for w in (2, 4, 8) for a in (2, 4, 8)]
+    sizes = {name: {m: _version_bytes(n, k, b, m) for m in modes} for name, (n, k, b) in EXPERT.items()}
+    return SharedBank(configurations=configs, shapes={n: [s[0], s[1]] for n, s in EXPERT.items()},
+                      activation_elements={n: 50 * s[1] for n, s in EXPERT.items()},
+                      shape_groups=[["q", "k", "v", "gate", "up"], ["o"], ["down"]],
+                      version_bytes=sizes, budget="w4a4", storage_limit=limit)
+
+
+def _install(tune=False, scales=False, seed=0):
+    model = Expert(seed).to(DEV)
+    bank = expert_bank()
+    clips = {n: {m: None for m in {c[n] for c in bank.configurations.values()}} for n in bank.shapes}
+    channel = None
+    if scales:
+        channel = {n: torch.linspace(0.5, 2.0, EXPERT[n][1]).to(torch.bfloat16) for n in ("q", "gate", "up")}
+    runtime = install_bank(model, bank, clips, channel_scales=channel, tune=tune)
+    return model, bank, runtime
+
+
+def test_install_bank_holds_w2_w4_w8_and_switches():
+    model, bank, runtime = _install()
+    assert sorted(model.gate.backends) == ["w2a4", "w4a4"] and sorted(model.up.backends) == ["w4a2", "w4a4"]
+    assert list(model.k.backends) == ["w8a4"] and list(model.o.backends) == ["w2a4"]
+    resident = sum(tensor_storage_bytes(getattr(model, n)) for n in EXPERT)
+    assert resident == bank.resident_bytes()
+    x = torch.randn(50, 1024, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    xd = x.to(DEV)
+    for q in CONFIGURATIONS:
+        runtime.before()
+        with precision_profile(q):
+            h, kk, vv = model(xd)
+        metrics = runtime.audit(q)
+        assert metrics["weight_bits"] <= 4 and metrics["activation_bits"] <= 4
+        g_mode, u_mode = SWITCH[q]
+        np.testing.assert_array_equal(bits(kk), _oracle_module(model.k.backends["w8a4"], x))
+        gate = model.gate.backends[g_mode](xd)
+        up = model.up.backends[u_mode](xd)
+        np.testing.assert_array_equal(bits(gate), _oracle_module(model.gate.backends[g_mode], x), err_msg=q)
+        np.testing.assert_array_equal(bits(up), _oracle_module(model.up.backends[u_mode], x), err_msg=q)
+
+
+def _denoise(step, x, profiles, model, fused=False):
+    """10 flow-matching steps: x <- x + dt * h(x) under a seeded per-call
+    precision schedule, with eager work between the calls."""
+    trace = []
+    for i, q in enumerate(profiles):
+        with precision_profile(q):
+            h, kk, vv = step(x, fused)
+        h = h.clone()
+        trace.append((h, kk.clone(), vv.clone()))
+        x = (x.float() + 0.1 * h.float()).to(torch.bfloat16)
+    return x, trace
+
+
+def _schedule(seed=1234, steps=10):
+    g = np.random.default_rng(seed)
+    return [CONFIGURATIONS[i] for i in g.integers(0, 4, steps)]
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_graph_replay_precision_schedule_matches_eager(fused):
+    """C5: 10 denoise steps over a 50-token chunk with q00/q01/q11/q10
+    switching from a seeded schedule. Graph replays (one graph per active
+    configuration) equal eager execution bit for bit, every replay, with eager
+    work and synchronisations in between; counters match eager counts."""
+    model, bank, runtime = _install()
+    profiles = _schedule()
+    assert len(set(profiles)) >= 3
+    x0 = torch.randn(50, 1024, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16).to(DEV)
+
+    runtime.before()
+    x_eager, eager = _denoise(model, x0, profiles, model, fused)
+    eager_counts = {n: (m.calls, m.input_elements) for n, m in runtime.modules.items()}
+
+    replay = GraphReplay(model, runtime.modules)
+    replay.enabled = True
+    runtime.before()
+    x_graph, graphed = _denoise(replay, x0, profiles, model, fused)
+    torch.cuda.synchronize()
+    assert len(replay.graphs) == len(set(profiles)) and replay.fallbacks == 0
+    assert replay.replays == len(profiles)
+    for i, (a, b) in enumerate(zip(eager, graphed)):
+        for t_e, t_g in zip(a, b):
+            assert torch.equal(t_e, t_g), (i, profiles[i])
+    assert torch.equal(x_eager, x_graph)
+    assert {n: (m.calls, m.input_elements) for n, m in runtime.modules.items()} == eager_counts
+    for q in set(profiles):
+        per_call = {n: 50 * EXPERT[n][1] for n in EXPERT}
+        bank.check_request(q, per_call)
+
+
+def test_graph_replay_limit_falls_back_to_eager():
+    model, _, runtime = _install()
+    replay = GraphReplay(model, runtime.modules, max_graphs=2)
+    replay.enabled = True
+    x = torch.randn(50, 1024, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16).to(DEV)
+    outs = {}
+    for q in CONFIGURATIONS + CONFIGURATIONS:
+        with precision_profile(q):
+            got = replay(x)[0].clone()
+            want = model(x)[0]
+        assert torch.equal(got, want), q
+        outs.setdefault(q, got)
+    assert len(replay.graphs) == 2 and replay.fallbacks == 4 and replay.replays == 4
+    assert not torch.equal(outs["q00"], outs["q11"])  # the profiles really differ
+
+
+def test_graph_replay_rejects_shared_a8():
+    with pytest.raises(NotImplementedError):
+        GraphReplay(lambda x: x, {}, shared_a8=True)
+
+
+def test_channel_scaled_bank_matches_eager_under_replay():
+    model, _, runtime = _install(scales=True)
+    x = torch.randn(50, 1024, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(DEV)
+    replay = GraphReplay(model, runtime.modules)
+    replay.enabled = True
+    for q in CONFIGURATIONS:
+        with precision_profile(q):
+            want = model(x)
+            for _ in range(3):
+                got = replay(x)
+                torch.cuda.synchronize()
+                assert all(torch.equal(a, b) for a, b in zip(want, got)), q
+    # the folded scale really is used: q's input is x / scale
+    scale = model.q.input_scale
+    backend = model.q.backends["w4a4"]
+    np.testing.assert_array_equal(bits(model.q(x)), _oracle_module(backend, x.cpu(), scale.cpu()))
+
+
+# ---------------------------------------------------------------- tuner and siblings
+def test_tuned_bank_is_bit_identical_to_untuned():
+    tuning.TUNINGS.clear()
+    tuned, _, _ = _install(tune=True)
+    plain, _, _ = _install(tune=False)
+    for m in (1, 8, 50, 300):
+        x = torch.randn(m, 1024, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16).to(DEV)
+        for q in CONFIGURATIONS:
+            with precision_profile(q):
+                a, b = tuned(x), plain(x)
+            assert all(torch.equal(s, t) for s, t in zip(a, b)), (m, q)
+    assert tuning.TUNINGS
+    for key, entry in tuning.TUNINGS.items():
+        assert all(c["exact"] for c in entry["candidates"]), key
+        assert _native.config_valid(entry["selected"], key[3])
+
+
+def test_tuner_refuses_untuned_signature_in_capture():
+    tuning.TUNINGS.clear()
+    backend = GroupedLinear(_linear(128, 32, False, 3), 4, 8, None).to(DEV)
+    x = torch.randn(2, 128).to(torch.bfloat16).to(DEV)
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="warmed before graph capture"):
+        with torch.cuda.graph(graph):
+            tuning.grouped_forward(backend, x)
+    torch.cuda.synchronize()
+    assert not tuning.TUNINGS
+
+
+@pytest.mark.parametrize("m", [1, 4, 9, 50])
+def test_sibling_forward_equals_separate_calls(m):
+    model, _, runtime = _install()
+    x = torch.randn(m, 1024, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16).to(DEV)
+    for q in CONFIGURATIONS:
+        with precision_profile(q):
+            runtime.before()
+            sep = [model.k(x), model.v(x), model.gate(x), model.up(x), model.q(x)]
+            sep_counts = {n: (mod.calls, mod.input_elements) for n, mod in runtime.modules.items()}
+            runtime.before()
+            kv = grouped_sibling_forward(x, [model.k, model.v])  # w8a4 + w4a4: separate launches
+            gu = grouped_sibling_forward(x, [model.gate, model.up])  # fused when (W, A) agree
+            qq = grouped_sibling_forward(x, [model.q])
+            counts = {n: (mod.calls, mod.input_elements) for n, mod in runtime.modules.items()}
+        assert all(torch.equal(a, b) for a, b in zip(sep, kv + gu + qq)), q
+        assert counts == sep_counts
