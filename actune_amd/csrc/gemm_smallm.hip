@@ -14,8 +14,10 @@
 //  * Each lane streams 16-byte weight loads (global_load_dwordx4): lanes
 //    kb = 0..3 of a row fetch 64 consecutive bytes = 8/W groups, and
 //    v_permlane32/16_swap turn them into MFMA slots without LDS.
-//  * Loads are batched: every weight, activation and scale load of DG groups
-//    is issued before the batch is consumed.
+//  * Loads are batched: every activation, scale and weight load of DG groups
+//    is issued before the batch is consumed, activations first (loads
+//    complete in issue order, so the activation work waits only for the
+//    activations). The epilogue's weight scale and bias are fetched at entry.
 //  * v_mfma_i32_16x16x64_i8 with the weight rows as the A operand and up to
 //    16 tokens per column tile (MT tiles) as the B operand; one fp32 FMA per
 //    (row, token, group).
@@ -57,11 +59,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
   constexpr bool FUSED = MODE == kModeFused;
   constexpr bool DOTS = MODE == kModeDots;
   constexpr int COLS = 16 * MT;
+  constexpr int EPT = (16 * COLS + NW * 64 - 1) / (NW * 64);  // epilogue outputs per thread
+  constexpr int XL = DT == kF32 ? 2 : 1;           // 16-byte loads per 8 elements of x
+  constexpr uint32_t ESZ = DT == kF32 ? 4 : 2;
+  constexpr int FM = 4;                            // largest M of the fused mode
   static_assert(!FUSED || (MT == 1 && DG == 8), "fused quantization serves M <= 4");
 
   __shared__ float red[DOTS ? 1 : kChunks][16][COLS + 1];
-  __shared__ __align__(16) uint8_t slab[FUSED ? NW : 1][FUSED ? DG * 4 * kGroup : 16];
-  __shared__ float sslab[FUSED ? NW : 1][FUSED ? DG * 4 : 1];
+  __shared__ __align__(16) uint8_t slab[FUSED ? NW : 1][FUSED ? DG * FM * kGroup : 16];
+  __shared__ float sslab[FUSED ? NW : 1][FUSED ? DG * FM : 1];
 
   const float fold = __builtin_ldexpf(1.0f, -T);
   const Problem pr = select_problem(args, blockIdx.x);
@@ -76,12 +82,22 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
   const uint32_t wrow = (uint32_t)(n0 + i) * wrow_bytes;
   const int slot_k = smallm_slot_k<W>(kb);
 
+  // Epilogue constants of the outputs this thread finishes, fetched first.
+  ChannelConst cc_out[DOTS ? 1 : EPT];
+  if constexpr (!DOTS) {
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int e = (int)threadIdx.x + j * NW * 64;
+      cc_out[j] = fetch_channel(pr.ws, pr.bias, args.bias_dt, N, n0 + e / COLS, e < 16 * COLS);
+    }
+  }
+
   // activation row offsets (bytes) of this lane's tokens, kOff when m >= M
   const uint32_t arow_bytes = (uint32_t)K * A / 8;
   Rsrc ares, sres, xres, xsres;
   if constexpr (FUSED) {
-    xres = make_rsrc(args.x, (uint32_t)M * K * (DT == kF32 ? 4 : 2));
-    xsres = make_rsrc(SCALE ? args.xscale : args.x, (uint32_t)K * (DT == kF32 ? 4 : 2));
+    xres = make_rsrc(args.x, (uint32_t)M * K * ESZ);
+    xsres = make_rsrc(SCALE ? args.xscale : args.x, (uint32_t)K * ESZ);
   } else {
     ares = make_rsrc(args.a, (uint32_t)M * arow_bytes);
     sres = make_rsrc(args.as, (uint32_t)M * G * 4);
@@ -105,45 +121,31 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
       for (int r = 0; r < 4; ++r) p[t][r] = 0.f;
 
     for (int g0 = gb; g0 < ge; g0 += DG) {
-      uint32_t wv[DS][4];
-#pragma unroll
-      for (int s = 0; s < DS; ++s) {
-        const int g = g0 + s * GS;
-        const uint32_t off = (uint32_t)g * 8 * W + kb * 16;
-        buffer_slot<8>(wres, row_ok && g < ge && off < wrow_bytes ? wrow + off : kOff, wv[s]);
-      }
+      // 1. Activation operands first: loads complete in issue order, so
+      //    consuming them waits only for them, not for the weights below.
+      //    Fused: lane (j = lane/8, seg = lane%8) reads elements seg*8..+7 of
+      //    group g0+j of every token m < M.
+      v4u xr[FUSED ? FM : 1][XL], dr[FUSED && SCALE ? FM : 1][XL];
       uint32_t ap[FUSED ? 1 : DG][MT][4];
       float sc[FUSED ? 1 : DG][MT];
+      const int fj = lane >> 3, seg = lane & 7;
       if constexpr (FUSED) {
-        // Quantize groups [g0, g0+8) of the M <= 4 rows: group-row idx = m*8 + j,
-        // 8 lanes per group-row, each lane 8 consecutive elements.
-        uint8_t* my_slab = slab[wave];
-        for (int base = 0; base < M * DG; base += 8) {
-          const int idx = base + (lane >> 3), seg = lane & 7;
-          const int m = idx >> 3, j = idx & 7, g = g0 + j;
-          const bool live = m < M && g < ge;
-          constexpr uint32_t esz = DT == kF32 ? 4 : 2;
-          const uint32_t k0 = (uint32_t)(g * kGroup + seg * 8);
-          float v[8];
-          buffer_load8<DT>(xres, live ? ((uint32_t)m * K + k0) * esz : kOff, v);
-          if constexpr (SCALE) {
-            float d[8];
-            buffer_load8<DT>(xsres, live ? k0 * esz : kOff, d);
+        const int g = g0 + fj;
+        const uint32_t k0 = (uint32_t)(g * kGroup + seg * 8);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = live ? round_to_dtype<DT>(v[e] / d[e]) : 0.0f;
-          }
-          int cq[8];
-          const float s = group_codes<A, DT>(v, cq);
-          if (live) {
-            store_half_slot<W, A>(my_slab + (j * 4 + m) * kGroup + (seg >> 1) * 16, seg & 1, cq);
-            if (seg == 0) sslab[wave][j * 4 + m] = s * fold;
+        for (int m = 0; m < FM; ++m) {
+          const bool live = m < M && g < ge;
+          const uint32_t xo = live ? ((uint32_t)m * K + k0) * ESZ : kOff;
+#pragma unroll
+          for (int h = 0; h < XL; ++h)
+            xr[m][h] = __builtin_amdgcn_raw_buffer_load_b128(xres, xo == kOff ? kOff : xo + 16 * h, 0, 0);
+          if constexpr (SCALE) {
+            const uint32_t so = live ? k0 * ESZ : kOff;
+#pragma unroll
+            for (int h = 0; h < XL; ++h)
+              dr[m][h] = __builtin_amdgcn_raw_buffer_load_b128(xsres, so == kOff ? kOff : so + 16 * h, 0, 0);
           }
         }
-        // LDS operations of one wave complete in order; keep the compiler from
-        // moving the slab reads above the writes.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       } else {
 #pragma unroll
         for (int j = 0; j < DG; ++j) {
@@ -157,6 +159,58 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
           }
         }
       }
+      // Keep the scheduler from hoisting weight loads above the activation
+      // loads (the point of the order above).
+      __builtin_amdgcn_sched_barrier(0);
+      // 2. Weights of the batch.
+      uint32_t wv[DS][4];
+#pragma unroll
+      for (int s = 0; s < DS; ++s) {
+        const int g = g0 + s * GS;
+        const uint32_t off = (uint32_t)g * 8 * W + kb * 16;
+        buffer_slot<8>(wres, row_ok && g < ge && off < wrow_bytes ? wrow + off : kOff, wv[s]);
+      }
+      // 3. Fused: quantize into the wave's slab (as MFMA B slots, row j*FM+m)
+      //    while the weights are in flight, then read the slots back.
+      uint32_t bq[FUSED ? DG : 1][4];
+      float bs[FUSED ? DG : 1];
+      if constexpr (FUSED) {
+        uint8_t* my_slab = slab[wave];
+        const bool glive = g0 + fj < ge;
+#pragma unroll
+        for (int m = 0; m < FM; ++m) {
+          if (m < M) {  // wave-uniform
+            float v[8];
+            unpack8<DT>(xr[m][0], xr[m][XL - 1], v);
+            if constexpr (SCALE) {
+              float d[8];
+              unpack8<DT>(dr[m][0], dr[m][XL - 1], d);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) v[e] = glive ? round_to_dtype<DT>(v[e] / d[e]) : 0.0f;
+            }
+            uint32_t cq[8];
+            const float s = group_code_bits<A, DT>(v, cq);
+            if (glive) {
+              store_half_slot<W, A>(my_slab + (fj * FM + m) * kGroup + (seg >> 1) * 16, seg & 1, cq);
+              if (seg == 0) sslab[wave][fj * FM + m] = s * fold;
+            }
+          }
+        }
+        // LDS operations of one wave complete in order; keep the compiler from
+        // moving the slab reads above the writes.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const bool ok = i < M;
+#pragma unroll
+        for (int j = 0; j < DG; ++j) {
+          v4u q = v4u{0u, 0u, 0u, 0u};
+          if (ok) q = *reinterpret_cast<const v4u*>(my_slab + (j * FM + i) * kGroup + slot_k);
+          bq[j][0] = q[0]; bq[j][1] = q[1]; bq[j][2] = q[2]; bq[j][3] = q[3];
+          bs[j] = ok ? sslab[wave][j * FM + i] : 0.0f;
+        }
+      }
+      // 4. Exchange, unpack, MFMA, rescale.
 #pragma unroll
       for (int s = 0; s < DS; ++s) {
         exchange<W>(wv[s]);
@@ -171,11 +225,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
             uint32_t bd[4];
             float scale;
             if constexpr (FUSED) {
-              const bool ok = i < M;
-              v4u q = v4u{0u, 0u, 0u, 0u};
-              if (ok) q = *reinterpret_cast<const v4u*>(slab[wave] + (j * 4 + i) * kGroup + slot_k);
-              bd[0] = q[0]; bd[1] = q[1]; bd[2] = q[2]; bd[3] = q[3];
-              scale = ok ? sslab[wave][j * 4 + i] : 0.0f;
+              bd[0] = bq[j][0]; bd[1] = bq[j][1]; bd[2] = bq[j][2]; bd[3] = bq[j][3];
+              scale = bs[j];
             } else {
               unpack_slot<A>(ap[j][t], bd);
               reorder_slot<A, W>(bd);
@@ -206,13 +257,16 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
   }
   if constexpr (DOTS) return;
   __syncthreads();
-  for (int e = threadIdx.x; e < 16 * COLS; e += NW * 64) {
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = (int)threadIdx.x + j * NW * 64;
+    if (e >= 16 * COLS) break;
     const int nl = e / COLS, m = e % COLS, n = n0 + nl;
     float acc = red[0][nl][m];
 #pragma unroll
     for (int c = 1; c < kChunks; ++c) acc = acc + red[c][nl][m];
     if (n < N && m < M) {
-      const float y = finish(acc, pr.ws[n], pr.bias, args.bias_dt, n);
+      const float y = finish_const(acc, cc_out[j], pr.bias != nullptr, args.bias_dt);
       const long o = (long)m * N + n;
       if (args.out_dt == kBF16) store_out<kBF16>(pr.out, o, y);
       else if (args.out_dt == kF16) store_out<kF16>(pr.out, o, y);

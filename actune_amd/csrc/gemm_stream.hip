@@ -38,7 +38,8 @@ __device__ __forceinline__ void tile_problem(const LinearArgs& args, int tile, c
 
 // LDS layout (dynamic): per wave a slab [GW][ROWS][64 B] of B slots and a
 // scale slab [GW][ROWS] (fp32, already multiplied by 2^-(sW+sA)), one 64-byte
-// zero row, and the chunk-partial array red[16][16][17].
+// zero row, and the chunk-partial arrays red[2][16][16][17] (one per parity of
+// the workgroup's tile counter, so one barrier per tile suffices).
 template <int W, int A, int NW, int MODE, int DT, bool SCALE>
 __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, int GW, int ROWS) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -59,7 +60,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
   uint8_t* slab = smem + (size_t)wave * GW * ROWS * kGroup;
   float* sslab = reinterpret_cast<float*>(smem + (size_t)NW * GW * ROWS * kGroup) + (size_t)wave * GW * ROWS;
   uint8_t* zero_row = reinterpret_cast<uint8_t*>(sslab - (size_t)wave * GW * ROWS + (size_t)NW * GW * ROWS);
-  float (*red)[16][17] = reinterpret_cast<float (*)[16][17]>(zero_row + kGroup);
+  float (*red2)[kChunks][16][17] = reinterpret_cast<float (*)[kChunks][16][17]>(zero_row + kGroup);
 
   // ---------------------------------------------------------------- stage
   // Two phases so that activation (L2) and weight (HBM) latencies overlap:
@@ -126,8 +127,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = live ? round_to_dtype<DT>(v[e] / d[e]) : 0.0f;
       }
-      int cq[8];
-      const float s = group_codes<A, DT>(v, cq);
+      uint32_t cq[8];
+      const float s = group_code_bits<A, DT>(v, cq);
       if (live) {
         store_half_slot<W, A>(slab + (gl * ROWS + m) * kGroup + (seg >> 1) * 16, seg & 1, cq);
         if (seg == 0) sslab[gl * ROWS + m] = s * fold;
@@ -147,6 +148,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
 #pragma unroll
   for (int p = 0; p < kPass; ++p)
     if (p < npass) issue(p, early[p]);
+  // Every wave's activation loads enter the CU's memory queue before any
+  // weight load: vector memory requests of a CU are served in issue order, so
+  // without this barrier the activations of late waves would wait behind the
+  // weight streams of early ones.
+  __syncthreads();
 
   // ---------------------------------------------------------------- stream
   const int slot_k = smallm_slot_k<W>(kb);
@@ -156,7 +162,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
   const int items = my_tiles * nb;
   const uint32_t wrow_bytes = (uint32_t)K * W / 8;
 
-  auto load_item = [&](int q, uint32_t (&buf)[DSB][4]) {
+  // Each item load also fetches the epilogue constants of its tile for the
+  // thread that finishes channel threadIdx.x / 16 (threads < 256), so the
+  // per-tile epilogue never waits on a fresh memory round trip.
+  auto load_item = [&](int q, uint32_t (&buf)[DSB][4], ChannelConst& cc) {
     const int tile = (int)blockIdx.x + (q / nb) * (int)gridDim.x;
     const int gs = wg0 + (q % nb) * GB;
     const uint8_t* w; const float* ws; const void* bias; void* out; int N, tile0;
@@ -170,10 +179,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
       const bool ok = n < N && g < wg1 && off < wrow_bytes;
       buffer_slot<8>(wres, ok ? (uint32_t)n * wrow_bytes + off : kOff, buf[s]);
     }
+    cc = fetch_channel(ws, bias, args.bias_dt, N, (tile - tile0) * 16 + ((int)threadIdx.x >> 4), threadIdx.x < 256);
   };
 
   uint32_t cur[DSB][4], nxt[DSB][4];
-  if (items > 0) load_item(0, cur);
+  ChannelConst cur_cc{0.0f, 0u}, nxt_cc{0.0f, 0u};
+  if (items > 0) load_item(0, cur, cur_cc);
 #pragma unroll
   for (int p = 0; p < kPass; ++p)
     if (p < npass) convert(p, early[p]);
@@ -185,11 +196,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
   __syncthreads();  // slabs and the zero row are visible to their readers
 
   float p[4] = {0.f, 0.f, 0.f, 0.f};
+  int par = 0;                                // parity of the workgroup's current tile
   int c = c_first;                            // chunk being accumulated
   int cend = chunk_begin(c + 1, G);
   for (int q = 0; q < items; ++q) {
     const bool more = q + 1 < items;
-    if (more) load_item(q + 1, nxt);
+    if (more) load_item(q + 1, nxt, nxt_cc);
     const int b = q % nb;
     const int gs = wg0 + b * GB;
 #pragma unroll
@@ -201,7 +213,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
         if (gg >= wg1) break;
         while (gg >= cend) {  // close finished (possibly empty) chunks
 #pragma unroll
-          for (int r = 0; r < 4; ++r) { red[c][4 * kb + r][i] = p[r]; p[r] = 0.f; }
+          for (int r = 0; r < 4; ++r) { red2[par][c][4 * kb + r][i] = p[r]; p[r] = 0.f; }
           ++c;
           cend = chunk_begin(c + 1, G);
         }
@@ -221,7 +233,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
       // end of this tile for the wave: close its remaining chunks, reduce
       for (; c < c_first + CPW; ++c) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) { red[c][4 * kb + r][i] = p[r]; p[r] = 0.f; }
+        for (int r = 0; r < 4; ++r) { red2[par][c][4 * kb + r][i] = p[r]; p[r] = 0.f; }
       }
       c = c_first;
       cend = chunk_begin(c + 1, G);
@@ -231,24 +243,28 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
         const uint8_t* w; const float* ws; const void* bias; void* out; int N, tile0;
         tile_problem(args, tile, w, ws, bias, out, N, tile0);
         const int nl = threadIdx.x >> 4, m = threadIdx.x & 15, n = (tile - tile0) * 16 + nl;
-        float acc = red[0][nl][m];
+        float acc = red2[par][0][nl][m];
 #pragma unroll
-        for (int cc = 1; cc < kChunks; ++cc) acc = acc + red[cc][nl][m];
+        for (int cc = 1; cc < kChunks; ++cc) acc = acc + red2[par][cc][nl][m];
         if (n < N && m < M) {
-          const float y = finish(acc, ws[n], bias, args.bias_dt, n);
+          const float y = finish_const(acc, cur_cc, bias != nullptr, args.bias_dt);
           const long o = (long)m * N + n;
           if (args.out_dt == kBF16) store_out<kBF16>(out, o, y);
           else if (args.out_dt == kF16) store_out<kF16>(out, o, y);
           else store_out<kF32>(out, o, y);
         }
       }
-      __syncthreads();
+      // No second barrier: the next tile writes red2[par ^ 1], and the one
+      // after it writes red2[par] only after the next tile's barrier, which
+      // the epilogue threads reach after finishing this epilogue.
+      par ^= 1;
     }
     if (more) {
 #pragma unroll
       for (int s = 0; s < DSB; ++s)
 #pragma unroll
         for (int e = 0; e < 4; ++e) cur[s][e] = nxt[s][e];
+      cur_cc = nxt_cc;
     }
   }
 }
@@ -268,7 +284,7 @@ static int max_wave_groups(int G, int nw) {
 size_t stream_lds_bytes(int K, int M, int nw) {
   const int G = K / kGroup, rows = (M + 3) & ~3;
   const size_t gw = (size_t)max_wave_groups(G, nw);
-  return (size_t)nw * gw * rows * (kGroup + 4) + kGroup + sizeof(float) * kChunks * 16 * 17;
+  return (size_t)nw * gw * rows * (kGroup + 4) + kGroup + 2 * sizeof(float) * kChunks * 16 * 17;
 }
 
 template <typename Kern>

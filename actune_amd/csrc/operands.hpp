@@ -40,6 +40,36 @@ __device__ __forceinline__ float buffer_f32(Rsrc r, uint32_t off) {
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
+// Epilogue constants of one output channel, fetched early so that their
+// latency hides under the weight stream: the weight scale and the raw bits
+// of the bias element (fp32 bits, or the 16-bit payload for bf16/f16). The
+// conversion waits until the value is used, so nothing stalls on the load.
+struct ChannelConst {
+  float ws;
+  uint32_t bias_bits;
+};
+
+__device__ __forceinline__ ChannelConst fetch_channel(const float* ws, const void* bias, int bias_dt, int N,
+                                                      int n, bool live) {
+  const Rsrc wr = make_rsrc(ws, (uint32_t)N * 4u);
+  const Rsrc br = make_rsrc(bias, bias ? (uint32_t)N * (bias_dt == kF32 ? 4u : 2u) : 0u);
+  live = live && n < N;
+  ChannelConst c;
+  c.ws = buffer_f32(wr, live ? (uint32_t)n * 4u : kOff);
+  if (bias_dt == kF32) c.bias_bits = __builtin_amdgcn_raw_buffer_load_b32(br, live ? (uint32_t)n * 4u : kOff, 0, 0);
+  else c.bias_bits = __builtin_amdgcn_raw_buffer_load_b16(br, live ? (uint32_t)n * 2u : kOff, 0, 0);
+  return c;
+}
+
+// y = fmaf(acc, ws, bias) with a bias, acc * ws without one (same as finish()).
+__device__ __forceinline__ float finish_const(float acc, ChannelConst c, bool has_bias, int bias_dt) {
+  if (!has_bias) return acc * c.ws;
+  const float b = bias_dt == kF32 ? __uint_as_float(c.bias_bits)
+                : bias_dt == kBF16 ? bf16_to_f32((uint16_t)c.bias_bits)
+                                   : f16_to_f32((uint16_t)c.bias_bits);
+  return __builtin_fmaf(acc, c.ws, b);
+}
+
 // Eight consecutive elements of dtype DT at byte offset off as fp32 (zeros
 // when off is out of range).
 template <int DT>
@@ -113,23 +143,40 @@ __device__ __forceinline__ void load8(const void* p, long i, float v[8]) {
   }
 }
 
+// Maximum of non-negative floats over an aligned 8-lane segment, in every
+// lane of the segment: DPP moves (quad xor 1, quad xor 2, then the mirror
+// inside each 8-lane half row) and integer max on the bit patterns, which
+// orders non-negative floats like their values; no LDS round trip. All 64
+// lanes must execute it.
+__device__ __forceinline__ float seg8_max(float a) {
+  uint32_t u = __float_as_uint(a);
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0xB1, 0xF, 0xF, false));   // [1,0,3,2]
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x4E, 0xF, 0xF, false));   // [2,3,0,1]
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x141, 0xF, 0xF, false));  // half-row mirror
+  return __uint_as_float(u);
+}
+
+// 1.5 * 2^23: adding it to a float q with |q| <= 2^22 rounds q to the nearest
+// integer (ties to even, the default rounding mode), and the low byte of the
+// sum's bit pattern is then that integer in two's complement.
+constexpr float kRoundMagic = 12582912.0f;
+
 // Group-64 codes of 8 elements held by one lane of an 8-lane segment group:
-// amax over the group (xor-shuffles inside the 8 lanes), s = fl(max(amax,
-// 1e-8) / P) and c = clamp(rint(fl(v / s)), -P-1, P). For 16-bit inputs the
-// quotient is x * y with y = fl(1/s) plus one FMA correction (Markstein),
-// which gives the IEEE codes for every bf16 and f16 input (proved
-// exhaustively by tests/exhaustive_division.c); fp32 inputs use the IEEE
-// division itself. All 64 lanes of the wave must call this together.
+// amax over the group, s = fl(max(amax, 1e-8) / P) and c = clamp(rint(fl(v /
+// s)), -P-1, P). For 16-bit inputs the quotient is x * y with y = fl(1/s)
+// plus one FMA correction (Markstein), which gives the IEEE codes for every
+// bf16 and f16 input (proved exhaustively by tests/exhaustive_division.c);
+// fp32 inputs use the IEEE division itself. The quotient is clamped first
+// (the bounds are integers, so clamp and round commute) and rounded by the
+// magic add; cb[e] holds the sum's bits, whose low byte is code e. All 64
+// lanes of the wave must call this together.
 template <int A, int DT>
-__device__ __forceinline__ float group_codes(const float v[8], int c[8]) {
+__device__ __forceinline__ float group_code_bits(const float v[8], uint32_t cb[8]) {
   constexpr int P = (1 << (A - 1)) - 1;
   float amax = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
-  amax = fmaxf(amax, 1e-8f);
+  amax = fmaxf(seg8_max(amax), 1e-8f);
   const float s = amax / (float)P;
   const float y = 1.0f / s;
 #pragma unroll
@@ -142,9 +189,19 @@ __device__ __forceinline__ float group_codes(const float v[8], int c[8]) {
       const float r = __builtin_fmaf(-q0, s, v[e]);
       q = __builtin_fmaf(r, y, q0);
     }
-    q = fminf(fmaxf(__builtin_rintf(q), (float)(-P - 1)), (float)P);
-    c[e] = (int)q;
+    q = fminf(fmaxf(q, (float)(-P - 1)), (float)P);
+    cb[e] = __float_as_uint(q + kRoundMagic);
   }
+  return s;
+}
+
+// Same codes as integers.
+template <int A, int DT>
+__device__ __forceinline__ float group_codes(const float v[8], int c[8]) {
+  uint32_t cb[8];
+  const float s = group_code_bits<A, DT>(v, cb);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) c[e] = (int)(int8_t)(cb[e] & 0xffu);
   return s;
 }
 
@@ -192,27 +249,39 @@ __device__ __forceinline__ void act_slot(const uint8_t* arow, bool ok, int koff,
   reorder_slot<A, W>(d);
 }
 
-__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
-         ((uint32_t)(d & 0xff) << 24);
+// Low bytes of code bits (group_code_bits) a, b, c, d as one dword
+// [a, b, c, d], with v_perm_b32.
+__device__ __forceinline__ uint32_t code_quad(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const uint32_t lo = perm_b32(b, a, 0x0C0C0400u);  // [a, b, 0, 0]
+  const uint32_t hi = perm_b32(d, c, 0x0C0C0400u);  // [c, d, 0, 0]
+  return perm_b32(hi, lo, 0x05040100u);
 }
 
-// Store 8 consecutive codes (elements 8h..8h+7 of a 16-element slot, shifted
-// to the top of their byte for width A) into the slot at `slot` in the
-// element order of weight width W (common.hpp, unpack_slot).
+// Shift every byte of d left by 8-A inside the byte (the code field moves to
+// the top of its byte: c * 2^(8-A) as int8).
+template <int A>
+__device__ __forceinline__ uint32_t shift_bytes(uint32_t d) {
+  if constexpr (A == 8) return d;
+  else if constexpr (A == 4) return (d << 4) & 0xF0F0F0F0u;
+  else return (d << 6) & 0xC0C0C0C0u;
+}
+
+// Store 8 consecutive codes (elements 8h..8h+7 of a 16-element slot, as
+// code bits from group_code_bits) into the slot at `slot`, shifted to the top
+// of their byte for width A, in the element order of weight width W
+// (common.hpp, unpack_slot).
 template <int W, int A>
-__device__ __forceinline__ void store_half_slot(uint8_t* slot, int h, const int c[8]) {
-  int b[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) b[e] = c[e] * (1 << shift_of(A));
+__device__ __forceinline__ void store_half_slot(uint8_t* slot, int h, const uint32_t cb[8]) {
   if constexpr (W == 8) {
-    *reinterpret_cast<v2u*>(slot + 8 * h) = v2u{pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7])};
+    *reinterpret_cast<v2u*>(slot + 8 * h) =
+        v2u{shift_bytes<A>(code_quad(cb[0], cb[1], cb[2], cb[3])), shift_bytes<A>(code_quad(cb[4], cb[5], cb[6], cb[7]))};
   } else if constexpr (W == 4) {
-    *reinterpret_cast<v2u*>(slot + 8 * h) = v2u{pack4(b[0], b[2], b[4], b[6]), pack4(b[1], b[3], b[5], b[7])};
+    *reinterpret_cast<v2u*>(slot + 8 * h) =
+        v2u{shift_bytes<A>(code_quad(cb[0], cb[2], cb[4], cb[6])), shift_bytes<A>(code_quad(cb[1], cb[3], cb[5], cb[7]))};
   } else {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      *reinterpret_cast<uint16_t*>(slot + 4 * r + 2 * h) = (uint16_t)((b[r] & 0xff) | ((b[4 + r] & 0xff) << 8));
+      *reinterpret_cast<uint16_t*>(slot + 4 * r + 2 * h) = (uint16_t)shift_bytes<A>(perm_b32(cb[4 + r], cb[r], 0x0C0C0400u));
   }
 }
 

@@ -11,8 +11,8 @@
 // Layout: groups are 64 contiguous elements, and the M*K/64 groups of the
 // row-major input are contiguous too. Each lane owns 8 consecutive elements
 // (one 16-byte load for 16-bit inputs), 8 lanes own a group, a wave covers 8
-// groups (1 KiB of bf16), and the group absmax is a 3-step xor-shuffle
-// reduction inside the 8-lane segment. Stores are contiguous per wave:
+// groups (1 KiB of bf16), and the group absmax is a 3-step DPP reduction
+// inside the 8-lane segment. Stores are contiguous per wave:
 // A8 writes 8 B/lane, A4 4 B/lane, A2 2 B/lane.
 #include "common.hpp"
 #include "launch.hpp"
