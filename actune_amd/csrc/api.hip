@@ -13,12 +13,14 @@ using namespace actune;
 
 namespace {
 
-constexpr int kNumConfigs = 10;
+constexpr int kNumConfigs = 14;
 constexpr int kSmallMConfigs = 3;  // ids 0..2: small-M kernel, M <= kSmallMMax
 constexpr int kSmallMMax = 64;
 constexpr int kTiledConfigs = 4;   // ids 3..6: MFMA-tiled kernel, any M
 constexpr int kStreamFirst = kSmallMConfigs + kTiledConfigs;  // ids 7..9: streaming kernel, M <= 16
 constexpr int kStreamMax = 16;
+constexpr int kStreamConfigs = 3;
+constexpr int kPrefillFirst = kStreamFirst + kStreamConfigs;  // ids 10..13: prefill kernel, any M
 constexpr int kFusedMaxM = 4;      // small-M calls up to this M quantize inside the GEMM
 constexpr int kSmallMWaves[kSmallMConfigs] = {4, 8, 16};
 thread_local char g_err[512];
@@ -62,7 +64,8 @@ int check_shape(int64_t M, int64_t K, int W, int A, int out_dt, int bias_dt, int
   if (!dtype_ok(out_dt) || !dtype_ok(bias_dt)) return fail(ACTUNE_ERR_INVALID, "unsupported output/bias dtype");
   if (config < 0 || config >= kNumConfigs) return fail(ACTUNE_ERR_INVALID, "invalid configuration");
   if (config < kSmallMConfigs && M > kSmallMMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
-  if (config >= kStreamFirst && M > kStreamMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 16");
+  if (config >= kStreamFirst && config < kPrefillFirst && M > kStreamMax)
+    return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 16");
   return ACTUNE_OK;
 }
 
@@ -92,6 +95,16 @@ int add_problem(LinearArgs& g, const uint8_t* w, const float* ws, const void* bi
 // streaming config whose LDS staging would not fit (or the dots mode) runs
 // the small-M kernel with the same wave count; results are identical.
 void run_gemm(int W, int A, int config, int mode, const LinearArgs& g, hipStream_t st) {
+  if (config >= kPrefillFirst) {
+    for (int p = 0; p < g.nprob; ++p) {
+      LinearArgs one = g;
+      one.prob[0] = g.prob[p];
+      one.prob[0].tile0 = 0;
+      one.nprob = 1;
+      launch_prefill(W, A, config - kPrefillFirst, mode == kModeDots, one, st);
+    }
+    return;
+  }
   if (config >= kStreamFirst) {
     const int nw = kSmallMWaves[config - kStreamFirst];
     if (mode != kModeDots && stream_lds_bytes(g.K, g.M, nw) <= kStreamLdsMax) {
@@ -135,7 +148,7 @@ int actune_num_configs(void) { return kNumConfigs; }
 int actune_config_valid(int config, int64_t M) {
   if (config < 0 || config >= kNumConfigs) return 0;
   if (config < kSmallMConfigs) return M <= kSmallMMax;
-  if (config >= kStreamFirst) return M <= kStreamMax;
+  if (config >= kStreamFirst && config < kPrefillFirst) return M <= kStreamMax;
   return 1;
 }
 
@@ -150,7 +163,14 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
   if (M <= kFusedMaxM) return tiles >= 768 ? kStreamFirst + 1 : 2;
   if (M <= kStreamMax) return tiles >= 512 ? kStreamFirst + 1 : kStreamFirst + 2;
   if (M <= kSmallMMax) return 1;
-  return M <= 128 ? 3 : 4;
+  // Prefill (measured on C3/C4 shapes): the prefill kernel with 64x64 tiles
+  // when there are at least two tiles per CU, 64x32 tiles below that (more
+  // workgroups for small problems), and the LDS-staged tiled kernel for the
+  // largest problems, whose 4-wave 64x64 tiles share weight fragments in LDS.
+  const int64_t t64 = ((N + 63) / 64) * ((M + 63) / 64);
+  if (t64 < 512) return kPrefillFirst + 3;
+  if (t64 < 2048) return kPrefillFirst + 2;
+  return kSmallMConfigs;
 }
 
 int actune_quantize_groups(const void* x, int x_dtype, const void* input_scale, int64_t M, int64_t K,
@@ -204,7 +224,7 @@ int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_s
   // The quantizer is fused into the GEMM for M <= 4 on the small-M and
   // streaming kernels (for larger M its per-workgroup cost is no longer
   // hidden under the weight loads; measured on MI355X).
-  const bool fused = M <= kFusedMaxM && (config < kSmallMConfigs || config >= kStreamFirst);
+  const bool fused = M <= kFusedMaxM && (config < kSmallMConfigs || (config >= kStreamFirst && config < kPrefillFirst));
   if (fused) {
     g.x = x;
     g.xscale = input_scale;

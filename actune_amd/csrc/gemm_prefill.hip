@@ -1,0 +1,377 @@
+// Prefill packed group-64 GEMM for gfx950 (M > 64): int8 MFMA with the
+// per-group fp32 rescale, organised around the VALU budget.
+//
+// Restates actune/kernels/grouped.py:74-94 / grouped_native.cu:42-88 with the
+// canonical chunked fp32 order (common.hpp), bit-identical to every other
+// kernel of the library.
+//
+// Cost model. Each 16x16x64 int8 MFMA (16 cycles of the matrix pipe) needs 4
+// v_cvt_f32_i32 + 4 v_fma_f32 per lane for the per-group rescale (32 cycles
+// of the vector pipe): the vector pipe is the bottleneck and any other VALU
+// work comes straight out of MFMA throughput. The layout below keeps the
+// remaining VALU work near one instruction per MFMA:
+//  * A workgroup is 4 waves, one per SIMD. Wave w owns TN 16-row weight tiles
+//    (rows n_blk + 16*TN*w ...) and all TM 16-token tiles of the workgroup, so
+//    the workgroup tile is (64*TN) x (16*TM).
+//  * Weights bypass LDS: each wave streams its own rows straight into MFMA
+//    A-operand registers (lane (i, kb) loads 16 bytes of row i; the lanes of a
+//    row fetch 64 consecutive bytes), swaps halves across lanes with
+//    v_permlane32/16_swap and unpacks sub-byte codes in registers; every
+//    unpacked slot feeds TM MFMAs.
+//  * Activations are staged once per workgroup per quad (4 groups) into LDS
+//    as 16-byte MFMA B slots, unpacked and reordered to the weight width's
+//    element order, with their group scales (2^-(sW+sA) folded in). LDS is
+//    double-buffered: one barrier per quad.
+//  * The MFMAs of group g are issued in the same block as the rescale of
+//    group g-1, so the matrix and vector pipes of a SIMD run side by side.
+//  * Weight loads run DW = 4 quads ahead in a register ring, activation loads
+//    DA = 2 quads ahead of their LDS store: the rows a workgroup streams are
+//    fetched together by the workgroups of its XCD that share them, so each
+//    load sees HBM latency and needs thousands of cycles of lead.
+//  * Tiles are ordered so that the workgroups of one XCD (workgroup ids are
+//    dealt to the 8 XCDs round-robin) cover a contiguous range of weight row
+//    blocks with all of their token blocks: each XCD's L2 holds the rows it
+//    re-reads.
+#include "common.hpp"
+#include "launch.hpp"
+#include "operands.hpp"
+
+namespace actune {
+
+constexpr int kXcds = 8;
+
+// LDS byte offset of B slot `slot` of token row `row` of group `gl` in a
+// [4][rows][4 x 16 B] slot array, XOR-swizzled so that the 16 rows read by one
+// ds_read_b128 spread over the banks.
+__device__ __forceinline__ int pf_slot_addr(int gl, int row, int rows, int slot) {
+  return ((gl * rows + row) * 4 + (slot ^ ((row >> 1) & 3))) * 16;
+}
+
+template <int W, int A, int TN, int TM, bool DOTS>
+__global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int tiles_m) {
+  constexpr int T = shift_of(W) + shift_of(A);
+  constexpr int BN = 64 * TN, BM = 16 * TM;
+  constexpr int KG = 4;                       // groups per stage (one quad)
+  constexpr int GS = 8 / W;                   // groups per 16-byte weight load per lane
+  constexpr int WST = KG / GS;                // weight load steps per quad
+  constexpr int AROW = KG * 8 * A;            // packed activation bytes per token per quad
+  constexpr int ACH = BM * AROW / 16;         // 16-byte activation chunks per quad
+  constexpr int APT = (ACH + 255) / 256;      // per thread
+  constexpr int SPT = (BM * KG + 255) / 256;  // activation scales per thread per quad
+  constexpr int ABYTES = KG * BM * 64, SBYTES = BM * KG * 4;
+  static_assert(KG % GS == 0, "a weight load never straddles a quad");
+  constexpr int DW = 4, DA = 2, UQ = 4;       // ring depths (quads) and quad unroll
+  static_assert(UQ % DW == 0 && UQ % DA == 0 && UQ % 2 == 0, "static ring indices");
+
+  __shared__ __align__(16) uint8_t alds[2][ABYTES + SBYTES];
+  __shared__ float wsl[DOTS ? 1 : BN], bsl[DOTS ? 1 : BN];
+
+  const float fold = __builtin_ldexpf(1.0f, -T);
+  const int M = args.M, K = args.K, N = args.prob[0].N, G = K / kGroup;
+  const int Qn = (G + KG - 1) / KG;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i = lane & 15, kb = lane >> 4;
+
+  // XCD-aware tile order: XCD x = id % 8 takes tiles [x*per + min(x, rem), ...)
+  // in n-major order (consecutive tiles share a weight row block).
+  const int ntiles = (int)gridDim.x, id = (int)blockIdx.x;
+  const int xcd = id % kXcds, per = ntiles / kXcds, rem = ntiles % kXcds;
+  const int tile = xcd * per + (xcd < rem ? xcd : rem) + id / kXcds;
+  const int n_blk = (tile / tiles_m) * BN, m_blk = (tile % tiles_m) * BM;
+  const int n_wave = n_blk + wave * 16 * TN;
+
+  const uint32_t wrow_bytes = (uint32_t)K * W / 8, arow_bytes = (uint32_t)K * A / 8;
+  const Rsrc wres = make_rsrc(args.prob[0].w, (uint32_t)N * wrow_bytes);
+  const Rsrc ares = make_rsrc(args.a, (uint32_t)M * arow_bytes);
+  const Rsrc sres = make_rsrc(args.as, DOTS ? 4u : (uint32_t)M * G * 4);
+  const int slot_b = smallm_slot_k<W>(kb) >> 4;  // B slot matching this lane's weight slot
+
+  // epilogue constants of the workgroup's rows, through LDS
+  if constexpr (!DOTS) {
+    for (int t = tid; t < BN; t += 256) {
+      const ChannelConst cc = fetch_channel(args.prob[0].ws, args.prob[0].bias, args.bias_dt, N, n_blk + t, true);
+      wsl[t] = cc.ws;
+      bsl[t] = bias_from_bits(cc.bias_bits, args.bias_dt);
+    }
+  }
+
+  // ---------------------------------------------------------------- operand movers
+  // Register rings: the weight loads of quad v sit in wring[v % DW] (issued DW
+  // quads ahead), the activation chunks of quad v in araw[v % DA] (issued DA
+  // quads ahead of their LDS store). The quad loop is unrolled by UQ so every
+  // ring index is a constant.
+  uint32_t wring[DW][WST][TN][4];
+  uint32_t araw[DA][APT][4];
+  float sraw[DA][SPT];
+
+  auto load_weights = [&](int q, int st, uint32_t (&buf)[TN][4]) {
+    const uint32_t off = (uint32_t)(q * KG + st * GS) * 8 * W + kb * 16;
+#pragma unroll
+    for (int x = 0; x < TN; ++x) {
+      const int n = n_wave + x * 16 + i;
+      const bool ok = n < N && off < wrow_bytes;
+      buffer_slot<8>(wres, ok ? (uint32_t)n * wrow_bytes + off : kOff, buf[x]);
+    }
+  };
+  auto load_acts = [&](int q, int rs) {  // quad q into ring slot rs
+#pragma unroll
+    for (int t = 0; t < APT; ++t) {
+      const int ch = tid + t * 256, row = ch / (AROW / 16), cc = ch % (AROW / 16);
+      const int m = m_blk + row;
+      const uint32_t off = (uint32_t)q * AROW + cc * 16;
+      const bool ok = ch < ACH && m < M && off < arow_bytes;
+      buffer_slot<8>(ares, ok ? (uint32_t)m * arow_bytes + off : kOff, araw[rs][t]);
+    }
+    if constexpr (!DOTS) {
+#pragma unroll
+      for (int t = 0; t < SPT; ++t) {
+        const int e = tid + t * 256, row = e / KG, gl = e % KG;
+        const int m = m_blk + row, g = q * KG + gl;
+        const bool ok = e < BM * KG && m < M && g < G;
+        sraw[rs][t] = buffer_f32(sres, ok ? ((uint32_t)m * G + g) * 4u : kOff);
+      }
+    }
+  };
+  auto store_acts = [&](uint8_t* buf, int rs) {  // ring slot rs into LDS buffer buf
+    float* sl = reinterpret_cast<float*>(buf + ABYTES);
+#pragma unroll
+    for (int t = 0; t < APT; ++t) {
+      const int ch = tid + t * 256;
+      if (ch >= ACH) break;
+      const int row = ch / (AROW / 16), cc = ch % (AROW / 16);
+      constexpr int SPC = 8 / A;  // slots per 16-byte chunk
+#pragma unroll
+      for (int u = 0; u < SPC; ++u) {
+        const int slot_all = cc * SPC + u, gl = slot_all / 4, slot = slot_all % 4;
+        uint32_t d[4];
+        unpack_slot<A>(&araw[rs][t][u * A / 2], d);
+        reorder_slot<A, W>(d);
+        *reinterpret_cast<v4u*>(buf + pf_slot_addr(gl, row, BM, slot)) = v4u{d[0], d[1], d[2], d[3]};
+      }
+    }
+    if constexpr (!DOTS) {
+#pragma unroll
+      for (int t = 0; t < SPT; ++t) {
+        const int e = tid + t * 256;
+        if (e < BM * KG) sl[e] = sraw[rs][t] * fold;  // [token][group of the quad]
+      }
+    }
+  };
+
+  // ---------------------------------------------------------------- accumulators
+  float acc[TN][TM][4], p[TN][TM][4];
+#pragma unroll
+  for (int x = 0; x < TN; ++x)
+#pragma unroll
+    for (int y = 0; y < TM; ++y)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[x][y][r] = p[x][y][r] = 0.f;
+  // MFMA results of group g live in D[g & 1] until the block of group g+1
+  // rescales them (no register copies: quads have an even number of groups,
+  // so the parity of g is that of its index in the quad). D[1] starts at zero,
+  // so the rescale in the block of group 0 adds fma(0, 0, +0) = +0.
+  v4i D[2][TN][TM];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int x = 0; x < TN; ++x)
+#pragma unroll
+      for (int y = 0; y < TM; ++y) D[b][x][y] = v4i{0, 0, 0, 0};
+  float scl[TM];  // token scales of the last group of the previous quad
+#pragma unroll
+  for (int y = 0; y < TM; ++y) scl[y] = 0.0f;
+  int c = 0, cend = chunk_begin(1, G);  // chunk being accumulated, and its end
+  // p += D[par] * scale for group gq (dots mode: store the dots of gq instead)
+  auto rescale = [&](int par, const float (&sc)[TM], int gq) {
+#pragma unroll
+    for (int x = 0; x < TN; ++x)
+#pragma unroll
+      for (int y = 0; y < TM; ++y) {
+        if constexpr (DOTS) {
+          if (gq < 0 || gq >= G) continue;
+          const int m = m_blk + y * 16 + i;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int n = n_wave + x * 16 + 4 * kb + r;
+            if (n < N && m < M) args.dots[((long)m * N + n) * G + gq] = D[par][x][y][r] >> T;
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) p[x][y][r] = __builtin_fmaf((float)D[par][x][y][r], sc[y], p[x][y][r]);
+        }
+      }
+  };
+  // acc += p in chunk order (acc starts at +0 and p is never -0, so closing an
+  // empty chunk adds +0 and changes nothing)
+  auto close_chunk = [&]() {
+#pragma unroll
+    for (int x = 0; x < TN; ++x)
+#pragma unroll
+      for (int y = 0; y < TM; ++y)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) { acc[x][y][r] = acc[x][y][r] + p[x][y][r]; p[x][y][r] = 0.f; }
+    ++c;
+    cend = chunk_begin(c + 1, G);
+  };
+
+  // ---------------------------------------------------------------- prologue
+#pragma unroll
+  for (int v = 0; v < DA; ++v) load_acts(v, v);
+#pragma unroll
+  for (int v = 0; v < DW; ++v)
+#pragma unroll
+    for (int st = 0; st < WST; ++st) load_weights(v, st, wring[v][st]);
+  store_acts(alds[0], 0);
+  load_acts(DA, 0);
+  __syncthreads();
+
+  // ---------------------------------------------------------------- main loop
+  // Branch-free per group: groups past G (the tail of the last quad) read
+  // zero weights, activations and scales through out-of-range buffer offsets,
+  // so their MFMAs give 0 and their rescale fma(0, 0, p) leaves p unchanged;
+  // loads past the last quad are switched off the same way.
+  for (int q0 = 0; q0 < Qn; q0 += UQ) {
+#pragma unroll
+  for (int u = 0; u < UQ; ++u) {
+    const int q = q0 + u;
+    if (q < Qn) {  // uniform: false only in the last pass
+    const int ws_slot = u % DW, as_next = (u + 1) % DA;
+    const uint8_t* buf = alds[u & 1];
+    const float* sl = reinterpret_cast<const float*>(buf + ABYTES);
+    float sq[TM][KG];
+    if constexpr (!DOTS) {
+#pragma unroll
+      for (int y = 0; y < TM; ++y) {
+        const v4u s4 = *reinterpret_cast<const v4u*>(sl + (y * 16 + i) * KG);
+#pragma unroll
+        for (int gl = 0; gl < KG; ++gl) sq[y][gl] = __uint_as_float(s4[gl]);
+      }
+    }
+    // B fragments of the current group and (read one block ahead) the next
+    uint32_t bf[2][TM][4];
+    auto read_b = [&](int gl, uint32_t (&dst)[TM][4]) {
+#pragma unroll
+      for (int y = 0; y < TM; ++y) {
+        const v4u b = *reinterpret_cast<const v4u*>(buf + pf_slot_addr(gl, y * 16 + i, BM, slot_b));
+        dst[y][0] = b[0]; dst[y][1] = b[1]; dst[y][2] = b[2]; dst[y][3] = b[3];
+      }
+    };
+    read_b(0, bf[0]);
+#pragma unroll
+    for (int gl = 0; gl < KG; ++gl) {
+      const int g = q * KG + gl;
+      const int st = gl / GS, jj = gl % GS;
+      if (jj == 0) {
+#pragma unroll
+        for (int x = 0; x < TN; ++x) exchange<W>(wring[ws_slot][st][x]);
+      }
+      uint32_t wd[TN][4];
+#pragma unroll
+      for (int x = 0; x < TN; ++x) unpack_slot<W>(&wring[ws_slot][st][x][jj * W / 2], wd[x]);
+      if (jj == GS - 1) load_weights(q + DW, st, wring[ws_slot][st]);
+      if (gl + 1 < KG) read_b(gl + 1, bf[(gl + 1) & 1]);
+#pragma unroll
+      for (int x = 0; x < TN; ++x)
+#pragma unroll
+        for (int y = 0; y < TM; ++y) D[gl & 1][x][y] = mfma16x16x64(wd[x], bf[gl & 1][y], v4i{0, 0, 0, 0});
+      {
+        float sp[TM];  // scales of group g-1
+#pragma unroll
+        for (int y = 0; y < TM; ++y) sp[y] = gl > 0 ? sq[y][gl > 0 ? gl - 1 : 0] : scl[y];
+        rescale((gl + 1) & 1, sp, g - 1);
+      }
+      if constexpr (!DOTS) {
+        // one MFMA of group g, then 8 VALU of the rescale of group g-1
+#pragma unroll
+        for (int k = 0; k < TN * TM; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+        }
+        if (gl == 0) {
+          while (g >= cend) close_chunk();  // chunks that end before group g
+        }
+      }
+      if constexpr (!DOTS) {
+        // Keep the rescale of group g-1 in this block: without a use here the
+        // compiler sinks it to the end of the quad, away from the MFMAs it is
+        // meant to overlap.
+#pragma unroll
+        for (int x = 0; x < TN; ++x)
+#pragma unroll
+          for (int y = 0; y < TM; ++y)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) asm volatile("" ::"v"(p[x][y][r]));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (!DOTS) {
+#pragma unroll
+      for (int y = 0; y < TM; ++y) scl[y] = sq[y][KG - 1];
+    }
+    store_acts(alds[(u + 1) & 1], as_next);
+    load_acts(q + 1 + DA, as_next);
+    __syncthreads();
+    }
+  }
+  }
+  rescale((KG - 1) & 1, scl, Qn * KG - 1);  // the last group
+  if constexpr (DOTS) return;
+  while (c < kChunks) close_chunk();
+
+  // ---------------------------------------------------------------- epilogue
+  const bool has_bias = args.prob[0].bias != nullptr;
+#pragma unroll
+  for (int x = 0; x < TN; ++x) {
+    const int nl = wave * 16 * TN + x * 16 + 4 * kb;  // first of this lane's 4 rows in the tile
+#pragma unroll
+    for (int y = 0; y < TM; ++y) {
+      const int m = m_blk + y * 16 + i;
+      if (m >= M) continue;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float a = acc[x][y][r];
+        v[r] = has_bias ? __builtin_fmaf(a, wsl[nl + r], bsl[nl + r]) : a * wsl[nl + r];
+      }
+      const int n0 = n_blk + nl;
+      const long o = (long)m * N + n0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (n0 + r >= N) break;
+        if (args.out_dt == kBF16) store_out<kBF16>(args.prob[0].out, o + r, v[r]);
+        else if (args.out_dt == kF16) store_out<kF16>(args.prob[0].out, o + r, v[r]);
+        else store_out<kF32>(args.prob[0].out, o + r, v[r]);
+      }
+    }
+  }
+}
+
+// Shapes (TN, TM): 0 = (2, 4) 128x64, 1 = (2, 2) 128x32, 2 = (1, 4) 64x64, 3 = (1, 2) 64x32.
+template <int W, int A, bool DOTS>
+static void launch_prefill_shape(int shape, const LinearArgs& g, hipStream_t st) {
+#define PREFILL(TN, TM)                                                                       \
+  do {                                                                                        \
+    const int tn = (g.prob[0].N + 64 * TN - 1) / (64 * TN), tm = (g.M + 16 * TM - 1) / (16 * TM); \
+    gemm_prefill<W, A, TN, TM, DOTS><<<dim3((unsigned)(tn * tm)), 256, 0, st>>>(g, tm);        \
+  } while (0)
+  switch (shape) {
+    case 0: PREFILL(2, 4); break;
+    case 1: PREFILL(2, 2); break;
+    case 2: PREFILL(1, 4); break;
+    default: PREFILL(1, 2); break;
+  }
+#undef PREFILL
+}
+
+void launch_prefill(int W, int A, int shape, bool dots, const LinearArgs& g, hipStream_t st) {
+#define CASE(WB, AB)                                                                \
+  if (W == WB && A == AB) {                                                         \
+    if (dots) launch_prefill_shape<WB, AB, true>(shape, g, st);                     \
+    else launch_prefill_shape<WB, AB, false>(shape, g, st);                         \
+    return;                                                                         \
+  }
+  CASE(8, 8) CASE(8, 4) CASE(8, 2) CASE(4, 8) CASE(4, 4) CASE(4, 2) CASE(2, 8) CASE(2, 4) CASE(2, 2)
+#undef CASE
+}
+
+}  // namespace actune

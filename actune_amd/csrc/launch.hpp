@@ -41,6 +41,7 @@ void launch_quantize(const void* x, int dt, const void* sc, long M, long K, int 
 void launch_smallm(int W, int A, int nw, int mode, const LinearArgs& g, hipStream_t st);
 void launch_tiled(int W, int A, int shape, bool dots, const LinearArgs& g, hipStream_t st);
 void launch_stream(int W, int A, int nw, int mode, const LinearArgs& g, hipStream_t st);
+void launch_prefill(int W, int A, int shape, bool dots, const LinearArgs& g, hipStream_t st);
 size_t stream_lds_bytes(int K, int M, int nw);
 
 }  // namespace actune

@@ -61,13 +61,17 @@ __device__ __forceinline__ ChannelConst fetch_channel(const float* ws, const voi
   return c;
 }
 
+// The bias value held by raw bias bits of dtype bias_dt.
+__device__ __forceinline__ float bias_from_bits(uint32_t bits, int bias_dt) {
+  return bias_dt == kF32 ? __uint_as_float(bits)
+       : bias_dt == kBF16 ? bf16_to_f32((uint16_t)bits)
+                          : f16_to_f32((uint16_t)bits);
+}
+
 // y = fmaf(acc, ws, bias) with a bias, acc * ws without one (same as finish()).
 __device__ __forceinline__ float finish_const(float acc, ChannelConst c, bool has_bias, int bias_dt) {
   if (!has_bias) return acc * c.ws;
-  const float b = bias_dt == kF32 ? __uint_as_float(c.bias_bits)
-                : bias_dt == kBF16 ? bf16_to_f32((uint16_t)c.bias_bits)
-                                   : f16_to_f32((uint16_t)c.bias_bits);
-  return __builtin_fmaf(acc, c.ws, b);
+  return __builtin_fmaf(acc, c.ws, bias_from_bits(c.bias_bits, bias_dt));
 }
 
 // Eight consecutive elements of dtype DT at byte offset off as fp32 (zeros

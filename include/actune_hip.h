@@ -113,6 +113,8 @@ int actune_grouped_dots_i32(const uint8_t* a, const uint8_t* w, int64_t M, int64
  *   0, 1, 2  small-M split-K kernel with 4, 8, 16 waves (M <= 64)
  *   3 .. 6   MFMA-tiled kernel shapes (any M)
  *   7, 8, 9  persistent streaming kernel with 4, 8, 16 waves (M <= 16)
+ *   10 .. 13 prefill kernel (weights streamed per wave, activations staged
+ *            per workgroup) with tiles 128x64, 128x32, 64x64, 64x32 (any M)
  * actune_config_valid: 1 if `config` can run a call with M rows.
  * actune_default_config: the config ACTUNE_CONFIG_AUTO resolves to.
  */

@@ -36,9 +36,10 @@ def test_version_and_layout_selftest():
 
 def test_config_table():
     n = _native.num_configs()
-    assert n == 10
+    assert n == 14
     assert _native.config_valid(0, 64) and not _native.config_valid(0, 65)
     assert all(_native.config_valid(c, 4096) for c in range(3, 7))
+    assert all(_native.config_valid(c, 1) and _native.config_valid(c, 4096) for c in range(10, 14))
     assert _native.config_valid(9, 16) and not _native.config_valid(9, 17)
     assert not _native.config_valid(n, 1) and not _native.config_valid(-2, 1)
     for m in (1, 8, 16, 17, 50, 512):
