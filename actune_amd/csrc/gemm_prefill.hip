@@ -60,7 +60,8 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
   constexpr int SPT = (BM * KG + 255) / 256;  // activation scales per thread per quad
   constexpr int ABYTES = KG * BM * 64, SBYTES = BM * KG * 4;
   static_assert(KG % GS == 0, "a weight load never straddles a quad");
-  constexpr int DW = 4, DA = 2, UQ = 4;       // ring depths (quads) and quad unroll
+  // ring depths (quads; W8 moves twice the bytes per quad) and quad unroll
+  constexpr int DW = W == 8 ? 2 : 4, DA = 2, UQ = 4;
   static_assert(UQ % DW == 0 && UQ % DA == 0 && UQ % 2 == 0, "static ring indices");
 
   __shared__ __align__(16) uint8_t alds[2][ABYTES + SBYTES];
@@ -104,24 +105,32 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
   uint32_t araw[DA][APT][4];
   float sraw[DA][SPT];
 
-  auto load_weights = [&](int q, int st, uint32_t (&buf)[TN][4]) {
-    const uint32_t off = (uint32_t)(q * KG + st * GS) * 8 * W + kb * 16;
+  // Load offsets = a per-lane base (kOff for rows/tokens past the end, so the
+  // sum stays out of range) + a uniform per-quad offset. Bytes past the end
+  // of K (tail quad, prefetch past the last quad) read the following row, or
+  // zeros past the buffer; their groups have activation scale 0, so they add
+  // fma(d, 0, p) = p exactly (and the dots mode skips them).
+  uint32_t wbase[TN];
 #pragma unroll
-    for (int x = 0; x < TN; ++x) {
-      const int n = n_wave + x * 16 + i;
-      const bool ok = n < N && off < wrow_bytes;
-      buffer_slot<8>(wres, ok ? (uint32_t)n * wrow_bytes + off : kOff, buf[x]);
-    }
+  for (int x = 0; x < TN; ++x) {
+    const int n = n_wave + x * 16 + i;
+    wbase[x] = n < N ? (uint32_t)n * wrow_bytes + kb * 16 : kOff;
+  }
+  auto load_weights = [&](int q, int st, uint32_t (&buf)[TN][4]) {
+    const uint32_t off = (uint32_t)(q * KG + st * GS) * 8 * W;
+#pragma unroll
+    for (int x = 0; x < TN; ++x) buffer_slot<8>(wres, wbase[x] + off, buf[x]);
   };
+  uint32_t abase[APT];
+#pragma unroll
+  for (int t = 0; t < APT; ++t) {
+    const int ch = tid + t * 256, row = ch / (AROW / 16), cc = ch % (AROW / 16);
+    const int m = m_blk + row;
+    abase[t] = ch < ACH && m < M ? (uint32_t)m * arow_bytes + cc * 16 : kOff;
+  }
   auto load_acts = [&](int q, int rs) {  // quad q into ring slot rs
 #pragma unroll
-    for (int t = 0; t < APT; ++t) {
-      const int ch = tid + t * 256, row = ch / (AROW / 16), cc = ch % (AROW / 16);
-      const int m = m_blk + row;
-      const uint32_t off = (uint32_t)q * AROW + cc * 16;
-      const bool ok = ch < ACH && m < M && off < arow_bytes;
-      buffer_slot<8>(ares, ok ? (uint32_t)m * arow_bytes + off : kOff, araw[rs][t]);
-    }
+    for (int t = 0; t < APT; ++t) buffer_slot<8>(ares, abase[t] + (uint32_t)q * AROW, araw[rs][t]);
     if constexpr (!DOTS) {
 #pragma unroll
       for (int t = 0; t < SPT; ++t) {
@@ -226,10 +235,8 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
   __syncthreads();
 
   // ---------------------------------------------------------------- main loop
-  // Branch-free per group: groups past G (the tail of the last quad) read
-  // zero weights, activations and scales through out-of-range buffer offsets,
-  // so their MFMAs give 0 and their rescale fma(0, 0, p) leaves p unchanged;
-  // loads past the last quad are switched off the same way.
+  // Branch-free per group: groups past G (the tail of the last quad) have
+  // activation scale 0, so their rescale fma(d, 0, p) leaves p unchanged.
   for (int q0 = 0; q0 < Qn; q0 += UQ) {
 #pragma unroll
   for (int u = 0; u < UQ; ++u) {
