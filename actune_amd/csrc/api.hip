@@ -155,12 +155,12 @@ int actune_config_valid(int config, int64_t M) {
 int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
   (void)W; (void)A;
   // Measured on MI355X (W4A8, Llama/Gemma shapes): the one-tile-per-CU
-  // small-M kernel with 16 waves is fastest for decode shapes of up to ~768
+  // small-M kernel with 16 waves is fastest for decode shapes of up to ~512
   // row tiles; beyond that, and for M > 4, the persistent streaming kernel
   // with 8 waves wins (it keeps the next tile's weights in flight and
   // quantizes once per workgroup).
   const int64_t tiles = (N + 15) / 16;
-  if (M <= kFusedMaxM) return tiles >= 768 ? kStreamFirst + 1 : 2;
+  if (M <= kFusedMaxM) return tiles >= 512 ? kStreamFirst + 1 : 2;
   if (M <= kStreamMax) return tiles >= 512 ? kStreamFirst + 1 : kStreamFirst + 2;
   if (M <= kSmallMMax) return 1;
   // Prefill (measured on C3/C4 shapes): the prefill kernel with 64x64 tiles

@@ -24,7 +24,13 @@ Printed JSON line: the driver's contract fields plus
                 rocprofv3 PMC summary (profiles/), if present;
   cpu_baseline  the reference's dequantize-then-matmul path in torch-CPU
                 (oracle/cpu_path.py) on a bounded sample (rank 0, N=1);
-  detail        per-linear schedule, M=8, per-shape us/launch.
+  detail        per-linear schedule, M=8, per-shape us/launch, and the other
+                BASELINE configurations: C3 (the same stack's shapes at
+                prefill M=512 for all nine W/A pairs, with the MFMA roofline
+                of the prefill kernel), C4 (Gemma-2B shapes at M=256 and M=1,
+                W4A4) and C5 (a Gemma-300M-shaped action expert bank, 10
+                denoise steps over a 50-token chunk with per-call
+                q00/q01/q11/q10 switching under graph replay).
 """
 from __future__ import annotations
 
@@ -35,6 +41,9 @@ import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
+PAIRS = [(w, a) for w in (8, 4, 2) for a in (8, 4, 2)]
+GEMMA_SHAPES = [("q", 2048, 2048), ("kv", 256, 2048), ("gate_up", 16384, 2048), ("down", 2048, 16384)]
 SHAPES = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
           ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
 METRIC = "µs per packed linear + achieved int8 TOPS / HBM GB/s vs roofline, per W/A config"
@@ -50,10 +59,12 @@ def parse():
     p.add_argument("--A", type=int, default=8)
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extra", action="store_true", help="skip the C3/C4/C5 detail sections")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 1 GiB device copy (for PMC byte-counter calibration)")
     p.add_argument("--only", choices=sorted(ONLY_SHAPES),
                    help="only launch one shape 24 times over distinct weights (for rocprofv3 counter runs)")
+    p.add_argument("--config", type=int, default=-1, help="kernel config for --only (default: automatic)")
     return p.parse_args()
 
 
@@ -65,8 +76,9 @@ ONLY_SHAPES = {
 }
 
 
-def run_only(torch, _native, name, W, A):
+def run_only(torch, _native, name, W, A, config):
     m, spec, cfg = ONLY_SHAPES[name]
+    cfg = config if config >= 0 else cfg
     k = spec[0][1]
     g = torch.Generator(device="cuda").manual_seed(0)
     x = torch.randn(m, k, device="cuda").to(torch.bfloat16)
@@ -81,7 +93,8 @@ def run_only(torch, _native, name, W, A):
         else:
             _native.grouped_forward_multi(x, t, W, A, config=cfg)
     torch.cuda.synchronize()
-    print(json.dumps(dict(only=name, M=m, targets=spec, launches=len(sets))))
+    print(json.dumps(dict(only=name, M=m, targets=spec, launches=len(sets),
+                          config=cfg if cfg >= 0 else _native.default_config(m, spec[0][0], k, W, A))))
 
 
 def build_stack(torch, m, layers, W, A, seed=0):
@@ -212,6 +225,148 @@ def load_traffic(m):
         return None
 
 
+def time_launches(torch, fn, steps, warmup):
+    """Microseconds per call of fn (captured once in a hipGraph)."""
+    graph = capture(torch, fn)
+    ms = time_graph(torch, graph, steps, warmup)
+    del graph
+    return ms * 1e3
+
+
+def packed_set(torch, n, k, W, copies, g):
+    return [(torch.randint(0, 256, (n, k * W // 8), generator=g, device="cuda", dtype=torch.uint8),
+             torch.rand(n, generator=g, device="cuda") * 0.01 + 0.005) for _ in range(copies)]
+
+
+def bench_prefill(torch, _native, steps, warmup):
+    """C3: the stack's three distinct shapes at M=512, all nine W/A pairs;
+    default kernel config (the prefill kernel), packed activations given."""
+    g = torch.Generator(device="cuda").manual_seed(3)
+    m, out = 512, {}
+    for W, A in PAIRS:
+        row = {}
+        for name, n, k in (SHAPES[0], SHAPES[4], SHAPES[6]):
+            x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
+            a, s = _native.quantize_groups(x, A)
+            ws = packed_set(torch, n, k, W, 4, g)
+            y = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+
+            def fn(ws=ws, a=a, s=s, x=x, y=y):
+                for w, sc in ws:
+                    _native.grouped_linear(a, s, w, sc, None, x, W, A, out=y)
+
+            us = time_launches(torch, fn, steps, warmup) / len(ws)
+            tops = 2 * m * n * k / us / 1e6
+            row[f"{n}x{k}"] = dict(us=round(us, 2), TOPS=round(tops, 1), frac=round(tops / INT8_PEAK_TOPS, 4),
+                                   config=_native.default_config(m, n, k, W, A))
+            del ws
+        out[f"W{W}A{A}"] = row
+    best = {pair: max(v["frac"] for v in out[pair].values()) for pair in ("W8A8", "W4A8")}
+    out["roofline"] = {"bound": "mfma", "unit": "TOPS", "peak": INT8_PEAK_TOPS,
+                       "kernel": "gemm_prefill (int8 MFMA + per-group fp32 rescale)",
+                       "W4A8_frac_best_shape": best["W4A8"], "W8A8_frac_best_shape": best["W8A8"],
+                       "note": "2 VALU per (token, channel, group) against 64 MACs caps int8 MFMA use at 50%"}
+    return out
+
+
+def bench_gemma(torch, _native, steps, warmup):
+    """C4: Gemma-2B-shaped linears at M=256 and M=1, W4A4 (default configs)."""
+    g = torch.Generator(device="cuda").manual_seed(4)
+    W, A, out = 4, 4, {}
+    for m in (256, 1):
+        row = {}
+        for name, n, k in GEMMA_SHAPES:
+            x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
+            ws = packed_set(torch, n, k, W, 8 if m == 1 else 4, g)
+            y = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+            a = torch.empty(m, k * A // 8, device="cuda", dtype=torch.uint8)
+            s = torch.empty(m, k // 64, device="cuda", dtype=torch.float32)
+
+            def fn(ws=ws, x=x, y=y, a=a, s=s):
+                for w, sc in ws:
+                    _native.grouped_forward(x, w, sc, None, W, A, out=y, packed=a, scales=s)
+
+            us = time_launches(torch, fn, steps, warmup) / len(ws)
+            row[name] = dict(N=n, K=k, us=round(us, 2), TOPS=round(2 * m * n * k / us / 1e6, 2),
+                             weight_GBps=round(n * k * W / 8 / us / 1e3, 1),
+                             config=_native.default_config(m, n, k, W, A))
+            del ws
+        out[f"M={m}"] = row
+    return out
+
+
+EXPERT = {"q": (1024, 1024), "k": (256, 1024), "v": (256, 1024), "o": (1024, 1024),
+          "gate": (4096, 1024), "up": (4096, 1024), "down": (1024, 4096)}
+
+
+def bench_expert(torch, steps):
+    """C5: a Gemma-300M-shaped action expert (width 1024, MLP 1024->4096->1024)
+    installed with install_bank as a W4A4 shared bank whose two binary
+    switchable matrices (gate, up) realise q00/q01/q11/q10, plus fixed W8A4
+    (k) and W2A4 (o) layers, so W2/W4/W8 versions are all resident in HBM.
+    One denoise step runs the block on a 50-token chunk; 10 steps follow a
+    seeded q00/q01/q11/q10 schedule, each step a GraphReplay replay of the
+    active configuration's graph."""
+    from actune_amd.graph import GraphReplay
+    from actune_amd.layers import install_bank
+    from actune_amd.precision import CONFIGURATIONS, SharedBank, precision_profile
+    torch.manual_seed(5)
+
+    class Expert(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            for name, (n, k) in EXPERT.items():
+                setattr(self, name, torch.nn.Linear(k, n, bias=False, dtype=torch.bfloat16, device="cuda"))
+
+        def forward(self, x):
+            q, kk, vv = self.q(x), self.k(x), self.v(x)
+            h = x + self.o(q * 0.5)
+            return h + self.down(torch.nn.functional.silu(self.gate(x)) * self.up(x)), kk, vv
+
+    fixed = {"q": "w4a4", "k": "w8a4", "v": "w4a4", "o": "w2a4", "down": "w4a4"}
+    switch = {"q00": ("w4a4", "w4a4"), "q01": ("w4a4", "w4a2"), "q11": ("w2a4", "w4a2"), "q10": ("w2a4", "w4a4")}
+    configs = {q: dict(fixed, gate=gm, up=um) for q, (gm, um) in switch.items()}
+    modes = [f"w{w}a{a}" for w in (2, 4, 8) for a in (2, 4, 8)]
+    sizes = {name: {md: n * k * int(md[1]) // 8 + 4 * n for md in modes} for name, (n, k) in EXPERT.items()}
+    bank = SharedBank(configurations=configs, shapes={n: list(s) for n, s in EXPERT.items()},
+                      activation_elements={n: 50 * s[1] for n, s in EXPERT.items()},
+                      shape_groups=[["q", "k", "v", "gate", "up"], ["o"], ["down"]],
+                      version_bytes=sizes, budget="w4a4", storage_limit=1 << 30)
+    model = Expert()
+    clips = {n: {md: None for md in {c[n] for c in configs.values()}} for n in EXPERT}
+    runtime = install_bank(model, bank, clips)
+    replay = GraphReplay(model, runtime.modules)
+    replay.enabled = True
+    rng = torch.Generator().manual_seed(1234)
+    schedule = [CONFIGURATIONS[int(i)] for i in torch.randint(0, 4, (10,), generator=rng)]
+    x0 = torch.randn(50, 1024, device="cuda").to(torch.bfloat16)
+
+    def denoise():
+        x = x0
+        for q in schedule:
+            with precision_profile(q):
+                h, _, _ = replay(x)
+            x = (x.float() + 0.1 * h.float()).to(torch.bfloat16)
+        return x
+
+    for _ in range(3):
+        denoise()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        denoise()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    resident = sum(sum(b.packed_weight.numel() + 4 * b.weight_scale.numel() for b in m.backends.values())
+                   for m in runtime.modules.values())
+    return dict(schedule=schedule, ms_per_10_steps=round(ms, 4), us_per_denoise_step=round(ms * 100, 2),
+                graphs=len(replay.graphs), replays=replay.replays, resident_bank_bytes=resident,
+                note="per denoise step: 7 group-64 linears at M=50 (+ the block's elementwise ops) in one "
+                     "hipGraph replay of the active configuration; the eager update between steps is included")
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -233,7 +388,7 @@ def main():
         print(json.dumps(dict(copy_bytes=1 << 30, launches=5)))
         return 0
     if args.only:
-        run_only(torch, _native, args.only, args.W, args.A)
+        run_only(torch, _native, args.only, args.W, args.A, args.config)
         return 0
 
     W, A = args.W, args.A
@@ -307,6 +462,10 @@ def main():
                            "weight_GBps": round(r["wbytes"] / (r["ms_lin"] * 1e-3) / 1e9, 1)},
             "per_shape": r["per_shape"],
         }
+    if not args.no_extra:
+        line["detail"]["C3_prefill_M512"] = bench_prefill(torch, _native, 10, 3)
+        line["detail"]["C4_gemma_W4A4"] = bench_gemma(torch, _native, 20, 5)
+        line["detail"]["C5_expert_switching"] = bench_expert(torch, 20)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, W, A)
     print(json.dumps(line), flush=True)
