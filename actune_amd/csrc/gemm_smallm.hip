@@ -9,8 +9,9 @@
 // Structure:
 //  * One workgroup owns 16 output channels of one problem (a problem is one
 //    linear; up to kMaxProblems linears that share the same input run in one
-//    launch) over all of K, and NW waves split K along the 16 canonical
-//    chunks (split-K inside the workgroup, no global scratch).
+//    launch) and one block of 16*MT tokens (blockIdx.y) over all of K, and NW
+//    waves split K along the 16 canonical chunks (split-K inside the
+//    workgroup, no global scratch).
 //  * Each lane streams 16-byte weight loads (global_load_dwordx4): lanes
 //    kb = 0..3 of a row fetch 64 consecutive bytes = 8/W groups, and
 //    v_permlane32/16_swap turn them into MFMA slots without LDS.
@@ -76,6 +77,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
   const int i = lane & 15, kb = lane >> 4;
   const int G = K / kGroup;
   const int n0 = ((int)blockIdx.x - pr.tile0) * 16;
+  const int m_base = (int)blockIdx.y * COLS;  // first token of this workgroup's token block
   const uint32_t wrow_bytes = (uint32_t)K * W / 8;
   const bool row_ok = n0 + i < N;
   const Rsrc wres = make_rsrc(pr.w, (uint32_t)N * wrow_bytes);
@@ -106,7 +108,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
   bool aok[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
-    const int m = 16 * t + i;
+    const int m = m_base + 16 * t + i;
     aok[t] = m < M;
     arow[t] = (uint32_t)m;
   }
@@ -234,7 +236,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
             }
             const v4i D = mfma16x16x64(wd, bd, v4i{0, 0, 0, 0});
             if constexpr (DOTS) {
-              const int m = 16 * t + i;
+              const int m = m_base + 16 * t + i;
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
                 const int n = n0 + 4 * kb + r;
@@ -261,10 +263,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
   for (int j = 0; j < EPT; ++j) {
     const int e = (int)threadIdx.x + j * NW * 64;
     if (e >= 16 * COLS) break;
-    const int nl = e / COLS, m = e % COLS, n = n0 + nl;
-    float acc = red[0][nl][m];
+    const int nl = e / COLS, mc = e % COLS, n = n0 + nl, m = m_base + mc;
+    float acc = red[0][nl][mc];
 #pragma unroll
-    for (int c = 1; c < kChunks; ++c) acc = acc + red[c][nl][m];
+    for (int c = 1; c < kChunks; ++c) acc = acc + red[c][nl][mc];
     if (n < N && m < M) {
       const float y = finish_const(acc, cc_out[j], pr.bias != nullptr, args.bias_dt);
       const long o = (long)m * N + n;
@@ -278,7 +280,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
 // ---------------------------------------------------------------------------
 template <int W, int A, int NW, int MT>
 static void launch_nw_mt(int mode, const LinearArgs& g, hipStream_t st) {
-  const dim3 grid((unsigned)g.tiles), block(NW * 64);
+  const dim3 grid((unsigned)g.tiles, (unsigned)((g.M + 16 * MT - 1) / (16 * MT))), block(NW * 64);
   if (mode == kModeDots) {
     gemm_smallm<W, A, NW, MT, kModeDots, kBF16, false><<<grid, block, 0, st>>>(g);
   } else if (mode == kModePacked) {
@@ -294,9 +296,13 @@ static void launch_nw_mt(int mode, const LinearArgs& g, hipStream_t st) {
   }
 }
 
+// Few row tiles: one 16-token block per workgroup, over a second grid
+// dimension, so that the workgroups cover the GPU (the weight rows are then
+// re-read per token block, from L2). Many row tiles: all tokens in one
+// workgroup, so each weight row is read once.
 template <int W, int A, int NW>
 static void launch_nw(int mode, const LinearArgs& g, hipStream_t st) {
-  if (g.M <= 16) launch_nw_mt<W, A, NW, 1>(mode, g, st);
+  if (g.M <= 16 || g.tiles < 512) launch_nw_mt<W, A, NW, 1>(mode, g, st);
   else if (g.M <= 32) launch_nw_mt<W, A, NW, 2>(mode, g, st);
   else launch_nw_mt<W, A, NW, 4>(mode, g, st);
 }
