@@ -13,7 +13,7 @@ using namespace actune;
 
 namespace {
 
-constexpr int kNumConfigs = 14;
+constexpr int kNumConfigs = 17;
 constexpr int kSmallMConfigs = 3;  // ids 0..2: small-M kernel, M <= kSmallMMax
 constexpr int kSmallMMax = 64;
 constexpr int kTiledConfigs = 4;   // ids 3..6: MFMA-tiled kernel, any M
@@ -21,6 +21,8 @@ constexpr int kStreamFirst = kSmallMConfigs + kTiledConfigs;  // ids 7..9: strea
 constexpr int kStreamMax = 16;
 constexpr int kStreamConfigs = 3;
 constexpr int kPrefillFirst = kStreamFirst + kStreamConfigs;  // ids 10..13: prefill kernel, any M
+constexpr int kPrefillConfigs = 4;
+constexpr int kDecodeFirst = kPrefillFirst + kPrefillConfigs;  // ids 14..16: decode kernel, M <= 4
 constexpr int kFusedMaxM = 4;      // small-M calls up to this M quantize inside the GEMM
 constexpr int kSmallMWaves[kSmallMConfigs] = {4, 8, 16};
 thread_local char g_err[512];
@@ -66,6 +68,7 @@ int check_shape(int64_t M, int64_t K, int W, int A, int out_dt, int bias_dt, int
   if (config < kSmallMConfigs && M > kSmallMMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
   if (config >= kStreamFirst && config < kPrefillFirst && M > kStreamMax)
     return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 16");
+  if (config >= kDecodeFirst && M > kFusedMaxM) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 4");
   return ACTUNE_OK;
 }
 
@@ -79,8 +82,14 @@ int check_target(const uint8_t* w, const float* ws, const void* out, int64_t N, 
   return ACTUNE_OK;
 }
 
-int resolve(int config, int64_t M, int64_t N, int64_t K, int W, int A) {
-  return config == ACTUNE_CONFIG_AUTO ? actune_default_config(M, N, K, W, A) : config;
+int packed_default(int64_t M, int64_t N, int64_t K, int W, int A);
+
+// ACTUNE_CONFIG_AUTO: calls that hand over x (and may fuse the quantizer) use
+// actune_default_config; calls on packed activations use packed_default,
+// which never picks a decode config (those need x).
+int resolve(int config, int64_t M, int64_t N, int64_t K, int W, int A, bool has_x) {
+  if (config != ACTUNE_CONFIG_AUTO) return config;
+  return has_x ? actune_default_config(M, N, K, W, A) : packed_default(M, N, K, W, A);
 }
 
 // Fill the problem table of a launch; returns the number of 16-row tiles.
@@ -95,6 +104,17 @@ int add_problem(LinearArgs& g, const uint8_t* w, const float* ws, const void* bi
 // streaming config whose LDS staging would not fit (or the dots mode) runs
 // the small-M kernel with the same wave count; results are identical.
 void run_gemm(int W, int A, int config, int mode, const LinearArgs& g, hipStream_t st) {
+  if (config >= kDecodeFirst) {
+    // the decode kernel serves the fused mode; packed activations and the
+    // dots mode run the small-M kernel with the same wave count
+    const int nw = kSmallMWaves[config - kDecodeFirst];
+    if (mode == kModeFused && decode_fits(g.K, g.M, W, nw)) {
+      launch_decode(W, A, nw, g, st);
+      return;
+    }
+    launch_smallm(W, A, nw, mode, g, st);
+    return;
+  }
   if (config >= kPrefillFirst) {
     for (int p = 0; p < g.nprob; ++p) {
       LinearArgs one = g;
@@ -149,11 +169,29 @@ int actune_config_valid(int config, int64_t M) {
   if (config < 0 || config >= kNumConfigs) return 0;
   if (config < kSmallMConfigs) return M <= kSmallMMax;
   if (config >= kStreamFirst && config < kPrefillFirst) return M <= kStreamMax;
+  if (config >= kDecodeFirst) return M <= kFusedMaxM;
   return 1;
 }
 
 int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
-  (void)W; (void)A;
+  // Fused decode (M <= 4, measured on MI355X at W4A8 Llama/Gemma shapes):
+  // the decode kernel beats the small-M and streaming kernels wherever a
+  // wave's K-range fits its load ring. Fewer waves per tile cost less
+  // per-workgroup work, so take the smallest wave count that still gives
+  // every SIMD a wave (tiles x waves >= 1024) and fits K.
+  if (M >= 1 && M <= kFusedMaxM) {
+    const int64_t tiles = (N + 15) / 16;
+    for (int c = 0; c < 3; ++c) {
+      const int nw = kSmallMWaves[c];
+      if ((tiles * nw >= 1024 || nw == kSmallMWaves[2]) && decode_fits((int)K, (int)M, W, nw)) return kDecodeFirst + c;
+    }
+  }
+  return packed_default(M, N, K, W, A);
+}
+
+namespace {
+int packed_default(int64_t M, int64_t N, int64_t K, int W, int A) {
+  (void)K; (void)W; (void)A;
   // Measured on MI355X (W4A8, Llama/Gemma shapes): the one-tile-per-CU
   // small-M kernel with 16 waves is fastest for decode shapes of up to ~512
   // row tiles; beyond that, and for M > 4, the persistent streaming kernel
@@ -172,6 +210,7 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
   if (t64 < 2048) return kPrefillFirst + 2;
   return kSmallMConfigs;
 }
+}  // namespace
 
 int actune_quantize_groups(const void* x, int x_dtype, const void* input_scale, int64_t M, int64_t K,
                            int A, uint8_t* packed, float* scales, void* stream) {
@@ -187,7 +226,7 @@ int actune_grouped_linear(const uint8_t* a, const float* a_scales, const uint8_t
                           int out_dtype, int64_t M, int64_t N, int64_t K, int W, int A, int config,
                           void* stream) {
   g_err[0] = 0;
-  config = resolve(config, M, N, K, W, A);
+  config = resolve(config, M, N, K, W, A, false);
   int rc = check_shape(M, K, W, A, out_dtype, bias_dtype, config);
   if (!rc) rc = check_target(w, w_scale, out, N, M, K, W);
   if (rc || M == 0) return rc;
@@ -210,7 +249,7 @@ int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_s
     return fail(ACTUNE_ERR_INVALID, "between 1 and 4 targets required");
   int64_t n_total = 0;
   for (int t = 0; t < ntargets; ++t) n_total += targets[t].N;
-  config = resolve(config, M, n_total, K, W, A);
+  config = resolve(config, M, n_total, K, W, A, true);
   int rc = check_shape(M, K, W, A, x_dtype, bias_dtype, config);
   if (!rc) rc = check_quantize(x, x_dtype, input_scale, M, K, A, a_buf, scale_buf);
   for (int t = 0; t < ntargets && !rc; ++t)
@@ -224,7 +263,8 @@ int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_s
   // The quantizer is fused into the GEMM for M <= 4 on the small-M and
   // streaming kernels (for larger M its per-workgroup cost is no longer
   // hidden under the weight loads; measured on MI355X).
-  const bool fused = M <= kFusedMaxM && (config < kSmallMConfigs || (config >= kStreamFirst && config < kPrefillFirst));
+  const bool fused = M <= kFusedMaxM &&
+                     (config < kSmallMConfigs || (config >= kStreamFirst && config < kPrefillFirst) || config >= kDecodeFirst);
   if (fused) {
     g.x = x;
     g.xscale = input_scale;
@@ -251,7 +291,7 @@ int actune_grouped_forward(const void* x, int x_dtype, const void* input_scale, 
 int actune_grouped_dots_i32(const uint8_t* a, const uint8_t* w, int64_t M, int64_t N, int64_t K,
                             int W, int A, int config, int32_t* dots, void* stream) {
   g_err[0] = 0;
-  config = resolve(config, M, N, K, W, A);
+  config = resolve(config, M, N, K, W, A, false);
   int rc = check_shape(M, K, W, A, kF32, kF32, config);
   if (!rc && (N <= 0 || N > INT_MAX / 2)) rc = fail(ACTUNE_ERR_INVALID, "invalid dimensions");
   if (!rc && N * K * W / 8 >= kMaxBufferBytes) rc = fail(ACTUNE_ERR_INVALID, "operand too large (each buffer must stay below 2 GiB)");

@@ -15,6 +15,7 @@ namespace actune {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 enum Dtype { kBF16 = 0, kF16 = 1, kF32 = 2 };

@@ -34,22 +34,6 @@
 
 namespace actune {
 
-// The problem owning row tile `tile`, selected field by field with constant
-// indices so the by-value kernel arguments stay in scalar kernarg loads.
-__device__ __forceinline__ Problem select_problem(const LinearArgs& args, int tile) {
-  Problem pr;
-  pr.w = args.prob[0].w; pr.ws = args.prob[0].ws; pr.bias = args.prob[0].bias;
-  pr.out = args.prob[0].out; pr.N = args.prob[0].N; pr.tile0 = args.prob[0].tile0;
-#pragma unroll
-  for (int q = 1; q < kMaxProblems; ++q) {
-    if (q < args.nprob && tile >= args.prob[q].tile0) {
-      pr.w = args.prob[q].w; pr.ws = args.prob[q].ws; pr.bias = args.prob[q].bias;
-      pr.out = args.prob[q].out; pr.N = args.prob[q].N; pr.tile0 = args.prob[q].tile0;
-    }
-  }
-  return pr;
-}
-
 template <int W, int A, int NW, int MT, int MODE, int DT, bool SCALE>
 __global__ __launch_bounds__(NW * 64) void gemm_smallm(const LinearArgs args) {
   constexpr int GS = 8 / W;                        // groups per 16-byte weight load per lane

@@ -63,12 +63,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
   float (*red2)[kChunks][16][17] = reinterpret_cast<float (*)[kChunks][16][17]>(zero_row + kGroup);
 
   // ---------------------------------------------------------------- stage
-  // Two phases so that activation (L2) and weight (HBM) latencies overlap:
-  // the activation loads of up to kPass passes are issued first, then the
-  // weights of the first streamed item, and only then are the activations
-  // converted into B slots (vmcnt drains in order, so waiting for the
-  // activations does not wait for the weights). Passes beyond kPass run
-  // load-then-convert.
+  // The activation loads of up to kPass passes are issued together, then
+  // converted into B slots; passes beyond kPass run load-then-convert. No
+  // weight load is issued before the staging is complete (see below).
   constexpr int kPass = 4;
   constexpr int ESZ = DT == kF32 ? 4 : 2;
   constexpr int LPR = FUSED ? 8 : 4;             // lanes per group-row
@@ -148,11 +145,6 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
 #pragma unroll
   for (int p = 0; p < kPass; ++p)
     if (p < npass) issue(p, early[p]);
-  // Every wave's activation loads enter the CU's memory queue before any
-  // weight load: vector memory requests of a CU are served in issue order, so
-  // without this barrier the activations of late waves would wait behind the
-  // weight streams of early ones.
-  __syncthreads();
 
   // ---------------------------------------------------------------- stream
   const int slot_k = smallm_slot_k<W>(kb);
@@ -184,7 +176,6 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
 
   uint32_t cur[DSB][4], nxt[DSB][4];
   ChannelConst cur_cc{0.0f, 0u}, nxt_cc{0.0f, 0u};
-  if (items > 0) load_item(0, cur, cur_cc);
 #pragma unroll
   for (int p = 0; p < kPass; ++p)
     if (p < npass) convert(p, early[p]);
@@ -194,6 +185,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream(const LinearArgs args, in
     convert(p, r);
   }
   __syncthreads();  // slabs and the zero row are visible to their readers
+  // The weight stream starts only now: issued earlier, the first items of all
+  // workgroups (tens of MB) would sit in front of the small activation loads
+  // in the memory system and hold the staging, and so every tile, back by
+  // several microseconds.
+  if (items > 0) load_item(0, cur, cur_cc);
 
   float p[4] = {0.f, 0.f, 0.f, 0.f};
   int par = 0;                                // parity of the workgroup's current tile
@@ -309,8 +305,8 @@ static void launch_one(const LinearArgs& g, hipStream_t st) {
   auto kern = gemm_stream<W, A, NW, MODE, DT, SCALE>;
   static bool attr_set = false;  // allow dynamic LDS beyond the default per-launch limit
   if (!attr_set) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)kStreamLdsMax);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)kStreamLdsMax);
     attr_set = true;
   }
   const int grid = resident_grid(kern, NW * 64, lds, g.tiles);

@@ -36,12 +36,33 @@ struct LinearArgs {
   int M, K, bias_dt, out_dt;
 };
 
+// The problem owning row tile `tile`, selected field by field with constant
+// indices so the by-value kernel arguments stay in scalar kernarg loads.
+__device__ __forceinline__ Problem select_problem(const LinearArgs& args, int tile) {
+  Problem pr;
+  pr.w = args.prob[0].w; pr.ws = args.prob[0].ws; pr.bias = args.prob[0].bias;
+  pr.out = args.prob[0].out; pr.N = args.prob[0].N; pr.tile0 = args.prob[0].tile0;
+#pragma unroll
+  for (int q = 1; q < kMaxProblems; ++q) {
+    if (q < args.nprob && tile >= args.prob[q].tile0) {
+      pr.w = args.prob[q].w; pr.ws = args.prob[q].ws; pr.bias = args.prob[q].bias;
+      pr.out = args.prob[q].out; pr.N = args.prob[q].N; pr.tile0 = args.prob[q].tile0;
+    }
+  }
+  return pr;
+}
+
 void launch_quantize(const void* x, int dt, const void* sc, long M, long K, int A, uint8_t* packed,
                      float* scales, hipStream_t stream);
 void launch_smallm(int W, int A, int nw, int mode, const LinearArgs& g, hipStream_t st);
 void launch_tiled(int W, int A, int shape, bool dots, const LinearArgs& g, hipStream_t st);
 void launch_stream(int W, int A, int nw, int mode, const LinearArgs& g, hipStream_t st);
 void launch_prefill(int W, int A, int shape, bool dots, const LinearArgs& g, hipStream_t st);
+void launch_decode(int W, int A, int nw, const LinearArgs& g, hipStream_t st);
+size_t decode_lds_bytes(int K, int M, int nw);
+// true when the decode kernel with nw waves takes an M x K problem of width W
+// (every wave's loads fit its register ring and x passes)
+bool decode_fits(int K, int M, int W, int nw);
 size_t stream_lds_bytes(int K, int M, int nw);
 
 }  // namespace actune

@@ -446,7 +446,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": None if traffic is None else traffic.get("bytes_per_launch"),
-                     "kernel": "fused group-64 quantize + packed W4A8 GEMM, small-M (gemm_smallm / gemm_stream)",
+                     "kernel": "fused group-64 quantize + packed W4A8 GEMM, decode kernel (gemm_decode)",
                      "avg_launch_us": round(r1["ms_sib"] * 1e3 / r1["launches_sib"], 3),
                      "algorithmic_bytes_per_launch": round(r1["abytes"] / r1["launches_sib"])},
         "detail": {},

@@ -196,7 +196,7 @@ def test_fused_small_m_equals_two_step(W, A, m, dtype):
     xd, bd = x.to(DEV), b.to(DEV)
     for scale in (None, torch.linspace(0.5, 2.0, k).to(dtype)):
         sd = None if scale is None else scale.to(DEV)
-        for config in range(3):
+        for config in (0, 1, 2, 14, 15, 16):  # small-M and decode kernels
             fused = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, input_scale=sd, config=config)
             p, s = _native.quantize_groups(xd, A, sd)
             two = _native.grouped_linear(p, s, w_dev, ws_dev, bd, xd, W, A, config)
@@ -205,6 +205,23 @@ def test_fused_small_m_equals_two_step(W, A, m, dtype):
         wc, wsc = oracle_weight(w, W, A)
         want = O.linear(a_codes, a_scales, wc, wsc, b.float().numpy(), bounds=canonical_bounds(k // 64))
         np.testing.assert_array_equal(bits(fused), O.round_out(want, dtype_name(dtype)))
+
+
+@pytest.mark.parametrize("W,A", [(4, 8), (2, 4), (8, 8), (8, 2)])
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("k", [4096, 8192, 11008])
+def test_decode_full_ring_equals_small_m(W, A, m, k):
+    """Decode configs at K where a wave's weight range fills its load ring
+    (and, for K = 11008 with 4 or 8 waves, exceeds it: those run the small-M
+    kernel) equal the small-M kernel bit for bit, with a ragged N."""
+    n = 72
+    x, w, b = seeded_inputs(m, k, n, seed=k + W * A + m, bias=True)
+    _, _, w_dev, ws_dev = _packed_weight(w, W, A)
+    xd, bd = x.to(DEV), b.to(DEV)
+    want = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, config=2)
+    for config in (14, 15, 16):
+        got = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, config=config)
+        assert torch.equal(got, want), config
 
 
 @pytest.mark.parametrize("m", [1, 4, 8, 50, 100])

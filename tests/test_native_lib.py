@@ -36,15 +36,23 @@ def test_version_and_layout_selftest():
 
 def test_config_table():
     n = _native.num_configs()
-    assert n == 14
+    assert n == 17
     assert _native.config_valid(0, 64) and not _native.config_valid(0, 65)
     assert all(_native.config_valid(c, 4096) for c in range(3, 7))
     assert all(_native.config_valid(c, 1) and _native.config_valid(c, 4096) for c in range(10, 14))
+    assert all(_native.config_valid(c, 4) and not _native.config_valid(c, 5) for c in range(14, 17))
     assert _native.config_valid(9, 16) and not _native.config_valid(9, 17)
     assert not _native.config_valid(n, 1) and not _native.config_valid(-2, 1)
     for m in (1, 8, 16, 17, 50, 512):
         c = _native.default_config(m, 4096, 4096, 4, 8)
         assert _native.config_valid(c, m)
+    # fused decode: the fewest waves whose load ring holds a wave's K-range
+    assert _native.default_config(1, 4096, 4096, 4, 8) == 14
+    assert _native.default_config(4, 4096, 4096, 4, 8) == 15   # 4 tokens x 16 groups exceed the x passes
+    assert _native.default_config(1, 4096, 11008, 4, 8) == 16
+    assert _native.default_config(1, 4096, 4096, 8, 8) == 15   # W8: 8 groups per ring
+    assert _native.default_config(1, 1024, 4096, 4, 8) == 16   # 64 tiles: 16 waves each
+    assert _native.default_config(1, 4096, 65536, 4, 8) == 2   # no decode config fits
 
 
 def _err():
