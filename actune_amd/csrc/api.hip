@@ -152,6 +152,7 @@ LinearArgs base_args(int64_t M, int64_t K, int bias_dt, int out_dt) {
   g.K = (int)K;
   g.bias_dt = bias_dt;
   g.out_dt = out_dt;
+  g.m_div = M > 0 ? (uint32_t)((65536 + M - 1) / M) : 0u;
   return g;
 }
 

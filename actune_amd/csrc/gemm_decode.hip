@@ -9,7 +9,10 @@
 //
 // Structure:
 //  * A workgroup is NW waves and owns one 16-row tile of one problem (up to
-//    kMaxProblems linears that read the same x share a launch). The waves
+//    kMaxProblems linears that read the same x share a launch; the problem
+//    is blockIdx.y, so each workgroup reads only its own problem's kernel
+//    arguments, in the one batch of scalar loads before its first memory
+//    load). The waves
 //    split K along the 16 canonical chunks. Workgroups are light (small LDS,
 //    no per-tile staging), so several are resident per CU and nearly every
 //    tile of a decode-size problem is in flight at once.
@@ -27,6 +30,8 @@
 //    slab. One fp32 FMA per (row, token, group).
 //  * Chunk partials meet in a small LDS array [16 chunks][16 rows][4 tokens]
 //    and are added in chunk order after one barrier.
+#include <algorithm>
+
 #include "common.hpp"
 #include "launch.hpp"
 #include "operands.hpp"
@@ -76,14 +81,29 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   constexpr int kPass = kDecodePass;      // x passes (8 group-rows each) loaded before the weights
 
   const float fold = __builtin_ldexpf(1.0f, -T);
-  const Problem pr = select_problem(args, blockIdx.x);
-  const int M = args.M, K = args.K, N = pr.N, G = K / kGroup;
+  // Every kernel argument the prologue needs is read here, in one batch of
+  // scalar loads with one wait: the empty asm takes the values as operands
+  // it may change, so none of them is reloaded later (a reload would put a
+  // scalar round trip between entry and the first weight load).
+  // The problem is blockIdx.y: its fields sit at an offset known at entry.
+  Problem pr = args.prob[blockIdx.y];
+  int M = args.M, K = args.K, bias_dt = args.bias_dt, out_dt = args.out_dt;
+  uint32_t m_inv = args.m_div;  // idx / M == (idx * m_inv) >> 16 here
+  const void* xsrc = args.x;
+  const void* xscale = args.xscale;
+  asm volatile("" : "+s"(M), "+s"(K), "+s"(bias_dt), "+s"(out_dt), "+s"(m_inv), "+s"(xsrc), "+s"(xscale), "+s"(GW),
+                    "+s"(pr.w), "+s"(pr.ws), "+s"(pr.bias), "+s"(pr.out), "+s"(pr.N));
+  const int N = pr.N, G = K / kGroup;
+  const int n0 = (int)blockIdx.x * 16;
+  // blockIdx.x spans the widest problem of the launch; a narrower one's
+  // workgroups past its rows leave at once (whole workgroup, before any
+  // barrier)
+  if (n0 >= N) return;
   // wave is read into a scalar register so that every K-range bound below is
   // wave-uniform: the step loop then branches on scalars and the memory
   // counter waits stay per slot.
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int i = lane & 15, kb = lane >> 4;
-  const int n0 = ((int)blockIdx.x - pr.tile0) * 16;
   const int c_first = wave * CPW;
   const int wg0 = chunk_begin(c_first, G), wg1 = chunk_begin(c_first + CPW, G);
   const int ng = wg1 - wg0;                 // groups of this wave
@@ -95,27 +115,24 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
                                                  (size_t)NW * GW * 4);
   float (*red)[16][kDecodeMaxM] = reinterpret_cast<float (*)[16][kDecodeMaxM]>(zero_row + kGroup);
 
-  // Epilogue constants of the output this thread finishes (wave 0: row
-  // lane / 4, token lane % 4), fetched first.
+  // The output this thread finishes in the epilogue (wave 0: row lane / 4,
+  // token lane % 4).
   const int e_row = lane >> 2, e_m = lane & 3;
-  const ChannelConst cc = fetch_channel(pr.ws, pr.bias, args.bias_dt, N, n0 + e_row, wave == 0 && e_m < M);
 
   // ---------------------------------------------------------------- x loads
   // Group-row r = gl * M + m (gl: group of the wave's range, m: token); a
   // pass covers 8 group-rows, 8 lanes each, 8 consecutive elements per lane.
   const int rows_here = ng * M;
   const int npass = (rows_here + 7) / 8;
-  const Rsrc xres = make_rsrc(args.x, (uint32_t)M * K * ESZ);
-  const Rsrc xsres = make_rsrc(SCALE ? args.xscale : args.x, (uint32_t)K * ESZ);
+  const Rsrc xres = make_rsrc(xsrc, (uint32_t)M * K * ESZ);
+  const Rsrc xsres = make_rsrc(SCALE ? xscale : xsrc, (uint32_t)K * ESZ);
   const int seg = lane & 7;
-  // idx / M for idx < 2^14 and M <= 4 as (idx * ceil(2^16 / M)) >> 16
-  const uint32_t m_inv = (65536u + (uint32_t)M - 1u) / (uint32_t)M;
   struct Raw { v4u x[XL], s[XL]; };
   auto issue_x = [&](int pass, Raw& r) {
     const int idx = pass * 8 + (lane >> 3);
     const bool live = idx < rows_here;
-    const int q = (int)(((uint32_t)idx * m_inv) >> 16);
-    const int gl = live ? q : 0, m = live ? idx - q * M : 0;
+    const int q = ONE ? idx : (int)(((uint32_t)idx * m_inv) >> 16);
+    const int gl = live ? q : 0, m = ONE || !live ? 0 : idx - q * M;
     const uint32_t k0 = (uint32_t)((wg0 + gl) * kGroup + seg * 8);
     const uint32_t xo = live ? ((uint32_t)m * K + k0) * ESZ : kOff;
 #pragma unroll
@@ -129,8 +146,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   auto convert_x = [&](int pass, const Raw& r) {
     const int idx = pass * 8 + (lane >> 3);
     const bool live = idx < rows_here;
-    const int q = (int)(((uint32_t)idx * m_inv) >> 16);
-    const int gl = live ? q : 0, m = live ? idx - q * M : 0;
+    const int q = ONE ? idx : (int)(((uint32_t)idx * m_inv) >> 16);
+    const int gl = live ? q : 0, m = ONE || !live ? 0 : idx - q * M;
     float v[8];
     unpack8<DT>(r.x[0], r.x[XL - 1], v);
     if constexpr (SCALE) {
@@ -162,6 +179,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   uint32_t ring[RING][4];
 #pragma unroll
   for (int r = 0; r < RING; ++r) load_step(r, ring[r]);
+  // epilogue constants, behind the weights: they are needed last
+  const ChannelConst cc = fetch_channel(pr.ws, pr.bias, bias_dt, N, n0 + e_row, wave == 0 && e_m < M);
 
   // ---------------------------------------------------------------- quantize x
   if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zero_row)[threadIdx.x] = 0u;
@@ -205,6 +224,19 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
       const int st = r;
       if (st >= ns) break;
       if (r + 1 < RING) read_b(r + 1, bq[(r + 1) & 1], bs[(r + 1) & 1]);
+      // Chunk boundaries are multiples of 4 groups and a slot's GS groups
+      // start at a multiple of GS, so chunks close only at slot starts. The
+      // close runs before the slot's MFMAs so that no branch separates an
+      // MFMA from the VALU reads of its result: the compiler's wait states
+      // for that hazard have been seen missing when a branch intervened.
+      const int g0 = wg0 + st * GS;
+      while (g0 >= cend) {  // close finished (possibly empty) chunks
+        if (lane < 16) *reinterpret_cast<v4f*>(&red[c][lane][0]) = v4f{p[0], p[1], p[2], p[3]};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) p[q] = 0.f;
+        ++c;
+        cend = chunk_begin(c + 1, G);
+      }
       exchange<W>(ring[r]);
       v4i D[GS];
 #pragma unroll
@@ -214,16 +246,6 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
         const v4u b = bq[r & 1][jj];
         const uint32_t bd[4] = {b[0], b[1], b[2], b[3]};
         D[jj] = mfma16x16x64(bd, wd, v4i{0, 0, 0, 0});
-      }
-      // Chunk boundaries are multiples of 4 groups and a slot's GS groups
-      // start at a multiple of GS, so chunks close only at slot starts.
-      const int g0 = wg0 + st * GS;
-      while (g0 >= cend) {  // close finished (possibly empty) chunks
-        if (lane < 16) *reinterpret_cast<v4f*>(&red[c][lane][0]) = v4f{p[0], p[1], p[2], p[3]};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) p[q] = 0.f;
-        ++c;
-        cend = chunk_begin(c + 1, G);
       }
 #pragma unroll
       for (int jj = 0; jj < GS; ++jj) {
@@ -250,10 +272,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
 #pragma unroll
     for (int q = 1; q < kChunks; ++q) acc = acc + red[q][e_row][e_m];
     if (n < N) {
-      const float y = finish_const(acc, cc, pr.bias != nullptr, args.bias_dt);
+      const float y = finish_const(acc, cc, pr.bias != nullptr, bias_dt);
       const long o = (long)e_m * N + n;
-      if (args.out_dt == kBF16) store_out<kBF16>(pr.out, o, y);
-      else if (args.out_dt == kF16) store_out<kF16>(pr.out, o, y);
+      if (out_dt == kBF16) store_out<kBF16>(pr.out, o, y);
+      else if (out_dt == kF16) store_out<kF16>(pr.out, o, y);
       else store_out<kF32>(pr.out, o, y);
     }
   }
@@ -271,7 +293,9 @@ static void launch_decode_one(const LinearArgs& g, hipStream_t st) {
                               (int)kStreamLdsMax);
     attr_set = true;
   }
-  kern<<<dim3((unsigned)g.tiles), NW * 64, lds, st>>>(g, decode_groups_per_wave(g.K, NW));
+  int row_tiles = 1;  // grid x: the row tiles of the widest problem; grid y: the problems
+  for (int q = 0; q < g.nprob; ++q) row_tiles = std::max(row_tiles, (g.prob[q].N + 15) / 16);
+  kern<<<dim3((unsigned)row_tiles, (unsigned)g.nprob), NW * 64, lds, st>>>(g, decode_groups_per_wave(g.K, NW));
 }
 
 template <int W, int A, int NW>

@@ -34,20 +34,30 @@ struct LinearArgs {
   int x_dt;
   int32_t* dots;        // [M, N, K/64] (dots mode, single problem)
   int M, K, bias_dt, out_dt;
+  uint32_t m_div;       // ceil(2^16 / M): idx / M == (idx * m_div) >> 16 for idx < 2^14, M <= 16
 };
 
-// The problem owning row tile `tile`, selected field by field with constant
-// indices so the by-value kernel arguments stay in scalar kernarg loads.
+// The problem owning row tile `tile`. Every slot is read unconditionally and
+// the owner is picked with scalar selects, so the by-value kernel arguments
+// arrive in one batch of scalar loads (a branch per slot would put a load
+// round trip on the path to the first weight load for each slot).
 __device__ __forceinline__ Problem select_problem(const LinearArgs& args, int tile) {
-  Problem pr;
-  pr.w = args.prob[0].w; pr.ws = args.prob[0].ws; pr.bias = args.prob[0].bias;
-  pr.out = args.prob[0].out; pr.N = args.prob[0].N; pr.tile0 = args.prob[0].tile0;
+  Problem pp[kMaxProblems];
+#pragma unroll
+  for (int q = 0; q < kMaxProblems; ++q) pp[q] = args.prob[q];
+  int sel = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxProblems; ++q) sel += (q < args.nprob && tile >= pp[q].tile0) ? 1 : 0;
+  Problem pr = pp[0];
 #pragma unroll
   for (int q = 1; q < kMaxProblems; ++q) {
-    if (q < args.nprob && tile >= args.prob[q].tile0) {
-      pr.w = args.prob[q].w; pr.ws = args.prob[q].ws; pr.bias = args.prob[q].bias;
-      pr.out = args.prob[q].out; pr.N = args.prob[q].N; pr.tile0 = args.prob[q].tile0;
-    }
+    const bool s = sel == q;
+    pr.w = s ? pp[q].w : pr.w;
+    pr.ws = s ? pp[q].ws : pr.ws;
+    pr.bias = s ? pp[q].bias : pr.bias;
+    pr.out = s ? pp[q].out : pr.out;
+    pr.N = s ? pp[q].N : pr.N;
+    pr.tile0 = s ? pp[q].tile0 : pr.tile0;
   }
   return pr;
 }
