@@ -64,13 +64,23 @@ bool decode_fits(int K, int M, int W, int nw) {
          decode_lds_bytes(K, M, nw) <= kStreamLdsMax;
 }
 
+// true when every one of nw waves gets exactly a full ring of weight slots
+static bool decode_full(int K, int W, int nw) {
+  const int G = K / kGroup, cpw = kChunks / nw, per = decode_ring(W) * (8 / W);
+  for (int w = 0; w < nw; ++w)
+    if (chunk_begin((w + 1) * cpw, G) - chunk_begin(w * cpw, G) != per) return false;
+  return true;
+}
+
 size_t decode_lds_bytes(int K, int M, int nw) {
   const int gw = decode_groups_per_wave(K, nw);
   return (size_t)nw * gw * (M * kGroup + 4 * sizeof(float)) + kGroup + sizeof(float) * kChunks * 16 * kDecodeMaxM;
 }
 
-// ONE: M == 1 (only register 0 of the MFMA result is rescaled).
-template <int W, int A, int NW, int RING, int DT, bool SCALE, bool ONE>
+// ONE: M == 1 (only register 0 of the MFMA result is rescaled). FULL: every
+// wave's K-range is exactly RING slots (decode_full), so the slot pipeline
+// runs without bounds tests.
+template <int W, int A, int NW, int RING, int DT, bool SCALE, bool ONE, bool FULL>
 __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, int GW) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int GS = 8 / W;                // groups per 16-byte weight load per lane
@@ -128,7 +138,22 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   const Rsrc xsres = make_rsrc(SCALE ? xscale : xsrc, (uint32_t)K * ESZ);
   const int seg = lane & 7;
   struct Raw { v4u x[XL], s[XL]; };
+  // M == 1: lane l of pass p reads elements wg0*64 + p*512 + 8l.. of x (the
+  // rows past the wave's range read neighbouring elements or zeros and are
+  // not stored); the pass is a constant offset, passes past npass are
+  // switched off through the scalar offset.
+  const uint32_t xbase1 = ((uint32_t)wg0 * kGroup + (uint32_t)lane * 8) * ESZ;
   auto issue_x = [&](int pass, Raw& r) {
+    if constexpr (ONE) {
+      const uint32_t soff = pass < npass ? 0u : kOff;
+#pragma unroll
+      for (int h = 0; h < XL; ++h) {
+        r.x[h] = __builtin_amdgcn_raw_buffer_load_b128(xres, xbase1 + (uint32_t)(pass * 512 * ESZ + 16 * h), soff, 0);
+        if constexpr (SCALE)
+          r.s[h] = __builtin_amdgcn_raw_buffer_load_b128(xsres, xbase1 + (uint32_t)(pass * 512 * ESZ + 16 * h), soff, 0);
+      }
+      return;
+    }
     const int idx = pass * 8 + (lane >> 3);
     const bool live = idx < rows_here;
     const int q = ONE ? idx : (int)(((uint32_t)idx * m_inv) >> 16);
@@ -170,15 +195,18 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   // ---------------------------------------------------------------- weight loads
   const uint32_t wrow_bytes = (uint32_t)K * W / 8;
   const Rsrc wres = make_rsrc(pr.w, (uint32_t)N * wrow_bytes);
-  const uint32_t wbase = n0 + i < N ? (uint32_t)(n0 + i) * wrow_bytes + kb * 16 : kOff;
-  auto load_step = [&](int st, uint32_t (&buf)[4]) {
-    const uint32_t off = (uint32_t)(wg0 + st * GS) * 8 * W;
-    buffer_slot<8>(wres, st < ns && wbase != kOff ? wbase + off : kOff, buf);
-  };
+  // Slot st of the wave is 64 bytes past slot st-1: a constant offset. Rows
+  // past N lie past the buffer's range and read zeros; slots past the wave's
+  // range are switched off through the scalar offset (the vector offset
+  // stays below 2^31, so the sum cannot wrap).
+  const uint32_t wbase = (uint32_t)(n0 + i) * wrow_bytes + kb * 16 + (uint32_t)wg0 * 8 * W;
   // the host guarantees ns <= RING and npass <= kPass (decode_fits)
   uint32_t ring[RING][4];
 #pragma unroll
-  for (int r = 0; r < RING; ++r) load_step(r, ring[r]);
+  for (int st = 0; st < RING; ++st) {
+    const v4u q = __builtin_amdgcn_raw_buffer_load_b128(wres, wbase + (uint32_t)st * 64, st < ns ? 0u : kOff, 0);
+    ring[st][0] = q[0]; ring[st][1] = q[1]; ring[st][2] = q[2]; ring[st][3] = q[3];
+  }
   // epilogue constants, behind the weights: they are needed last
   const ChannelConst cc = fetch_channel(pr.ws, pr.bias, bias_dt, N, n0 + e_row, wave == 0 && e_m < M);
 
@@ -193,9 +221,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   // ---------------------------------------------------------------- stream the K-range
   // The tokens are the MFMA A operand and the weight rows the B operand, so
   // token m of weight row c lands in lane c, register m: only M registers of
-  // lanes 0..15 carry results and only those are rescaled. Slot r's token
-  // operands (slab rows and the group scales) are read one slot ahead; the GS
-  // MFMAs of a slot are issued together and folded in group order.
+  // lanes 0..15 carry results and only those are rescaled. The GS MFMAs of a
+  // slot are issued together and folded in group order.
   const int slot_k = smallm_slot_k<W>(kb);
   // Lanes of absent tokens (i >= M) read the zero row with stride 0. A group
   // past the wave's range (the tail of its last slot, or a slot read ahead
@@ -213,48 +240,66 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
       bs[jj] = *reinterpret_cast<const v4f*>(srow);  // same address in every lane
     }
   };
-  v4u bq[2][GS];
-  v4f bs[2][GS];
-  read_b(0, bq[0], bs[0]);
+  // Software pipeline over the wave's ns slots: slot st+1's MFMAs are issued
+  // before slot st's results are rescaled, so MFMA latency hides under that
+  // work. Token operands are read three slots ahead. (Slot 0's MFMAs run
+  // even when the wave has no slot: its weights and scales are zero.)
+  constexpr int RA = 3;
+  v4u bq[RING][GS];
+  v4f bs[RING][GS];
+  v4i D[RING][GS];
+#pragma unroll
+  for (int st = 0; st < RA && st < RING; ++st) read_b(st, bq[st], bs[st]);
+  auto mfma_slot = [&](int st) {
+    exchange<W>(ring[st]);
+#pragma unroll
+    for (int jj = 0; jj < GS; ++jj) {
+      uint32_t wd[4];
+      unpack_slot<W>(&ring[st][jj * W / 2], wd);
+      const uint32_t bd[4] = {bq[st][jj][0], bq[st][jj][1], bq[st][jj][2], bq[st][jj][3]};
+      D[st][jj] = mfma16x16x64(bd, wd, v4i{0, 0, 0, 0});
+    }
+  };
   float p[4] = {0.f, 0.f, 0.f, 0.f};
   int c = c_first, cend = chunk_begin(c + 1, G);
-  {
+  const int c_last = c_first + CPW - 1;
+  mfma_slot(0);
 #pragma unroll
-    for (int r = 0; r < RING; ++r) {
-      const int st = r;
+  for (int st = 0; st < RING; ++st) {
+    if constexpr (!FULL) {
       if (st >= ns) break;
-      if (r + 1 < RING) read_b(r + 1, bq[(r + 1) & 1], bs[(r + 1) & 1]);
-      // Chunk boundaries are multiples of 4 groups and a slot's GS groups
-      // start at a multiple of GS, so chunks close only at slot starts. The
-      // close runs before the slot's MFMAs so that no branch separates an
-      // MFMA from the VALU reads of its result: the compiler's wait states
-      // for that hazard have been seen missing when a branch intervened.
-      const int g0 = wg0 + st * GS;
-      while (g0 >= cend) {  // close finished (possibly empty) chunks
-        if (lane < 16) *reinterpret_cast<v4f*>(&red[c][lane][0]) = v4f{p[0], p[1], p[2], p[3]};
+    }
+    if (st + 1 < RING && (FULL || st + 1 < ns)) {
+      if (st + RA < RING) read_b(st + RA, bq[st + RA], bs[st + RA]);
+      mfma_slot(st + 1);
+    }
+    // Chunk boundaries are multiples of 4 groups and a slot's GS groups
+    // start at a multiple of GS, so chunks close only at slot starts.
+    const int g0 = wg0 + st * GS;
+    while (g0 >= cend && c < c_last) {  // close finished (possibly empty) chunks
+      if (lane < 16) *reinterpret_cast<v4f*>(&red[c][lane][0]) = v4f{p[0], p[1], p[2], p[3]};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) p[q] = 0.f;
-        ++c;
-        cend = chunk_begin(c + 1, G);
-      }
-      exchange<W>(ring[r]);
-      v4i D[GS];
+      for (int q = 0; q < 4; ++q) p[q] = 0.f;
+      ++c;
+      cend = chunk_begin(c + 1, G);
+    }
+    // With one MFMA and one FMA per slot (W8, M == 1) the last slot's
+    // result would be read 7 instructions after its MFMA across branches,
+    // one short of the wait states the compiler keeps in straight-line
+    // code; two more are added here, fenced so the scheduler keeps them in
+    // front of the rescale.
+    if constexpr (GS == 1 && ONE) {
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_nop 1");
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
-      for (int jj = 0; jj < GS; ++jj) {
-        uint32_t wd[4];
-        unpack_slot<W>(&ring[r][jj * W / 2], wd);
-        const v4u b = bq[r & 1][jj];
-        const uint32_t bd[4] = {b[0], b[1], b[2], b[3]};
-        D[jj] = mfma16x16x64(bd, wd, v4i{0, 0, 0, 0});
-      }
+    for (int jj = 0; jj < GS; ++jj) {
+      // registers of absent tokens hold zeros (their scale entries are
+      // unset and their partials never read)
+      const v4f sc = bs[st][jj];
 #pragma unroll
-      for (int jj = 0; jj < GS; ++jj) {
-        // registers of absent tokens hold zeros (their scale entries are
-        // unset and their partials never read)
-        const v4f sc = bs[r & 1][jj];
-#pragma unroll
-        for (int q = 0; q < (ONE ? 1 : 4); ++q) p[q] = __builtin_fmaf((float)D[jj][q], sc[q], p[q]);
-      }
+      for (int q = 0; q < (ONE ? 1 : 4); ++q) p[q] = __builtin_fmaf((float)D[st][jj][q], sc[q], p[q]);
     }
   }
   // lane c < 16 holds row c of tokens 0..3 (zero for absent tokens)
@@ -282,11 +327,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
 }
 
 // ---------------------------------------------------------------------------
-template <int W, int A, int NW, int DT, bool SCALE, bool ONE>
+template <int W, int A, int NW, int DT, bool SCALE, bool ONE, bool FULL>
 static void launch_decode_one(const LinearArgs& g, hipStream_t st) {
   constexpr int RING = decode_ring(W);
   const size_t lds = decode_lds_bytes(g.K, g.M, NW);
-  auto kern = gemm_decode<W, A, NW, RING, DT, SCALE, ONE>;
+  auto kern = gemm_decode<W, A, NW, RING, DT, SCALE, ONE, FULL>;
   static bool attr_set = false;  // allow dynamic LDS beyond the default per-launch limit
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -301,8 +346,20 @@ static void launch_decode_one(const LinearArgs& g, hipStream_t st) {
 template <int W, int A, int NW>
 static void launch_decode_nw(const LinearArgs& g, hipStream_t st) {
 #define DEC_ONE(DTV, SC)                                                        \
-  if (g.M == 1) launch_decode_one<W, A, NW, DTV, SC, true>(g, st);              \
-  else launch_decode_one<W, A, NW, DTV, SC, false>(g, st)
+  if (g.M == 1) launch_decode_one<W, A, NW, DTV, SC, true, false>(g, st);       \
+  else launch_decode_one<W, A, NW, DTV, SC, false, false>(g, st)
+  // bf16 activations of shapes whose waves each fill the ring exactly take
+  // the bound-free pipeline
+  if (g.x_dt == kBF16 && decode_full(g.K, W, NW)) {
+    if (g.xscale) {
+      if (g.M == 1) launch_decode_one<W, A, NW, kBF16, true, true, true>(g, st);
+      else launch_decode_one<W, A, NW, kBF16, true, false, true>(g, st);
+    } else {
+      if (g.M == 1) launch_decode_one<W, A, NW, kBF16, false, true, true>(g, st);
+      else launch_decode_one<W, A, NW, kBF16, false, false, true>(g, st);
+    }
+    return;
+  }
 #define DEC_DT(DTV)                                                             \
   if (g.xscale) { DEC_ONE(DTV, true); }                                         \
   else { DEC_ONE(DTV, false); }

@@ -224,6 +224,30 @@ def test_decode_full_ring_equals_small_m(W, A, m, k):
         assert torch.equal(got, want), config
 
 
+@pytest.mark.parametrize("W,A", [(4, 8), (2, 2), (8, 4), (4, 4)])
+@pytest.mark.parametrize("m", [1, 3])
+def test_decode_full_ring_with_channel_scale(W, A, m):
+    """K = 4096: every wave of the 4-wave (W2/W4) or 8-wave (W8) decode
+    config fills its load ring exactly, which runs the bound-free slot
+    pipeline; with and without the fused channel scale it equals quantize +
+    GEMM and the oracle bit for bit (N ragged)."""
+    k, n = 4096, 88
+    x, w, b = seeded_inputs(m, k, n, seed=7 * W + A + m, bias=True)
+    _, _, w_dev, ws_dev = _packed_weight(w, W, A)
+    xd, bd = x.to(DEV), b.to(DEV)
+    scale = torch.linspace(0.5, 2.0, k).to(torch.bfloat16)
+    for sd in (None, scale.to(DEV)):
+        p, s = _native.quantize_groups(xd, A, sd)
+        ref = _native.grouped_linear(p, s, w_dev, ws_dev, bd, xd, W, A, 2)
+        for config in (14, 15, 16):
+            out = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, input_scale=sd, config=config)
+            assert torch.equal(out, ref), (config, sd is None)
+    a_packed, a_scales, a_codes = oracle_activation(x, A, scale)
+    wc, wsc = oracle_weight(w, W, A)
+    want = O.linear(a_codes, a_scales, wc, wsc, b.float().numpy(), bounds=canonical_bounds(k // 64))
+    np.testing.assert_array_equal(bits(out), O.round_out(want, "bf16"))
+
+
 @pytest.mark.parametrize("m", [1, 4, 8, 50, 100])
 @pytest.mark.parametrize("W,A", [(4, 8), (2, 4), (8, 2)])
 def test_multi_target_equals_separate_calls(m, W, A):
