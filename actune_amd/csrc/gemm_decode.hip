@@ -72,14 +72,29 @@ static bool decode_full(int K, int W, int nw) {
   return true;
 }
 
+// zero region: a wave's widest K-range (16 groups) of 64-byte zero rows
+constexpr int kDecodeZeroBytes = 16 * kGroup;
+
 size_t decode_lds_bytes(int K, int M, int nw) {
   const int gw = decode_groups_per_wave(K, nw);
-  return (size_t)nw * gw * (M * kGroup + 4 * sizeof(float)) + kGroup + sizeof(float) * kChunks * 16 * kDecodeMaxM;
+  return (size_t)nw * gw * (M * kGroup + 4 * sizeof(float)) + kDecodeZeroBytes +
+         sizeof(float) * kChunks * 16 * kDecodeMaxM;
+}
+
+// chunk_begin in unsigned arithmetic (c, G >= 0): shifts instead of the
+// signed-division sequences, for the slot loop's scalar chunk tracking
+__device__ __forceinline__ int chunk_begin_u(int c, int G) {
+  const uint32_t Q = ((uint32_t)G + 3u) >> 2;
+  const uint32_t b = (((uint32_t)c * Q) >> 4) << 2;
+  return b < (uint32_t)G ? (int)b : G;
 }
 
 // ONE: M == 1 (only register 0 of the MFMA result is rescaled). FULL: every
 // wave's K-range is exactly RING slots (decode_full), so the slot pipeline
-// runs without bounds tests.
+// runs without bounds tests. FULL and ONE together (the decode step's
+// launches) also take exactly the x passes of the K-range, read token
+// operands at constant LDS offsets and keep the group scales in scalar
+// registers.
 template <int W, int A, int NW, int RING, int DT, bool SCALE, bool ONE, bool FULL>
 __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, int GW) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -89,6 +104,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   constexpr int ESZ = DT == kF32 ? 4 : 2;
   constexpr int XL = DT == kF32 ? 2 : 1;   // 16-byte loads per 8 elements of x
   constexpr int kPass = kDecodePass;      // x passes (8 group-rows each) loaded before the weights
+  constexpr bool FAST = FULL && ONE;
+  constexpr int NPX = FAST ? (RING * GS + 7) / 8 : kPass;  // x passes issued
 
   const float fold = __builtin_ldexpf(1.0f, -T);
   // Every kernel argument the prologue needs is read here, in one batch of
@@ -123,7 +140,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   float* sslab = reinterpret_cast<float*>(smem + (size_t)NW * GW * M * kGroup) + (size_t)wave * GW * 4;
   uint8_t* zero_row = reinterpret_cast<uint8_t*>(reinterpret_cast<float*>(smem + (size_t)NW * GW * M * kGroup) +
                                                  (size_t)NW * GW * 4);
-  float (*red)[16][kDecodeMaxM] = reinterpret_cast<float (*)[16][kDecodeMaxM]>(zero_row + kGroup);
+  float (*red)[16][kDecodeMaxM] = reinterpret_cast<float (*)[16][kDecodeMaxM]>(zero_row + kDecodeZeroBytes);
 
   // The output this thread finishes in the epilogue (wave 0: row lane / 4,
   // token lane % 4).
@@ -185,12 +202,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
     const float s = group_code_bits<A, DT>(v, cq);
     if (live) {
       store_half_slot<W, A>(slab + (gl * M + m) * kGroup + (seg >> 1) * 16, seg & 1, cq);
-      if (seg == 0) sslab[gl * 4 + m] = s * fold;
+      if (!FAST && seg == 0) sslab[gl * 4 + m] = s * fold;
     }
+    return s * fold;  // the same in the 8 lanes of a group
   };
   Raw early[kPass];
 #pragma unroll
-  for (int p = 0; p < kPass; ++p) issue_x(p, early[p]);
+  for (int p = 0; p < NPX; ++p) issue_x(p, early[p]);
 
   // ---------------------------------------------------------------- weight loads
   const uint32_t wrow_bytes = (uint32_t)K * W / 8;
@@ -204,102 +222,174 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   uint32_t ring[RING][4];
 #pragma unroll
   for (int st = 0; st < RING; ++st) {
+    // (a runtime test also where every slot is live: with a constant offset
+    // the compiler schedules the loads differently and the launch measured
+    // 0.4 us slower at one workgroup per CU)
     const v4u q = __builtin_amdgcn_raw_buffer_load_b128(wres, wbase + (uint32_t)st * 64, st < ns ? 0u : kOff, 0);
     ring[st][0] = q[0]; ring[st][1] = q[1]; ring[st][2] = q[2]; ring[st][3] = q[3];
   }
-  // epilogue constants, behind the weights: they are needed last
+  // epilogue constants, behind the weights: they are needed last, by wave 0.
+  // Every wave issues the two loads (switched off outside wave 0) so that all
+  // waves have the same loads in flight: behind a branch, the compiler's
+  // waits for the x passes would count from the shorter path and make wave 0
+  // wait for weight slots before quantizing.
   const ChannelConst cc = fetch_channel(pr.ws, pr.bias, bias_dt, N, n0 + e_row, wave == 0 && e_m < M);
 
   // ---------------------------------------------------------------- quantize x
-  if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zero_row)[threadIdx.x] = 0u;
+  // the zero region: one dword per thread of the first four waves
+  if (threadIdx.x < kDecodeZeroBytes / 4) reinterpret_cast<uint32_t*>(zero_row)[threadIdx.x] = 0u;
+  // FAST: the wave's group scales (s * 2^-T, wave-uniform) move from the
+  // quantizing lanes into scalar registers
+  float gsc[FAST ? RING * GS : 1];
 #pragma unroll
-  for (int p = 0; p < kPass; ++p)
-    if (p < npass) convert_x(p, early[p]);
-  // the zero row is written by wave 0 and read by every wave
+  for (int p = 0; p < NPX; ++p) {
+    if (FAST || p < npass) {
+      const float sf = convert_x(p, early[p]);
+      if constexpr (FAST) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (p * 8 + j < RING * GS) gsc[p * 8 + j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sf), 8 * j));
+      }
+    }
+  }
+  // the zero region and the slabs are written across waves
   __syncthreads();
 
   // ---------------------------------------------------------------- stream the K-range
-  // The tokens are the MFMA A operand and the weight rows the B operand, so
-  // token m of weight row c lands in lane c, register m: only M registers of
-  // lanes 0..15 carry results and only those are rescaled. The GS MFMAs of a
-  // slot are issued together and folded in group order.
-  const int slot_k = smallm_slot_k<W>(kb);
-  // Lanes of absent tokens (i >= M) read the zero row with stride 0. A group
-  // past the wave's range (the tail of its last slot, or a slot read ahead
-  // and never used) reads a clamped slab row and a zero scale, so it adds
-  // exactly nothing.
-  const bool tok = i < M;
-  const uint8_t* bbase = tok ? slab + i * kGroup + slot_k : zero_row;
-  const uint32_t bstride = tok ? (uint32_t)M * kGroup : 0u;
-  auto read_b = [&](int st, v4u (&bq)[GS], v4f (&bs)[GS]) {
-#pragma unroll
-    for (int jj = 0; jj < GS; ++jj) {
-      const int gl = max(0, min(st * GS + jj, ng - 1));
-      bq[jj] = *reinterpret_cast<const v4u*>(bbase + __umul24((uint32_t)gl, bstride));
-      const float* srow = st * GS + jj < ng ? sslab + gl * 4 : reinterpret_cast<const float*>(zero_row);
-      bs[jj] = *reinterpret_cast<const v4f*>(srow);  // same address in every lane
-    }
-  };
-  // Software pipeline over the wave's ns slots: slot st+1's MFMAs are issued
-  // before slot st's results are rescaled, so MFMA latency hides under that
-  // work. Token operands are read three slots ahead. (Slot 0's MFMAs run
-  // even when the wave has no slot: its weights and scales are zero.)
-  constexpr int RA = 3;
-  v4u bq[RING][GS];
-  v4f bs[RING][GS];
-  v4i D[RING][GS];
-#pragma unroll
-  for (int st = 0; st < RA && st < RING; ++st) read_b(st, bq[st], bs[st]);
-  auto mfma_slot = [&](int st) {
-    exchange<W>(ring[st]);
-#pragma unroll
-    for (int jj = 0; jj < GS; ++jj) {
-      uint32_t wd[4];
-      unpack_slot<W>(&ring[st][jj * W / 2], wd);
-      const uint32_t bd[4] = {bq[st][jj][0], bq[st][jj][1], bq[st][jj][2], bq[st][jj][3]};
-      D[st][jj] = mfma16x16x64(bd, wd, v4i{0, 0, 0, 0});
-    }
-  };
   float p[4] = {0.f, 0.f, 0.f, 0.f};
-  int c = c_first, cend = chunk_begin(c + 1, G);
-  const int c_last = c_first + CPW - 1;
-  mfma_slot(0);
+  int c = c_first;
+  if constexpr (FAST) {
+    // M == 1, every wave's range exactly RING slots: lanes of token 0 (i ==
+    // 0) read the wave's slab, the others the zero region, both with stride
+    // 64 per group, so every token operand read is one LDS load at a
+    // constant offset; the rescale takes its scale from a scalar register.
+    // Same pipeline and order as the general loop below.
+    constexpr int RA = 3;
+    const uint8_t* tbase = (i == 0 ? slab : zero_row) + smallm_slot_k<W>(kb);
+    v4u bq[RING][GS];
+    v4i D[RING][GS];
+    auto read_q = [&](int st) {
 #pragma unroll
-  for (int st = 0; st < RING; ++st) {
-    if constexpr (!FULL) {
-      if (st >= ns) break;
-    }
-    if (st + 1 < RING && (FULL || st + 1 < ns)) {
-      if (st + RA < RING) read_b(st + RA, bq[st + RA], bs[st + RA]);
-      mfma_slot(st + 1);
-    }
-    // Chunk boundaries are multiples of 4 groups and a slot's GS groups
-    // start at a multiple of GS, so chunks close only at slot starts.
-    const int g0 = wg0 + st * GS;
-    while (g0 >= cend && c < c_last) {  // close finished (possibly empty) chunks
-      if (lane < 16) *reinterpret_cast<v4f*>(&red[c][lane][0]) = v4f{p[0], p[1], p[2], p[3]};
+      for (int jj = 0; jj < GS; ++jj) bq[st][jj] = *reinterpret_cast<const v4u*>(tbase + (st * GS + jj) * kGroup);
+    };
 #pragma unroll
-      for (int q = 0; q < 4; ++q) p[q] = 0.f;
-      ++c;
-      cend = chunk_begin(c + 1, G);
-    }
-    // With one MFMA and one FMA per slot (W8, M == 1) the last slot's
-    // result would be read 7 instructions after its MFMA across branches,
-    // one short of the wait states the compiler keeps in straight-line
-    // code; two more are added here, fenced so the scheduler keeps them in
-    // front of the rescale.
-    if constexpr (GS == 1 && ONE) {
-      __builtin_amdgcn_sched_barrier(0);
-      asm volatile("s_nop 1");
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    for (int st = 0; st < RA && st < RING; ++st) read_q(st);
+    auto mfma_slot = [&](int st) {
+      exchange<W>(ring[st]);
 #pragma unroll
-    for (int jj = 0; jj < GS; ++jj) {
-      // registers of absent tokens hold zeros (their scale entries are
-      // unset and their partials never read)
-      const v4f sc = bs[st][jj];
+      for (int jj = 0; jj < GS; ++jj) {
+        uint32_t wd[4];
+        unpack_slot<W>(&ring[st][jj * W / 2], wd);
+        const uint32_t bd[4] = {bq[st][jj][0], bq[st][jj][1], bq[st][jj][2], bq[st][jj][3]};
+        D[st][jj] = mfma16x16x64(bd, wd, v4i{0, 0, 0, 0});
+      }
+    };
+    int cend = chunk_begin_u(c + 1, G);
+    const int c_last = c_first + CPW - 1;
+    mfma_slot(0);
 #pragma unroll
-      for (int q = 0; q < (ONE ? 1 : 4); ++q) p[q] = __builtin_fmaf((float)D[st][jj][q], sc[q], p[q]);
+    for (int st = 0; st < RING; ++st) {
+      if (st + 1 < RING) {
+        if (st + RA < RING) read_q(st + RA);
+        mfma_slot(st + 1);
+      }
+      const int g0 = wg0 + st * GS;
+      while (g0 >= cend && c < c_last) {  // close finished (possibly empty) chunks
+        if (lane < 16) *reinterpret_cast<v4f*>(&red[c][lane][0]) = v4f{p[0], 0.f, 0.f, 0.f};
+        p[0] = 0.f;
+        ++c;
+        cend = chunk_begin_u(c + 1, G);
+      }
+      if constexpr (GS == 1) {  // see the general loop
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 1");
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int jj = 0; jj < GS; ++jj) p[0] = __builtin_fmaf((float)D[st][jj][0], gsc[st * GS + jj], p[0]);
+    }
+  } else {
+    // The tokens are the MFMA A operand and the weight rows the B operand, so
+    // token m of weight row c lands in lane c, register m: only M registers of
+    // lanes 0..15 carry results and only those are rescaled. The GS MFMAs of a
+    // slot are issued together and folded in group order.
+    const int slot_k = smallm_slot_k<W>(kb);
+    // Lanes of absent tokens (i >= M) read the zero row with stride 0. A group
+    // past the wave's range (the tail of its last slot, or a slot read ahead
+    // and never used) reads a clamped slab row and a zero scale, so it adds
+    // exactly nothing.
+    const bool tok = i < M;
+    const uint8_t* bbase = tok ? slab + i * kGroup + slot_k : zero_row;
+    const uint32_t bstride = tok ? (uint32_t)M * kGroup : 0u;
+    auto read_b = [&](int st, v4u (&bq)[GS], v4f (&bs)[GS]) {
+#pragma unroll
+      for (int jj = 0; jj < GS; ++jj) {
+        const int gl = max(0, min(st * GS + jj, ng - 1));
+        bq[jj] = *reinterpret_cast<const v4u*>(bbase + __umul24((uint32_t)gl, bstride));
+        const float* srow = st * GS + jj < ng ? sslab + gl * 4 : reinterpret_cast<const float*>(zero_row);
+        bs[jj] = *reinterpret_cast<const v4f*>(srow);  // same address in every lane
+      }
+    };
+    // Software pipeline over the wave's ns slots: slot st+1's MFMAs are issued
+    // before slot st's results are rescaled, so MFMA latency hides under that
+    // work. Token operands are read three slots ahead. (Slot 0's MFMAs run
+    // even when the wave has no slot: its weights and scales are zero.)
+    constexpr int RA = 3;
+    v4u bq[RING][GS];
+    v4f bs[RING][GS];
+    v4i D[RING][GS];
+#pragma unroll
+    for (int st = 0; st < RA && st < RING; ++st) read_b(st, bq[st], bs[st]);
+    auto mfma_slot = [&](int st) {
+      exchange<W>(ring[st]);
+#pragma unroll
+      for (int jj = 0; jj < GS; ++jj) {
+        uint32_t wd[4];
+        unpack_slot<W>(&ring[st][jj * W / 2], wd);
+        const uint32_t bd[4] = {bq[st][jj][0], bq[st][jj][1], bq[st][jj][2], bq[st][jj][3]};
+        D[st][jj] = mfma16x16x64(bd, wd, v4i{0, 0, 0, 0});
+      }
+    };
+    int cend = chunk_begin(c + 1, G);
+    const int c_last = c_first + CPW - 1;
+    mfma_slot(0);
+#pragma unroll
+    for (int st = 0; st < RING; ++st) {
+      if constexpr (!FULL) {
+        if (st >= ns) break;
+      }
+      if (st + 1 < RING && (FULL || st + 1 < ns)) {
+        if (st + RA < RING) read_b(st + RA, bq[st + RA], bs[st + RA]);
+        mfma_slot(st + 1);
+      }
+      // Chunk boundaries are multiples of 4 groups and a slot's GS groups
+      // start at a multiple of GS, so chunks close only at slot starts.
+      const int g0 = wg0 + st * GS;
+      while (g0 >= cend && c < c_last) {  // close finished (possibly empty) chunks
+        if (lane < 16) *reinterpret_cast<v4f*>(&red[c][lane][0]) = v4f{p[0], p[1], p[2], p[3]};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) p[q] = 0.f;
+        ++c;
+        cend = chunk_begin(c + 1, G);
+      }
+      // With one MFMA and one FMA per slot (W8, M == 1) the last slot's
+      // result would be read 7 instructions after its MFMA across branches,
+      // one short of the wait states the compiler keeps in straight-line
+      // code; two more are added here, fenced so the scheduler keeps them in
+      // front of the rescale.
+      if constexpr (GS == 1 && ONE) {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 1");
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int jj = 0; jj < GS; ++jj) {
+        // registers of absent tokens hold zeros (their scale entries are
+        // unset and their partials never read)
+        const v4f sc = bs[st][jj];
+#pragma unroll
+        for (int q = 0; q < (ONE ? 1 : 4); ++q) p[q] = __builtin_fmaf((float)D[st][jj][q], sc[q], p[q]);
+      }
     }
   }
   // lane c < 16 holds row c of tokens 0..3 (zero for absent tokens)
