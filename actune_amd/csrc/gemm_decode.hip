@@ -91,10 +91,9 @@ __device__ __forceinline__ int chunk_begin_u(int c, int G) {
 
 // ONE: M == 1 (only register 0 of the MFMA result is rescaled). FULL: every
 // wave's K-range is exactly RING slots (decode_full), so the slot pipeline
-// runs without bounds tests. FULL and ONE together (the decode step's
-// launches) also take exactly the x passes of the K-range, read token
-// operands at constant LDS offsets and keep the group scales in scalar
-// registers.
+// runs without bounds tests. ONE launches read token operands at constant
+// LDS offsets and keep the group scales in scalar registers; with FULL they
+// also issue exactly the x passes of the K-range.
 template <int W, int A, int NW, int RING, int DT, bool SCALE, bool ONE, bool FULL>
 __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, int GW) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -104,8 +103,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   constexpr int ESZ = DT == kF32 ? 4 : 2;
   constexpr int XL = DT == kF32 ? 2 : 1;   // 16-byte loads per 8 elements of x
   constexpr int kPass = kDecodePass;      // x passes (8 group-rows each) loaded before the weights
-  constexpr bool FAST = FULL && ONE;
-  constexpr int NPX = FAST ? (RING * GS + 7) / 8 : kPass;  // x passes issued
+  constexpr bool FAST = ONE;
+  constexpr int NPX = FULL && ONE ? (RING * GS + 7) / 8 : kPass;  // x passes issued
 
   const float fold = __builtin_ldexpf(1.0f, -T);
   // Every kernel argument the prologue needs is read here, in one batch of
@@ -243,7 +242,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   float gsc[FAST ? RING * GS : 1];
 #pragma unroll
   for (int p = 0; p < NPX; ++p) {
-    if (FAST || p < npass) {
+    if ((FULL && ONE) || p < npass) {
       const float sf = convert_x(p, early[p]);
       if constexpr (FAST) {
 #pragma unroll
@@ -259,11 +258,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   float p[4] = {0.f, 0.f, 0.f, 0.f};
   int c = c_first;
   if constexpr (FAST) {
-    // M == 1, every wave's range exactly RING slots: lanes of token 0 (i ==
-    // 0) read the wave's slab, the others the zero region, both with stride
-    // 64 per group, so every token operand read is one LDS load at a
-    // constant offset; the rescale takes its scale from a scalar register.
-    // Same pipeline and order as the general loop below.
+    // M == 1: lanes of token 0 (i == 0) read the wave's slab, the others the
+    // zero region, both with stride 64 per group, so every token operand
+    // read is one LDS load at a constant offset (reads past the wave's range
+    // stay inside LDS and are never used); the rescale takes its scale from
+    // a scalar register. Same pipeline and order as the general loop below.
     constexpr int RA = 3;
     const uint8_t* tbase = (i == 0 ? slab : zero_row) + smallm_slot_k<W>(kb);
     v4u bq[RING][GS];
@@ -289,7 +288,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
     mfma_slot(0);
 #pragma unroll
     for (int st = 0; st < RING; ++st) {
-      if (st + 1 < RING) {
+      if constexpr (!FULL) {
+        if (st >= ns) break;
+      }
+      if (st + 1 < RING && (FULL || st + 1 < ns)) {
         if (st + RA < RING) read_q(st + RA);
         mfma_slot(st + 1);
       }
