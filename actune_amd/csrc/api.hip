@@ -22,8 +22,9 @@ constexpr int kStreamMax = 16;
 constexpr int kStreamConfigs = 3;
 constexpr int kPrefillFirst = kStreamFirst + kStreamConfigs;  // ids 10..13: prefill kernel, any M
 constexpr int kPrefillConfigs = 4;
-constexpr int kDecodeFirst = kPrefillFirst + kPrefillConfigs;  // ids 14..16: decode kernel, M <= 4
-constexpr int kFusedMaxM = 4;      // small-M calls up to this M quantize inside the GEMM
+constexpr int kDecodeFirst = kPrefillFirst + kPrefillConfigs;  // ids 14..16: decode kernel, M <= 8
+constexpr int kDecodeMax = 8;
+constexpr int kFusedMaxM = 4;      // small-M and streaming calls up to this M quantize inside the GEMM
 constexpr int kSmallMWaves[kSmallMConfigs] = {4, 8, 16};
 thread_local char g_err[512];
 // Kernels address every operand through 32-bit buffer offsets and use
@@ -68,7 +69,7 @@ int check_shape(int64_t M, int64_t K, int W, int A, int out_dt, int bias_dt, int
   if (config < kSmallMConfigs && M > kSmallMMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
   if (config >= kStreamFirst && config < kPrefillFirst && M > kStreamMax)
     return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 16");
-  if (config >= kDecodeFirst && M > kFusedMaxM) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 4");
+  if (config >= kDecodeFirst && M > kDecodeMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 8");
   return ACTUNE_OK;
 }
 
@@ -83,6 +84,21 @@ int check_target(const uint8_t* w, const float* ws, const void* out, int64_t N, 
 }
 
 int packed_default(int64_t M, int64_t N, int64_t K, int W, int A);
+
+// Whether a decode-config call quantizes x inside the GEMM. Every workgroup
+// quantizes the whole activation, so the in-launch work grows as row tiles x
+// groups x tokens; measured on MI355X (W4A8, M = 1..8, N = 2048..22016), past
+// about 180 group-rows per SIMD (1024 SIMDs) the quantizer launch followed by
+// the GEMM on its codes is faster. Where the codes path cannot run the
+// decode kernel (M <= 4), the fused small-M kernel runs instead.
+bool decode_light(int64_t M, int64_t n_total, int64_t K) {
+  return ((n_total + 15) / 16) * (K / kGroup) * M <= 180 * 1024;
+}
+
+bool decode_fused(int64_t M, int64_t n_total, int64_t K, int W, int nw, int x_dt) {
+  if (decode_fits((int)K, (int)M, W, nw, false, x_dt) && decode_light(M, n_total, K)) return true;
+  return M <= kFusedMaxM && !decode_fits((int)K, (int)M, W, nw, true, x_dt);
+}
 
 // ACTUNE_CONFIG_AUTO: calls that hand over x (and may fuse the quantizer) use
 // actune_default_config; calls on packed activations use packed_default,
@@ -105,11 +121,12 @@ int add_problem(LinearArgs& g, const uint8_t* w, const float* ws, const void* bi
 // the small-M kernel with the same wave count; results are identical.
 void run_gemm(int W, int A, int config, int mode, const LinearArgs& g, hipStream_t st) {
   if (config >= kDecodeFirst) {
-    // the decode kernel serves the fused mode; packed activations and the
-    // dots mode run the small-M kernel with the same wave count
+    // the decode kernel serves the fused (bf16 x) and packed modes where a
+    // wave's K-range fits its loads; other calls and the dots mode run the
+    // small-M kernel with the same wave count
     const int nw = kSmallMWaves[config - kDecodeFirst];
-    if (mode == kModeFused && decode_fits(g.K, g.M, W, nw)) {
-      launch_decode(W, A, nw, g, st);
+    if (mode != kModeDots && decode_fits(g.K, g.M, W, nw, mode == kModePacked, g.x_dt)) {
+      launch_decode(W, A, nw, mode == kModePacked, g, st);
       return;
     }
     launch_smallm(W, A, nw, mode, g, st);
@@ -170,22 +187,26 @@ int actune_config_valid(int config, int64_t M) {
   if (config < 0 || config >= kNumConfigs) return 0;
   if (config < kSmallMConfigs) return M <= kSmallMMax;
   if (config >= kStreamFirst && config < kPrefillFirst) return M <= kStreamMax;
-  if (config >= kDecodeFirst) return M <= kFusedMaxM;
+  if (config >= kDecodeFirst) return M <= kDecodeMax;
   return 1;
 }
 
 int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
-  // Fused decode (M <= 4, measured on MI355X at W4A8 Llama/Gemma shapes):
-  // the decode kernel beats the small-M and streaming kernels wherever a
-  // wave's K-range fits its load ring. Fewer waves per tile cost less
-  // per-workgroup work, so take the smallest wave count that still gives
-  // every SIMD a wave (tiles x waves >= 1024) and fits K.
-  if (M >= 1 && M <= kFusedMaxM) {
+  // Decode (M <= 8, measured on MI355X at W4A8 Llama/Gemma shapes): the
+  // decode kernel beats the small-M and streaming kernels wherever a wave's
+  // K-range fits its load ring. Fewer waves per tile cost less per-workgroup
+  // work, so take the smallest wave count that still gives every SIMD a wave
+  // (tiles x waves >= 1024) and fits K: first with bf16 x quantized in the
+  // launch where that pays (decode_light), then with the quantizer's codes.
+  if (M >= 1 && M <= kDecodeMax) {
     const int64_t tiles = (N + 15) / 16;
-    for (int c = 0; c < 3; ++c) {
-      const int nw = kSmallMWaves[c];
-      if ((tiles * nw >= 1024 || nw == kSmallMWaves[2]) && decode_fits((int)K, (int)M, W, nw)) return kDecodeFirst + c;
-    }
+    for (int packed = 0; packed < 2; ++packed)
+      for (int c = 0; c < 3; ++c) {
+        const int nw = kSmallMWaves[c];
+        if (!(tiles * nw >= 1024 || nw == kSmallMWaves[2])) continue;
+        if (decode_fits((int)K, (int)M, W, nw, packed, kBF16) && (packed || decode_light(M, N, K)))
+          return kDecodeFirst + c;
+      }
   }
   return packed_default(M, N, K, W, A);
 }
@@ -263,9 +284,10 @@ int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_s
     add_problem(g, targets[t].w, targets[t].w_scale, targets[t].bias, targets[t].out, targets[t].N);
   // The quantizer is fused into the GEMM for M <= 4 on the small-M and
   // streaming kernels (for larger M its per-workgroup cost is no longer
-  // hidden under the weight loads; measured on MI355X).
-  const bool fused = M <= kFusedMaxM &&
-                     (config < kSmallMConfigs || (config >= kStreamFirst && config < kPrefillFirst) || config >= kDecodeFirst);
+  // hidden under the weight loads; measured on MI355X). On the decode
+  // configs decode_fused decides.
+  bool fused = M <= kFusedMaxM && (config < kSmallMConfigs || (config >= kStreamFirst && config < kPrefillFirst));
+  if (config >= kDecodeFirst) fused = decode_fused(M, n_total, K, W, kSmallMWaves[config - kDecodeFirst], x_dtype);
   if (fused) {
     g.x = x;
     g.xscale = input_scale;

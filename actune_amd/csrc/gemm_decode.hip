@@ -1,6 +1,6 @@
-// Decode packed group-64 GEMM for gfx950 (M <= 4 tokens, quantizer fused):
-// the launch is bound by the HBM read of the packed weights, so the kernel is
-// shaped for memory-level parallelism.
+// Decode packed group-64 GEMM for gfx950 (M <= 8 tokens): the launch is bound
+// by the HBM read of the packed weights, so the kernel is shaped to start
+// that read early and keep all of it in flight.
 //
 // Restates the per-call math of actune/kernels/grouped.py:55-94 (group-64
 // quantizer, exact int32 dot per group, fp32 rescale, weight-scale epilogue;
@@ -9,27 +9,26 @@
 //
 // Structure:
 //  * A workgroup is NW waves and owns one 16-row tile of one problem (up to
-//    kMaxProblems linears that read the same x share a launch; the problem
-//    is blockIdx.y, so each workgroup reads only its own problem's kernel
-//    arguments, in the one batch of scalar loads before its first memory
-//    load). The waves
-//    split K along the 16 canonical chunks. Workgroups are light (small LDS,
-//    no per-tile staging), so several are resident per CU and nearly every
-//    tile of a decode-size problem is in flight at once.
-//  * Each wave issues all its loads at entry, unconditionally (lanes and
-//    passes with nothing to read load out of range and get zeros without
-//    memory traffic): kPass x passes, then its whole K-range of weights as
-//    RING 16-byte loads per lane. It then quantizes its K-range of x into a
-//    wave-private LDS slab while the weights arrive. Straight-line loads let
-//    every use wait for exactly its own load (in-order memory counter);
-//    shapes whose K-range per wave needs more loads run the small-M kernel
-//    (decode_fits).
-//  * Weight slots reach MFMA A-operand form with v_permlane32/16_swap and
-//    register unpacking (the small-M kernel's load pattern: lanes of a row
-//    fetch 64 consecutive bytes); the tokens are the B operand, read from the
-//    slab. One fp32 FMA per (row, token, group).
-//  * Chunk partials meet in a small LDS array [16 chunks][16 rows][4 tokens]
-//    and are added in chunk order after one barrier.
+//    kMaxProblems linears that read the same activations share a launch; the
+//    problem is blockIdx.y, so each workgroup reads only its own problem's
+//    kernel arguments, in one batch of scalar loads before its first memory
+//    load). The waves split K along the 16 canonical chunks.
+//  * Each wave issues all its loads at entry: its activation passes, then its
+//    whole K-range of weights as RING 16-byte loads per lane at constant
+//    offsets (lanes of a row fetch 64 consecutive bytes; passes and slots
+//    past the wave's range are switched off and read zeros without memory
+//    traffic). Straight-line loads let every use wait for exactly its own
+//    load (in-order memory counter). It then fills a wave-private LDS slab
+//    with its K-range of the activations as MFMA operand rows while the
+//    weights arrive: bf16 x is quantized in place (fused), packed codes from
+//    the quantizer launch are unpacked (packed).
+//  * The wave walks its slots in a software pipeline: slot s+1's
+//    v_permlane32/16_swap exchange, register unpack and MFMAs are issued
+//    before slot s's results are rescaled. The tokens are the MFMA A operand
+//    (token m of weight row c lands in lane 16*(m/4) + c, register m%4); one
+//    fp32 FMA per (row, token, group) rescales the exact int32 dot.
+//  * Chunk partials meet in LDS [16 chunks][16 rows][MT tokens] and are added
+//    in chunk order after one barrier.
 #include <algorithm>
 
 #include "common.hpp"
@@ -38,11 +37,18 @@
 
 namespace actune {
 
-constexpr int kDecodeMaxM = 4;
+constexpr int kDecodeMaxM = 8;
+// zero region: a wave's widest K-range (16 groups) of 64-byte zero rows
+constexpr int kDecodeZeroBytes = 16 * kGroup;
 
-// Dynamic LDS: per wave a slab [GW groups][M tokens][64 B] and a scale slab
-// [GW][4] (fp32, 2^-(sW+sA) folded in; entries of absent tokens unused), one
-// 64-byte zero row, and the chunk partials red[16][16][kDecodeMaxM].
+// 16-byte weight loads per lane: 16 groups of W2 / W4, 8 groups of W8
+__host__ __device__ constexpr int decode_ring(int W) { return W == 2 ? 4 : 8; }
+// token tile: tokens 0..3 land in lanes 0..15, tokens 4..7 in lanes 16..31
+static int decode_token_tile(int M) { return M <= 4 ? 4 : 8; }
+// activation passes a wave issues up front: fused passes quantize 8
+// group-rows, packed passes unpack 16
+__host__ __device__ constexpr int decode_passes(int MT, bool packed) { return packed ? MT : (MT == 8 ? 8 : 4); }
+
 // Largest groups per wave of a K split over nw waves.
 static int decode_groups_per_wave(int K, int nw) {
   const int G = K / kGroup, cpw = kChunks / nw;
@@ -54,16 +60,6 @@ static int decode_groups_per_wave(int K, int nw) {
   return gw;
 }
 
-// 16-byte weight loads per lane: 16 groups of W2 / W4, 8 groups of W8
-__host__ __device__ constexpr int decode_ring(int W) { return W == 2 ? 4 : 8; }
-constexpr int kDecodePass = 4;   // x passes of 8 group-rows
-
-bool decode_fits(int K, int M, int W, int nw) {
-  const int gw = decode_groups_per_wave(K, nw);
-  return M <= kDecodeMaxM && (gw + 8 / W - 1) / (8 / W) <= decode_ring(W) && gw * M <= 8 * kDecodePass &&
-         decode_lds_bytes(K, M, nw) <= kStreamLdsMax;
-}
-
 // true when every one of nw waves gets exactly a full ring of weight slots
 static bool decode_full(int K, int W, int nw) {
   const int G = K / kGroup, cpw = kChunks / nw, per = decode_ring(W) * (8 / W);
@@ -72,13 +68,22 @@ static bool decode_full(int K, int W, int nw) {
   return true;
 }
 
-// zero region: a wave's widest K-range (16 groups) of 64-byte zero rows
-constexpr int kDecodeZeroBytes = 16 * kGroup;
-
+// Dynamic LDS: per wave a slab [GW groups][M tokens][64 B] and a scale slab
+// [GW][MT] (fp32, 2^-(sW+sA) folded in; entries of absent tokens unused), the
+// zero region, and the chunk partials red[16][16][MT].
 size_t decode_lds_bytes(int K, int M, int nw) {
-  const int gw = decode_groups_per_wave(K, nw);
-  return (size_t)nw * gw * (M * kGroup + 4 * sizeof(float)) + kDecodeZeroBytes +
-         sizeof(float) * kChunks * 16 * kDecodeMaxM;
+  const int gw = decode_groups_per_wave(K, nw), MT = decode_token_tile(M);
+  return (size_t)nw * gw * (M * kGroup + MT * sizeof(float)) + kDecodeZeroBytes + sizeof(float) * kChunks * 16 * MT;
+}
+
+bool decode_fits(int K, int M, int W, int nw, bool packed, int x_dt) {
+  if (!packed && x_dt != kBF16) return false;  // fused mode quantizes bf16 x
+  if (M < 1 || M > kDecodeMaxM || (nw != 4 && nw != 8 && nw != 16)) return false;
+  const int gw = decode_groups_per_wave(K, nw), gps = 8 / W;
+  if ((gw + gps - 1) / gps > decode_ring(W)) return false;
+  const int per = packed ? 16 : 8;
+  if ((gw * M + per - 1) / per > decode_passes(decode_token_tile(M), packed)) return false;
+  return decode_lds_bytes(K, M, nw) <= kStreamLdsMax;
 }
 
 // chunk_begin in unsigned arithmetic (c, G >= 0): shifts instead of the
@@ -89,22 +94,26 @@ __device__ __forceinline__ int chunk_begin_u(int c, int G) {
   return b < (uint32_t)G ? (int)b : G;
 }
 
-// ONE: M == 1 (only register 0 of the MFMA result is rescaled). FULL: every
+// MT: token tile (4 or 8). PACKED: activations come as packed codes +
+// scales (args.a, args.as); otherwise bf16 x (and the bf16 channel scale
+// when SCALE) is quantized here. ONE: M == 1 (only register 0 of a lane's
+// MFMA result can be nonzero); its launches read token operands at constant
+// LDS offsets and keep the group scales in scalar registers. FULL: every
 // wave's K-range is exactly RING slots (decode_full), so the slot pipeline
-// runs without bounds tests. ONE launches read token operands at constant
-// LDS offsets and keep the group scales in scalar registers; with FULL they
-// also issue exactly the x passes of the K-range.
-template <int W, int A, int NW, int RING, int DT, bool SCALE, bool ONE, bool FULL>
+// runs without bounds tests (and a fused ONE launch issues exactly the x
+// passes of the range).
+template <int W, int A, int NW, int RING, int MT, bool PACKED, bool SCALE, bool ONE, bool FULL>
 __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, int GW) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int GS = 8 / W;                // groups per 16-byte weight load per lane
   constexpr int CPW = kChunks / NW;        // canonical chunks per wave
   constexpr int T = shift_of(W) + shift_of(A);
-  constexpr int ESZ = DT == kF32 ? 4 : 2;
-  constexpr int XL = DT == kF32 ? 2 : 1;   // 16-byte loads per 8 elements of x
-  constexpr int kPass = kDecodePass;      // x passes (8 group-rows each) loaded before the weights
+  constexpr int DT = kBF16;
+  constexpr int ESZ = 2;
   constexpr bool FAST = ONE;
-  constexpr int NPX = FULL && ONE ? (RING * GS + 7) / 8 : kPass;  // x passes issued
+  constexpr int PR = PACKED ? 16 : 8;      // group-rows per activation pass
+  constexpr int NPX = FULL && ONE && !PACKED ? (RING * GS + 7) / 8 : decode_passes(MT, PACKED);
+  static_assert(!ONE || MT == 4, "M == 1 uses the 4-token tile");
 
   const float fold = __builtin_ldexpf(1.0f, -T);
   // Every kernel argument the prologue needs is read here, in one batch of
@@ -114,10 +123,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   // The problem is blockIdx.y: its fields sit at an offset known at entry.
   Problem pr = args.prob[blockIdx.y];
   int M = args.M, K = args.K, bias_dt = args.bias_dt, out_dt = args.out_dt;
-  uint32_t m_inv = args.m_div;  // idx / M == (idx * m_inv) >> 16 here
-  const void* xsrc = args.x;
-  const void* xscale = args.xscale;
-  asm volatile("" : "+s"(M), "+s"(K), "+s"(bias_dt), "+s"(out_dt), "+s"(m_inv), "+s"(xsrc), "+s"(xscale), "+s"(GW),
+  uint32_t m_inv = args.m_div;  // r / M == (r * m_inv) >> 16 for the row indices here
+  const void* xsrc = PACKED ? static_cast<const void*>(args.a) : args.x;
+  const void* xaux = PACKED ? static_cast<const void*>(args.as) : args.xscale;
+  asm volatile("" : "+s"(M), "+s"(K), "+s"(bias_dt), "+s"(out_dt), "+s"(m_inv), "+s"(xsrc), "+s"(xaux), "+s"(GW),
                     "+s"(pr.w), "+s"(pr.ws), "+s"(pr.bias), "+s"(pr.out), "+s"(pr.N));
   const int N = pr.N, G = K / kGroup;
   const int n0 = (int)blockIdx.x * 16;
@@ -136,76 +145,98 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   const int ns = (ng + GS - 1) / GS;        // weight steps of this wave
 
   uint8_t* slab = smem + (size_t)wave * GW * M * kGroup;
-  float* sslab = reinterpret_cast<float*>(smem + (size_t)NW * GW * M * kGroup) + (size_t)wave * GW * 4;
+  float* sslab = reinterpret_cast<float*>(smem + (size_t)NW * GW * M * kGroup) + (size_t)wave * GW * MT;
   uint8_t* zero_row = reinterpret_cast<uint8_t*>(reinterpret_cast<float*>(smem + (size_t)NW * GW * M * kGroup) +
-                                                 (size_t)NW * GW * 4);
-  float (*red)[16][kDecodeMaxM] = reinterpret_cast<float (*)[16][kDecodeMaxM]>(zero_row + kDecodeZeroBytes);
+                                                 (size_t)NW * GW * MT);
+  float* red = reinterpret_cast<float*>(zero_row + kDecodeZeroBytes);  // [chunk][row][MT]
 
-  // The output this thread finishes in the epilogue (wave 0: row lane / 4,
-  // token lane % 4).
+  // Wave 0 finishes output row lane / 4 for tokens lane % 4 + 4j.
   const int e_row = lane >> 2, e_m = lane & 3;
 
-  // ---------------------------------------------------------------- x loads
-  // Group-row r = gl * M + m (gl: group of the wave's range, m: token); a
-  // pass covers 8 group-rows, 8 lanes each, 8 consecutive elements per lane.
+  // ---------------------------------------------------------------- activation loads
+  // Group-row r = gl * M + m (gl: group of the wave's range, m: token).
   const int rows_here = ng * M;
-  const int npass = (rows_here + 7) / 8;
-  const Rsrc xres = make_rsrc(xsrc, (uint32_t)M * K * ESZ);
-  const Rsrc xsres = make_rsrc(SCALE ? xscale : xsrc, (uint32_t)K * ESZ);
+  const int npass = (rows_here + PR - 1) / PR;
+  struct Raw { v4u x, s; uint32_t q[4]; float sc; };
+  // fused: a pass covers 8 group-rows, 8 lanes each, 8 consecutive elements
+  // per lane
+  const Rsrc xres = make_rsrc(xsrc, PACKED ? (uint32_t)M * K * A / 8 : (uint32_t)M * K * ESZ);
+  const Rsrc xsres = make_rsrc(PACKED || SCALE ? xaux : xsrc, PACKED ? (uint32_t)(M * G) * 4u : (uint32_t)K * ESZ);
   const int seg = lane & 7;
-  struct Raw { v4u x[XL], s[XL]; };
   // M == 1: lane l of pass p reads elements wg0*64 + p*512 + 8l.. of x (the
   // rows past the wave's range read neighbouring elements or zeros and are
   // not stored); the pass is a constant offset, passes past npass are
   // switched off through the scalar offset.
   const uint32_t xbase1 = ((uint32_t)wg0 * kGroup + (uint32_t)lane * 8) * ESZ;
-  auto issue_x = [&](int pass, Raw& r) {
-    if constexpr (ONE) {
+  // packed: a pass covers 16 group-rows; lane (row lane / 4, k-slot lane % 4)
+  constexpr int CB = 16 * A / 8;            // bytes of one 16-code slot
+  const uint32_t arow_bytes = (uint32_t)K * A / 8;
+  auto row_of = [&](int r, int& gl, int& m) {
+    gl = ONE ? r : (int)(((uint32_t)r * m_inv) >> 16);
+    m = ONE ? 0 : r - gl * M;
+  };
+  auto issue_x = [&](int pass, Raw& raw) {
+    if constexpr (PACKED) {
+      const int r = pass * 16 + (lane >> 2), j = lane & 3;
+      const bool live = r < rows_here;
+      int gl, m;
+      row_of(live ? r : 0, gl, m);
+      buffer_slot<A>(xres, live ? (uint32_t)m * arow_bytes + (uint32_t)((wg0 + gl) * 4 + j) * CB : kOff, raw.q);
+      raw.sc = buffer_f32(xsres, live && j == 0 ? ((uint32_t)m * G + wg0 + gl) * 4u : kOff);
+    } else if constexpr (ONE) {
       const uint32_t soff = pass < npass ? 0u : kOff;
-#pragma unroll
-      for (int h = 0; h < XL; ++h) {
-        r.x[h] = __builtin_amdgcn_raw_buffer_load_b128(xres, xbase1 + (uint32_t)(pass * 512 * ESZ + 16 * h), soff, 0);
-        if constexpr (SCALE)
-          r.s[h] = __builtin_amdgcn_raw_buffer_load_b128(xsres, xbase1 + (uint32_t)(pass * 512 * ESZ + 16 * h), soff, 0);
+      raw.x = __builtin_amdgcn_raw_buffer_load_b128(xres, xbase1 + (uint32_t)(pass * 512 * ESZ), soff, 0);
+      if constexpr (SCALE) raw.s = __builtin_amdgcn_raw_buffer_load_b128(xsres, xbase1 + (uint32_t)(pass * 512 * ESZ), soff, 0);
+    } else {
+      const int r = pass * 8 + (lane >> 3);
+      const bool live = r < rows_here;
+      int gl, m;
+      row_of(live ? r : 0, gl, m);
+      const uint32_t k0 = (uint32_t)((wg0 + gl) * kGroup + seg * 8);
+      raw.x = __builtin_amdgcn_raw_buffer_load_b128(xres, live ? ((uint32_t)m * K + k0) * ESZ : kOff, 0, 0);
+      if constexpr (SCALE) raw.s = __builtin_amdgcn_raw_buffer_load_b128(xsres, live ? k0 * ESZ : kOff, 0, 0);
+    }
+  };
+  // Slab row r gets its operand slots; returns the group scale s * 2^-T (the
+  // same in the lanes of a group-row).
+  auto convert_x = [&](int pass, const Raw& raw) -> float {
+    if constexpr (PACKED) {
+      const int r = pass * 16 + (lane >> 2), j = lane & 3;
+      const float sf = raw.sc * fold;
+      if (r < rows_here) {
+        int gl, m;
+        row_of(r, gl, m);
+        uint32_t d[4];
+        unpack_slot<A>(raw.q, d);
+        reorder_slot<A, W>(d);
+        *reinterpret_cast<v4u*>(slab + (size_t)r * kGroup + 16 * j) = v4u{d[0], d[1], d[2], d[3]};
+        if (!FAST && j == 0) sslab[gl * MT + m] = sf;
       }
-      return;
-    }
-    const int idx = pass * 8 + (lane >> 3);
-    const bool live = idx < rows_here;
-    const int q = ONE ? idx : (int)(((uint32_t)idx * m_inv) >> 16);
-    const int gl = live ? q : 0, m = ONE || !live ? 0 : idx - q * M;
-    const uint32_t k0 = (uint32_t)((wg0 + gl) * kGroup + seg * 8);
-    const uint32_t xo = live ? ((uint32_t)m * K + k0) * ESZ : kOff;
+      return sf;
+    } else {
+      const int r = pass * 8 + (lane >> 3);
+      const bool live = r < rows_here;
+      float v[8];
+      unpack8<DT>(raw.x, raw.x, v);
+      if constexpr (SCALE) {
+        float d[8];
+        unpack8<DT>(raw.s, raw.s, d);
 #pragma unroll
-    for (int h = 0; h < XL; ++h) r.x[h] = __builtin_amdgcn_raw_buffer_load_b128(xres, xo == kOff ? kOff : xo + 16 * h, 0, 0);
-    if constexpr (SCALE) {
-      const uint32_t so = live ? k0 * ESZ : kOff;
-#pragma unroll
-      for (int h = 0; h < XL; ++h) r.s[h] = __builtin_amdgcn_raw_buffer_load_b128(xsres, so == kOff ? kOff : so + 16 * h, 0, 0);
+        for (int e = 0; e < 8; ++e) v[e] = live ? round_to_dtype<DT>(v[e] / d[e]) : 0.0f;
+      }
+      // every lane joins the group max, live or not
+      uint32_t cq[8];
+      const float s = group_code_bits<A, DT>(v, cq);
+      if (live) {
+        int gl, m;
+        row_of(r, gl, m);
+        store_half_slot<W, A>(slab + (size_t)r * kGroup + (seg >> 1) * 16, seg & 1, cq);
+        if (!FAST && seg == 0) sslab[gl * MT + m] = s * fold;
+      }
+      return s * fold;
     }
   };
-  auto convert_x = [&](int pass, const Raw& r) {
-    const int idx = pass * 8 + (lane >> 3);
-    const bool live = idx < rows_here;
-    const int q = ONE ? idx : (int)(((uint32_t)idx * m_inv) >> 16);
-    const int gl = live ? q : 0, m = ONE || !live ? 0 : idx - q * M;
-    float v[8];
-    unpack8<DT>(r.x[0], r.x[XL - 1], v);
-    if constexpr (SCALE) {
-      float d[8];
-      unpack8<DT>(r.s[0], r.s[XL - 1], d);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = live ? round_to_dtype<DT>(v[e] / d[e]) : 0.0f;
-    }
-    uint32_t cq[8];
-    const float s = group_code_bits<A, DT>(v, cq);
-    if (live) {
-      store_half_slot<W, A>(slab + (gl * M + m) * kGroup + (seg >> 1) * 16, seg & 1, cq);
-      if (!FAST && seg == 0) sslab[gl * 4 + m] = s * fold;
-    }
-    return s * fold;  // the same in the 8 lanes of a group
-  };
-  Raw early[kPass];
+  Raw early[NPX];
 #pragma unroll
   for (int p = 0; p < NPX; ++p) issue_x(p, early[p]);
 
@@ -217,7 +248,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   // range are switched off through the scalar offset (the vector offset
   // stays below 2^31, so the sum cannot wrap).
   const uint32_t wbase = (uint32_t)(n0 + i) * wrow_bytes + kb * 16 + (uint32_t)wg0 * 8 * W;
-  // the host guarantees ns <= RING and npass <= kPass (decode_fits)
+  // the host guarantees ns <= RING and npass <= NPX (decode_fits)
   uint32_t ring[RING][4];
 #pragma unroll
   for (int st = 0; st < RING; ++st) {
@@ -230,24 +261,25 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   // epilogue constants, behind the weights: they are needed last, by wave 0.
   // Every wave issues the two loads (switched off outside wave 0) so that all
   // waves have the same loads in flight: behind a branch, the compiler's
-  // waits for the x passes would count from the shorter path and make wave 0
-  // wait for weight slots before quantizing.
-  const ChannelConst cc = fetch_channel(pr.ws, pr.bias, bias_dt, N, n0 + e_row, wave == 0 && e_m < M);
+  // waits for the activation passes would count from the shorter path and
+  // make wave 0 wait for weight slots before quantizing.
+  const ChannelConst cc = fetch_channel(pr.ws, pr.bias, bias_dt, N, n0 + e_row, wave == 0);
 
-  // ---------------------------------------------------------------- quantize x
+  // ---------------------------------------------------------------- activation slab
   // the zero region: one dword per thread of the first four waves
   if (threadIdx.x < kDecodeZeroBytes / 4) reinterpret_cast<uint32_t*>(zero_row)[threadIdx.x] = 0u;
   // FAST: the wave's group scales (s * 2^-T, wave-uniform) move from the
-  // quantizing lanes into scalar registers
+  // lanes that computed or loaded them into scalar registers
   float gsc[FAST ? RING * GS : 1];
 #pragma unroll
   for (int p = 0; p < NPX; ++p) {
-    if ((FULL && ONE) || p < npass) {
+    if ((FULL && ONE && !PACKED) || p < npass) {
       const float sf = convert_x(p, early[p]);
       if constexpr (FAST) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (p * 8 + j < RING * GS) gsc[p * 8 + j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sf), 8 * j));
+        for (int j = 0; j < PR; ++j)
+          if (p * PR + j < RING * GS)
+            gsc[p * PR + j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sf), (64 / PR) * j));
       }
     }
   }
@@ -257,6 +289,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   // ---------------------------------------------------------------- stream the K-range
   float p[4] = {0.f, 0.f, 0.f, 0.f};
   int c = c_first;
+  // partials: lane l holds rows l % 16 of tokens 4*(l/16)..+3; the lanes of
+  // the token tile write them
+  const bool writer = lane < 16 * (MT / 4);
+  float* red_lane = red + (size_t)(lane & 15) * MT + 4 * ((lane >> 4) & (MT / 4 - 1));
   if constexpr (FAST) {
     // M == 1: lanes of token 0 (i == 0) read the wave's slab, the others the
     // zero region, both with stride 64 per group, so every token operand
@@ -297,7 +333,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
       }
       const int g0 = wg0 + st * GS;
       while (g0 >= cend && c < c_last) {  // close finished (possibly empty) chunks
-        if (lane < 16) *reinterpret_cast<v4f*>(&red[c][lane][0]) = v4f{p[0], 0.f, 0.f, 0.f};
+        if (lane < 16) *reinterpret_cast<v4f*>(red_lane + (size_t)c * 16 * MT) = v4f{p[0], 0.f, 0.f, 0.f};
         p[0] = 0.f;
         ++c;
         cend = chunk_begin_u(c + 1, G);
@@ -311,32 +347,33 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
       for (int jj = 0; jj < GS; ++jj) p[0] = __builtin_fmaf((float)D[st][jj][0], gsc[st * GS + jj], p[0]);
     }
   } else {
-    // The tokens are the MFMA A operand and the weight rows the B operand, so
-    // token m of weight row c lands in lane c, register m: only M registers of
-    // lanes 0..15 carry results and only those are rescaled. The GS MFMAs of a
-    // slot are issued together and folded in group order.
+    // The GS MFMAs of a slot are issued together and folded in group order.
     const int slot_k = smallm_slot_k<W>(kb);
     // Lanes of absent tokens (i >= M) read the zero row with stride 0. A group
     // past the wave's range (the tail of its last slot, or a slot read ahead
     // and never used) reads a clamped slab row and a zero scale, so it adds
-    // exactly nothing.
+    // exactly nothing. Lane l rescales tokens 4*(l/16) + q; lanes past the
+    // token tile read the first tokens' scales against zero MFMA rows.
     const bool tok = i < M;
     const uint8_t* bbase = tok ? slab + i * kGroup + slot_k : zero_row;
     const uint32_t bstride = tok ? (uint32_t)M * kGroup : 0u;
+    const float* sbase = sslab + 4 * ((lane >> 4) & (MT / 4 - 1));
     auto read_b = [&](int st, v4u (&bq)[GS], v4f (&bs)[GS]) {
 #pragma unroll
       for (int jj = 0; jj < GS; ++jj) {
         const int gl = max(0, min(st * GS + jj, ng - 1));
         bq[jj] = *reinterpret_cast<const v4u*>(bbase + __umul24((uint32_t)gl, bstride));
-        const float* srow = st * GS + jj < ng ? sslab + gl * 4 : reinterpret_cast<const float*>(zero_row);
-        bs[jj] = *reinterpret_cast<const v4f*>(srow);  // same address in every lane
+        const float* srow = st * GS + jj < ng ? sbase + gl * MT : reinterpret_cast<const float*>(zero_row);
+        bs[jj] = *reinterpret_cast<const v4f*>(srow);
       }
     };
     // Software pipeline over the wave's ns slots: slot st+1's MFMAs are issued
     // before slot st's results are rescaled, so MFMA latency hides under that
-    // work. Token operands are read three slots ahead. (Slot 0's MFMAs run
-    // even when the wave has no slot: its weights and scales are zero.)
-    constexpr int RA = 3;
+    // work. Token operands are read three slots ahead (one for W2 at 16
+    // waves, whose 4-group slots would not fit 128 registers three deep).
+    // (Slot 0's MFMAs run even when the wave has no slot: its weights and
+    // scales are zero.)
+    constexpr int RA = GS == 4 && NW == 16 ? 1 : 3;
     v4u bq[RING][GS];
     v4f bs[RING][GS];
     v4i D[RING][GS];
@@ -368,21 +405,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
       // start at a multiple of GS, so chunks close only at slot starts.
       const int g0 = wg0 + st * GS;
       while (g0 >= cend && c < c_last) {  // close finished (possibly empty) chunks
-        if (lane < 16) *reinterpret_cast<v4f*>(&red[c][lane][0]) = v4f{p[0], p[1], p[2], p[3]};
+        if (writer) *reinterpret_cast<v4f*>(red_lane + (size_t)c * 16 * MT) = v4f{p[0], p[1], p[2], p[3]};
 #pragma unroll
         for (int q = 0; q < 4; ++q) p[q] = 0.f;
         ++c;
         cend = chunk_begin(c + 1, G);
-      }
-      // With one MFMA and one FMA per slot (W8, M == 1) the last slot's
-      // result would be read 7 instructions after its MFMA across branches,
-      // one short of the wait states the compiler keeps in straight-line
-      // code; two more are added here, fenced so the scheduler keeps them in
-      // front of the rescale.
-      if constexpr (GS == 1 && ONE) {
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_nop 1");
-        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int jj = 0; jj < GS; ++jj) {
@@ -390,40 +417,44 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
         // unset and their partials never read)
         const v4f sc = bs[st][jj];
 #pragma unroll
-        for (int q = 0; q < (ONE ? 1 : 4); ++q) p[q] = __builtin_fmaf((float)D[st][jj][q], sc[q], p[q]);
+        for (int q = 0; q < 4; ++q) p[q] = __builtin_fmaf((float)D[st][jj][q], sc[q], p[q]);
       }
     }
   }
-  // lane c < 16 holds row c of tokens 0..3 (zero for absent tokens)
   for (; c < c_first + CPW; ++c) {
-    if (lane < 16) *reinterpret_cast<v4f*>(&red[c][lane][0]) = v4f{p[0], p[1], p[2], p[3]};
+    if (writer) *reinterpret_cast<v4f*>(red_lane + (size_t)c * 16 * MT) = v4f{p[0], p[1], p[2], p[3]};
 #pragma unroll
     for (int q = 0; q < 4; ++q) p[q] = 0.f;
   }
   __syncthreads();
 
   // ---------------------------------------------------------------- epilogue
-  if (wave == 0 && e_m < M) {
+  if (wave == 0) {
     const int n = n0 + e_row;
-    float acc = red[0][e_row][e_m];
 #pragma unroll
-    for (int q = 1; q < kChunks; ++q) acc = acc + red[q][e_row][e_m];
-    if (n < N) {
-      const float y = finish_const(acc, cc, pr.bias != nullptr, bias_dt);
-      const long o = (long)e_m * N + n;
-      if (out_dt == kBF16) store_out<kBF16>(pr.out, o, y);
-      else if (out_dt == kF16) store_out<kF16>(pr.out, o, y);
-      else store_out<kF32>(pr.out, o, y);
+    for (int jt = 0; jt < MT / 4; ++jt) {
+      const int m = e_m + 4 * jt;
+      if (m < M && n < N) {
+        const float* rr = red + (size_t)e_row * MT + m;
+        float acc = rr[0];
+#pragma unroll
+        for (int q = 1; q < kChunks; ++q) acc = acc + rr[(size_t)q * 16 * MT];
+        const float y = finish_const(acc, cc, pr.bias != nullptr, bias_dt);
+        const long o = (long)m * N + n;
+        if (out_dt == kBF16) store_out<kBF16>(pr.out, o, y);
+        else if (out_dt == kF16) store_out<kF16>(pr.out, o, y);
+        else store_out<kF32>(pr.out, o, y);
+      }
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-template <int W, int A, int NW, int DT, bool SCALE, bool ONE, bool FULL>
+template <int W, int A, int NW, int MT, bool PACKED, bool SCALE, bool ONE, bool FULL>
 static void launch_decode_one(const LinearArgs& g, hipStream_t st) {
   constexpr int RING = decode_ring(W);
   const size_t lds = decode_lds_bytes(g.K, g.M, NW);
-  auto kern = gemm_decode<W, A, NW, RING, DT, SCALE, ONE, FULL>;
+  auto kern = gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL>;
   static bool attr_set = false;  // allow dynamic LDS beyond the default per-launch limit
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -436,41 +467,39 @@ static void launch_decode_one(const LinearArgs& g, hipStream_t st) {
 }
 
 template <int W, int A, int NW>
-static void launch_decode_nw(const LinearArgs& g, hipStream_t st) {
-#define DEC_ONE(DTV, SC)                                                        \
-  if (g.M == 1) launch_decode_one<W, A, NW, DTV, SC, true, false>(g, st);       \
-  else launch_decode_one<W, A, NW, DTV, SC, false, false>(g, st)
-  // bf16 activations of shapes whose waves each fill the ring exactly take
-  // the bound-free pipeline
-  if (g.x_dt == kBF16 && decode_full(g.K, W, NW)) {
-    if (g.xscale) {
-      if (g.M == 1) launch_decode_one<W, A, NW, kBF16, true, true, true>(g, st);
-      else launch_decode_one<W, A, NW, kBF16, true, false, true>(g, st);
-    } else {
-      if (g.M == 1) launch_decode_one<W, A, NW, kBF16, false, true, true>(g, st);
-      else launch_decode_one<W, A, NW, kBF16, false, false, true>(g, st);
-    }
+static void launch_decode_nw(bool packed, const LinearArgs& g, hipStream_t st) {
+  const bool full = decode_full(g.K, W, NW), scale = g.xscale != nullptr;
+  if (packed) {
+    if (g.M == 1) launch_decode_one<W, A, NW, 4, true, false, true, false>(g, st);
+    else if (g.M <= 4) launch_decode_one<W, A, NW, 4, true, false, false, false>(g, st);
+    else launch_decode_one<W, A, NW, 8, true, false, false, false>(g, st);
     return;
   }
-#define DEC_DT(DTV)                                                             \
-  if (g.xscale) { DEC_ONE(DTV, true); }                                         \
-  else { DEC_ONE(DTV, false); }
-  if (g.x_dt == kBF16) { DEC_DT(kBF16); }
-  else if (g.x_dt == kF16) { DEC_DT(kF16); }
-  else { DEC_DT(kF32); }
-#undef DEC_DT
-#undef DEC_ONE
+#define DEC_FULL(MTV, SC, ONEV)                                                 \
+  if (full) launch_decode_one<W, A, NW, MTV, false, SC, ONEV, true>(g, st);     \
+  else launch_decode_one<W, A, NW, MTV, false, SC, ONEV, false>(g, st)
+  if (g.M == 1) {
+    if (scale) { DEC_FULL(4, true, true); }
+    else { DEC_FULL(4, false, true); }
+  } else if (g.M <= 4) {
+    if (scale) { DEC_FULL(4, true, false); }
+    else { DEC_FULL(4, false, false); }
+  } else {
+    if (scale) launch_decode_one<W, A, NW, 8, false, true, false, false>(g, st);
+    else launch_decode_one<W, A, NW, 8, false, false, false, false>(g, st);
+  }
+#undef DEC_FULL
 }
 
 template <int W, int A>
-static void launch_decode_wa(int nw, const LinearArgs& g, hipStream_t st) {
-  if (nw == 4) launch_decode_nw<W, A, 4>(g, st);
-  else if (nw == 8) launch_decode_nw<W, A, 8>(g, st);
-  else launch_decode_nw<W, A, 16>(g, st);
+static void launch_decode_wa(int nw, bool packed, const LinearArgs& g, hipStream_t st) {
+  if (nw == 4) launch_decode_nw<W, A, 4>(packed, g, st);
+  else if (nw == 8) launch_decode_nw<W, A, 8>(packed, g, st);
+  else launch_decode_nw<W, A, 16>(packed, g, st);
 }
 
-void launch_decode(int W, int A, int nw, const LinearArgs& g, hipStream_t st) {
-#define CASE(WB, AB) if (W == WB && A == AB) return launch_decode_wa<WB, AB>(nw, g, st)
+void launch_decode(int W, int A, int nw, bool packed, const LinearArgs& g, hipStream_t st) {
+#define CASE(WB, AB) if (W == WB && A == AB) return launch_decode_wa<WB, AB>(nw, packed, g, st)
   CASE(8, 8); CASE(8, 4); CASE(8, 2);
   CASE(4, 8); CASE(4, 4); CASE(4, 2);
   CASE(2, 8); CASE(2, 4); CASE(2, 2);

@@ -68,11 +68,14 @@ void launch_smallm(int W, int A, int nw, int mode, const LinearArgs& g, hipStrea
 void launch_tiled(int W, int A, int shape, bool dots, const LinearArgs& g, hipStream_t st);
 void launch_stream(int W, int A, int nw, int mode, const LinearArgs& g, hipStream_t st);
 void launch_prefill(int W, int A, int shape, bool dots, const LinearArgs& g, hipStream_t st);
-void launch_decode(int W, int A, int nw, const LinearArgs& g, hipStream_t st);
+// packed: the activations are codes + scales from the quantizer launch
+// (g.a, g.as); otherwise bf16 x is quantized inside the launch (g.x)
+void launch_decode(int W, int A, int nw, bool packed, const LinearArgs& g, hipStream_t st);
 size_t decode_lds_bytes(int K, int M, int nw);
 // true when the decode kernel with nw waves takes an M x K problem of width W
-// (every wave's loads fit its register ring and x passes)
-bool decode_fits(int K, int M, int W, int nw);
+// in the given activation mode (every wave's loads fit its register ring and
+// activation passes; the fused mode takes bf16 x only)
+bool decode_fits(int K, int M, int W, int nw, bool packed, int x_dt);
 size_t stream_lds_bytes(int K, int M, int nw);
 
 }  // namespace actune

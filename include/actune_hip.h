@@ -90,8 +90,10 @@ int actune_grouped_forward(const void* x, int x_dtype, const void* input_scale, 
  * group-64 path; it mirrors the sibling-projection grouping of the
  * reference's tokenwise decode path (actune/kernels/decode_w4a8_triton.py:152-239).
  * The quantizer runs inside the GEMM (a_buf / scale_buf are then not
- * written) for M <= 4 on the small-M and streaming configs; otherwise
- * a_buf / scale_buf receive the packed activations and scales.
+ * written) for M <= 4 on the small-M and streaming configs and, on the
+ * decode configs, for bf16 x wherever the decode kernel's activation passes
+ * cover a wave's K-range; otherwise a_buf / scale_buf receive the packed
+ * activations and scales.
  */
 int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_scale, uint8_t* a_buf,
                                  float* scale_buf, const actune_linear_target* targets, int ntargets,
@@ -115,9 +117,10 @@ int actune_grouped_dots_i32(const uint8_t* a, const uint8_t* w, int64_t M, int64
  *   7, 8, 9  persistent streaming kernel with 4, 8, 16 waves (M <= 16)
  *   10 .. 13 prefill kernel (weights streamed per wave, activations staged
  *            per workgroup) with tiles 128x64, 128x32, 64x64, 64x32 (any M)
- *   14 .. 16 decode kernel with 4, 8, 16 waves (M <= 4, quantizer fused;
- *            a K too long for a wave's load ring, packed activations and
- *            the dots mode run the small-M kernel with the same waves)
+ *   14 .. 16 decode kernel with 4, 8, 16 waves (M <= 8; bf16 x quantized
+ *            in the launch, other dtypes and longer K-ranges through the
+ *            quantizer launch; a K too long for a wave's load ring and the
+ *            dots mode run the small-M kernel with the same waves)
  * actune_config_valid: 1 if `config` can run a call with M rows.
  * actune_default_config: the config ACTUNE_CONFIG_AUTO resolves to in
  *   actune_grouped_forward(_multi). actune_grouped_linear and

@@ -185,35 +185,39 @@ def test_full_size_sampled_parity(m, n, k, W, A):
 
 # ---------------------------------------------------------------- fused / siblings
 @pytest.mark.parametrize("W,A", PAIRS)
-@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_fused_small_m_equals_two_step(W, A, m, dtype):
-    """M <= 4 quantizes inside the GEMM; it must equal quantize + GEMM and the
-    oracle bit for bit, with and without the fused channel scale."""
+    """Small-M (fused for M <= 4) and decode configs (fused for bf16 x up to
+    M = 8, quantizer launch + packed codes otherwise): forward on x and the
+    GEMM on the quantizer's codes both equal the oracle bit for bit, with and
+    without the fused channel scale."""
     k, n = 704, 80  # G = 11: ragged chunks and a partial weight step
     x, w, b = seeded_inputs(m, k, n, seed=W * A + m, dtype=dtype, bias=True)
     _, _, w_dev, ws_dev = _packed_weight(w, W, A)
     xd, bd = x.to(DEV), b.to(DEV)
+    wc, wsc = oracle_weight(w, W, A)
     for scale in (None, torch.linspace(0.5, 2.0, k).to(dtype)):
         sd = None if scale is None else scale.to(DEV)
+        a_packed, a_scales, a_codes = oracle_activation(x, A, scale)
+        want = O.round_out(O.linear(a_codes, a_scales, wc, wsc, b.float().numpy(), bounds=canonical_bounds(k // 64)),
+                           dtype_name(dtype))
+        p, s = _native.quantize_groups(xd, A, sd)
         for config in (0, 1, 2, 14, 15, 16):  # small-M and decode kernels
             fused = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, input_scale=sd, config=config)
-            p, s = _native.quantize_groups(xd, A, sd)
             two = _native.grouped_linear(p, s, w_dev, ws_dev, bd, xd, W, A, config)
             assert torch.equal(fused, two), (config, scale is None)
-        a_packed, a_scales, a_codes = oracle_activation(x, A, scale)
-        wc, wsc = oracle_weight(w, W, A)
-        want = O.linear(a_codes, a_scales, wc, wsc, b.float().numpy(), bounds=canonical_bounds(k // 64))
-        np.testing.assert_array_equal(bits(fused), O.round_out(want, dtype_name(dtype)))
+            np.testing.assert_array_equal(bits(fused), want, err_msg=f"config {config}")
 
 
 @pytest.mark.parametrize("W,A", [(4, 8), (2, 4), (8, 8), (8, 2)])
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 4, 8])
 @pytest.mark.parametrize("k", [4096, 8192, 11008])
 def test_decode_full_ring_equals_small_m(W, A, m, k):
     """Decode configs at K where a wave's weight range fills its load ring
     (and, for K = 11008 with 4 or 8 waves, exceeds it: those run the small-M
-    kernel) equal the small-M kernel bit for bit, with a ragged N."""
+    kernel; at M = 8 the longer ranges take the quantizer's codes) equal the
+    small-M kernel bit for bit, with a ragged N."""
     n = 72
     x, w, b = seeded_inputs(m, k, n, seed=k + W * A + m, bias=True)
     _, _, w_dev, ws_dev = _packed_weight(w, W, A)
@@ -225,7 +229,7 @@ def test_decode_full_ring_equals_small_m(W, A, m, k):
 
 
 @pytest.mark.parametrize("W,A", [(4, 8), (2, 2), (8, 4), (4, 4)])
-@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("m", [1, 3, 6, 8])
 def test_decode_full_ring_with_channel_scale(W, A, m):
     """K = 4096: every wave of the 4-wave (W2/W4) or 8-wave (W8) decode
     config fills its load ring exactly, which runs the bound-free slot

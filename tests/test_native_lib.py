@@ -40,7 +40,7 @@ def test_config_table():
     assert _native.config_valid(0, 64) and not _native.config_valid(0, 65)
     assert all(_native.config_valid(c, 4096) for c in range(3, 7))
     assert all(_native.config_valid(c, 1) and _native.config_valid(c, 4096) for c in range(10, 14))
-    assert all(_native.config_valid(c, 4) and not _native.config_valid(c, 5) for c in range(14, 17))
+    assert all(_native.config_valid(c, 8) and not _native.config_valid(c, 9) for c in range(14, 17))
     assert _native.config_valid(9, 16) and not _native.config_valid(9, 17)
     assert not _native.config_valid(n, 1) and not _native.config_valid(-2, 1)
     for m in (1, 8, 16, 17, 50, 512):
@@ -53,6 +53,15 @@ def test_config_table():
     assert _native.default_config(1, 4096, 4096, 8, 8) == 15   # W8: 8 groups per ring
     assert _native.default_config(1, 1024, 4096, 4, 8) == 16   # 64 tiles: 16 waves each
     assert _native.default_config(1, 4096, 65536, 4, 8) == 2   # no decode config fits
+    # M = 8: 8 waves quantize their 8 groups x 8 tokens in the launch; for
+    # K = 11008 no wave count both fits its ring and quantizes its range, so
+    # 16 waves take the quantizer's codes
+    assert _native.default_config(8, 4096, 4096, 4, 8) == 15
+    assert _native.default_config(8, 4096, 11008, 4, 8) == 16
+    # wide N: every workgroup would quantize all of x, so 4 waves take codes
+    assert _native.default_config(8, 11008, 4096, 4, 8) == 14
+    assert _native.default_config(3, 11008, 4096, 4, 8) == 15  # still fused
+    assert _native.default_config(9, 4096, 4096, 4, 8) not in (14, 15, 16)
 
 
 def _err():
