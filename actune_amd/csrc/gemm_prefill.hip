@@ -24,10 +24,11 @@
 //    double-buffered: one barrier per quad.
 //  * The MFMAs of group g are issued in the same block as the rescale of
 //    group g-1, so the matrix and vector pipes of a SIMD run side by side.
-//  * Weight loads run DW = 4 quads ahead in a register ring, activation loads
-//    DA = 2 quads ahead of their LDS store: the rows a workgroup streams are
-//    fetched together by the workgroups of its XCD that share them, so each
-//    load sees HBM latency and needs thousands of cycles of lead.
+//  * Weight loads run DW = 2 quads ahead in a register ring, activation loads
+//    DA = 1 quad ahead of their LDS store (a quad takes over a microsecond:
+//    enough lead for loads that miss L2). Shallow rings keep the 64x64 tile
+//    at 162 VGPRs, three waves per SIMD; measured on MI355X, the deeper rings
+//    (4 / 2 quads, 204 VGPRs, two waves per SIMD) were 3-11% slower.
 //  * Tiles are ordered so that the workgroups of one XCD (workgroup ids are
 //    dealt to the 8 XCDs round-robin) cover a contiguous range of weight row
 //    blocks with all of their token blocks: each XCD's L2 holds the rows it
@@ -60,8 +61,8 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
   constexpr int SPT = (BM * KG + 255) / 256;  // activation scales per thread per quad
   constexpr int ABYTES = KG * BM * 64, SBYTES = BM * KG * 4;
   static_assert(KG % GS == 0, "a weight load never straddles a quad");
-  // ring depths (quads; W8 moves twice the bytes per quad) and quad unroll
-  constexpr int DW = W == 8 ? 2 : 4, DA = 2, UQ = 4;
+  // ring depths (quads) and quad unroll
+  constexpr int DW = 2, DA = 1, UQ = 4;
   static_assert(UQ % DW == 0 && UQ % DA == 0 && UQ % 2 == 0, "static ring indices");
 
   __shared__ __align__(16) uint8_t alds[2][ABYTES + SBYTES];
