@@ -40,6 +40,10 @@
 namespace actune {
 
 constexpr int kXcds = 8;
+// 64x32-tile launches of at most this many workgroups (one per CU) split K
+// in two inside the workgroup; measured on MI355X: 2048x16384 at M=256 43.7 ->
+// 32.9 us, 4096x4096 at M=128 13.6 -> 12.2 us, and slower with more tiles
+constexpr int kPrefillSplitTiles = 256;
 
 // LDS byte offset of B slot `slot` of token row `row` of group `gl` of a quad:
 // each row holds its quad's 16 slots (256 B) with the slot index XORed by
@@ -50,8 +54,14 @@ __device__ __forceinline__ int pf_slot_addr(int gl, int row, int slot) {
   return (row * 16 + ((gl * 4 + slot) ^ (row & 15))) * 16;
 }
 
-template <int W, int A, int TN, int TM, bool DOTS>
-__global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int tiles_m) {
+// KS > 1 splits K inside the workgroup: KS groups of 4 waves each take
+// kChunks / KS consecutive canonical chunks of the same output tile. Group 0
+// accumulates its chunks as usual; the other groups leave each chunk's
+// partial in LDS, and group 0 adds them in chunk order at the end, so the
+// result is the canonical one bit for bit. Shapes with few tiles use it to
+// shorten each wave's serial walk over K.
+template <int W, int A, int TN, int TM, int KS, bool DOTS>
+__global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, int tiles_m) {
   constexpr int T = shift_of(W) + shift_of(A);
   constexpr int BN = 64 * TN, BM = 16 * TM;
   constexpr int KG = 4;                       // groups per stage (one quad)
@@ -66,15 +76,38 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
   // ring depths (quads) and quad unroll
   constexpr int DW = 2, DA = 1, UQ = 4;
   static_assert(UQ % DW == 0 && UQ % DA == 0 && UQ % 2 == 0, "static ring indices");
+  constexpr int NC = kChunks / KS;            // canonical chunks per K group
+  // chunk partials of K groups 1..KS-1: [group - 1][wave][chunk][tile][lane] x 4
+  constexpr int CPART = KS > 1 && !DOTS ? (KS - 1) * 4 * NC * TN * TM * 64 * 4 : 1;
+  static_assert(KS == 1 || KS * 2 * (ABYTES + SBYTES) + CPART * 4 <= 150 * 1024, "LDS");
 
-  __shared__ __align__(16) uint8_t alds[2][ABYTES + SBYTES];
+  __shared__ __align__(16) uint8_t alds[KS][2][ABYTES + SBYTES];
+  __shared__ __align__(16) float cpart[CPART];
   __shared__ float wsl[DOTS ? 1 : BN], bsl[DOTS ? 1 : BN];
 
   const float fold = __builtin_ldexpf(1.0f, -T);
   const int M = args.M, K = args.K, N = args.prob[0].N, G = K / kGroup;
-  const int Qn = (G + KG - 1) / KG;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3;
+  const int kgrp = __builtin_amdgcn_readfirstlane(tid >> 8), ltid = tid & 255;  // K group, thread in it
   const int i = lane & 15, kb = lane >> 4;
+  // This K group's groups [g_lo, g_hi) and quads [q_begin, q_begin + Qk); chunk
+  // starts are multiples of 4 groups unless clipped to G, and a clipped (empty)
+  // range gets no quads. Qmax: the most quads of any K group (every wave runs
+  // that many barrier rounds).
+  auto k_range = [&](int k, int& glo, int& ghi, int& qb, int& qk) {
+    glo = chunk_begin(k * NC, G);
+    ghi = chunk_begin((k + 1) * NC, G);
+    qb = glo / KG;
+    qk = glo < ghi ? (ghi + KG - 1) / KG - qb : 0;
+  };
+  int g_lo, g_hi, q_begin, Qk, Qmax = 0;
+#pragma unroll
+  for (int k = 0; k < KS; ++k) {
+    int a, b, c, d;
+    k_range(k, a, b, c, d);
+    Qmax = d > Qmax ? d : Qmax;
+  }
+  k_range(kgrp, g_lo, g_hi, q_begin, Qk);
 
   // XCD-aware tile order: XCD x = id % 8 takes tiles [x*per + min(x, rem), ...)
   // in n-major order (consecutive tiles share a weight row block).
@@ -92,7 +125,7 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
 
   // epilogue constants of the workgroup's rows, through LDS
   if constexpr (!DOTS) {
-    for (int t = tid; t < BN; t += 256) {
+    for (int t = tid; t < BN; t += 256 * KS) {
       const ChannelConst cc = fetch_channel(args.prob[0].ws, args.prob[0].bias, args.bias_dt, N, n_blk + t, true);
       wsl[t] = cc.ws;
       bsl[t] = bias_from_bits(cc.bias_bits, args.bias_dt);
@@ -127,7 +160,7 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
   uint32_t abase[APT];
 #pragma unroll
   for (int t = 0; t < APT; ++t) {
-    const int ch = tid + t * 256, row = ch / (AROW / 16), cc = ch % (AROW / 16);
+    const int ch = ltid + t * 256, row = ch / (AROW / 16), cc = ch % (AROW / 16);
     const int m = m_blk + row;
     abase[t] = ch < ACH && m < M ? (uint32_t)m * arow_bytes + cc * 16 : kOff;
   }
@@ -137,7 +170,7 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
     if constexpr (!DOTS) {
 #pragma unroll
       for (int t = 0; t < SPT; ++t) {
-        const int e = tid + t * 256, row = e / KG, gl = e % KG;
+        const int e = ltid + t * 256, row = e / KG, gl = e % KG;
         const int m = m_blk + row, g = q * KG + gl;
         const bool ok = e < BM * KG && m < M && g < G;
         sraw[rs][t] = buffer_f32(sres, ok ? ((uint32_t)m * G + g) * 4u : kOff);
@@ -148,7 +181,7 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
     float* sl = reinterpret_cast<float*>(buf + ABYTES);
 #pragma unroll
     for (int t = 0; t < APT; ++t) {
-      const int ch = tid + t * 256;
+      const int ch = ltid + t * 256;
       if (ch >= ACH) break;
       const int row = ch / (AROW / 16), cc = ch % (AROW / 16);
       constexpr int SPC = 8 / A;  // slots per 16-byte chunk
@@ -164,7 +197,7 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
     if constexpr (!DOTS) {
 #pragma unroll
       for (int t = 0; t < SPT; ++t) {
-        const int e = tid + t * 256;
+        const int e = ltid + t * 256;
         if (e < BM * KG) sl[e] = sraw[rs][t] * fold;  // [token][group of the quad]
       }
     }
@@ -192,7 +225,7 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
   float scl[TM];  // token scales of the last group of the previous quad
 #pragma unroll
   for (int y = 0; y < TM; ++y) scl[y] = 0.0f;
-  int c = 0, cend = chunk_begin(1, G);  // chunk being accumulated, and its end
+  int c = kgrp * NC, cend = chunk_begin(kgrp * NC + 1, G);  // chunk being accumulated, and its end
   // p += D[par] * scale for group gq (dots mode: store the dots of gq instead)
   auto rescale = [&](int par, const float (&sc)[TM], int gq) {
 #pragma unroll
@@ -200,7 +233,7 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
 #pragma unroll
       for (int y = 0; y < TM; ++y) {
         if constexpr (DOTS) {
-          if (gq < 0 || gq >= G) continue;
+          if (gq < g_lo || gq >= g_hi) continue;  // the groups of this K group
           const int m = m_blk + y * 16 + i;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
@@ -214,39 +247,56 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
       }
   };
   // acc += p in chunk order (acc starts at +0 and p is never -0, so closing an
-  // empty chunk adds +0 and changes nothing)
+  // empty chunk adds +0 and changes nothing); K groups past the first leave
+  // the chunk's partial in LDS for group 0 instead
+  auto cpart_at = [&](int k, int cl, int x, int y) {
+    return cpart + (((((k - 1) * 4 + wave) * NC + cl) * TN + x) * TM + y) * 256 + lane * 4;
+  };
   auto close_chunk = [&]() {
 #pragma unroll
     for (int x = 0; x < TN; ++x)
 #pragma unroll
-      for (int y = 0; y < TM; ++y)
+      for (int y = 0; y < TM; ++y) {
+        if constexpr (KS > 1 && !DOTS) {
+          if (kgrp != 0) {
+            *reinterpret_cast<v4f*>(cpart_at(kgrp, c - kgrp * NC, x, y)) = v4f{p[x][y][0], p[x][y][1], p[x][y][2], p[x][y][3]};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) p[x][y][r] = 0.f;
+            continue;
+          }
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) { acc[x][y][r] = acc[x][y][r] + p[x][y][r]; p[x][y][r] = 0.f; }
+      }
     ++c;
     cend = chunk_begin(c + 1, G);
   };
 
   // ---------------------------------------------------------------- prologue
 #pragma unroll
-  for (int v = 0; v < DA; ++v) load_acts(v, v);
+  for (int v = 0; v < DA; ++v) load_acts(q_begin + v, v);
 #pragma unroll
   for (int v = 0; v < DW; ++v)
 #pragma unroll
-    for (int st = 0; st < WST; ++st) load_weights(v, st, wring[v][st]);
-  store_acts(alds[0], 0);
-  load_acts(DA, 0);
+    for (int st = 0; st < WST; ++st) load_weights(q_begin + v, st, wring[v][st]);
+  store_acts(alds[kgrp][0], 0);
+  load_acts(q_begin + DA, 0);
   __syncthreads();
 
   // ---------------------------------------------------------------- main loop
   // Branch-free per group: groups past G (the tail of the last quad) have
   // activation scale 0, so their rescale fma(d, 0, p) leaves p unchanged.
-  for (int q0 = 0; q0 < Qn; q0 += UQ) {
+  // Every wave runs Qmax barrier rounds; a K group with fewer quads idles
+  // through the last ones.
+  for (int v0 = 0; v0 < Qmax; v0 += UQ) {
 #pragma unroll
   for (int u = 0; u < UQ; ++u) {
-    const int q = q0 + u;
-    if (q < Qn) {  // uniform: false only in the last pass
+    const int v = v0 + u;
+    if (v < Qmax) {  // uniform: false only in the last pass
+    if (v < Qk) {    // uniform
+    const int q = q_begin + v;
     const int ws_slot = u % DW, as_next = (u + 1) % DA;
-    const uint8_t* buf = alds[u & 1];
+    const uint8_t* buf = alds[kgrp][u & 1];
     const float* sl = reinterpret_cast<const float*>(buf + ABYTES);
     float sq[TM][KG];
     if constexpr (!DOTS) {
@@ -318,15 +368,31 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
 #pragma unroll
       for (int y = 0; y < TM; ++y) scl[y] = sq[y][KG - 1];
     }
-    store_acts(alds[(u + 1) & 1], as_next);
+    store_acts(alds[kgrp][(u + 1) & 1], as_next);
     load_acts(q + 1 + DA, as_next);
+    }
     __syncthreads();
     }
   }
   }
-  rescale((KG - 1) & 1, scl, Qn * KG - 1);  // the last group
+  rescale((KG - 1) & 1, scl, (q_begin + Qk) * KG - 1);  // the last group
   if constexpr (DOTS) return;
-  while (c < kChunks) close_chunk();
+  while (c < (kgrp + 1) * NC) close_chunk();
+  if constexpr (KS > 1) {
+    // group 0 adds the other groups' chunk partials in chunk order
+    __syncthreads();
+    if (kgrp != 0) return;
+    for (int k = 1; k < KS; ++k)
+      for (int cl = 0; cl < NC; ++cl)
+#pragma unroll
+        for (int x = 0; x < TN; ++x)
+#pragma unroll
+          for (int y = 0; y < TM; ++y) {
+            const v4f pv = *reinterpret_cast<const v4f*>(cpart_at(k, cl, x, y));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[x][y][r] = acc[x][y][r] + pv[r];
+          }
+  }
 
   // ---------------------------------------------------------------- epilogue
   const bool has_bias = args.prob[0].bias != nullptr;
@@ -359,16 +425,18 @@ __global__ __launch_bounds__(256) void gemm_prefill(const LinearArgs args, int t
 // Shapes (TN, TM): 0 = (2, 4) 128x64, 1 = (2, 2) 128x32, 2 = (1, 4) 64x64, 3 = (1, 2) 64x32.
 template <int W, int A, bool DOTS>
 static void launch_prefill_shape(int shape, const LinearArgs& g, hipStream_t st) {
-#define PREFILL(TN, TM)                                                                       \
-  do {                                                                                        \
-    const int tn = (g.prob[0].N + 64 * TN - 1) / (64 * TN), tm = (g.M + 16 * TM - 1) / (16 * TM); \
-    gemm_prefill<W, A, TN, TM, DOTS><<<dim3((unsigned)(tn * tm)), 256, 0, st>>>(g, tm);        \
-  } while (0)
+#define PREFILL(TN, TM, KS)                                                                   \
+  gemm_prefill<W, A, TN, TM, KS, DOTS><<<dim3((unsigned)(tn * tm)), 256 * KS, 0, st>>>(g, tm)
+  const int TN_ = shape < 2 ? 2 : 1, TM_ = (shape & 1) ? 2 : 4;
+  const int tn = (g.prob[0].N + 64 * TN_ - 1) / (64 * TN_), tm = (g.M + 16 * TM_ - 1) / (16 * TM_);
   switch (shape) {
-    case 0: PREFILL(2, 4); break;
-    case 1: PREFILL(2, 2); break;
-    case 2: PREFILL(1, 4); break;
-    default: PREFILL(1, 2); break;
+    case 0: PREFILL(2, 4, 1); break;
+    case 1: PREFILL(2, 2, 1); break;
+    case 2: PREFILL(1, 4, 1); break;
+    default:
+      if (tn * tm <= kPrefillSplitTiles) PREFILL(1, 2, 2);
+      else PREFILL(1, 2, 1);
+      break;
   }
 #undef PREFILL
 }
