@@ -290,3 +290,47 @@ def test_streaming_fused_equals_two_step(W, A, m):
         wc, wsc = oracle_weight(w, W, A)
         want = O.linear(a_codes, a_scales, wc, wsc, b.float().numpy(), bounds=canonical_bounds(k // 64))
         np.testing.assert_array_equal(bits(out), O.round_out(want, dtype_name(dtype)))
+
+
+# ---------------------------------------------------------------- activation regimes
+def _regime(x: torch.Tensor, regime: str) -> torch.Tensor:
+    xf = x.float()
+    if regime == "small":
+        xf = xf * 1e-4
+    elif regime == "large":
+        xf = xf * 1e3
+    elif regime == "near_floor":  # group maxima around the 1e-8 scale floor
+        xf = xf * 3e-9
+    elif regime == "tiny":  # every group below the floor: all codes 0
+        xf = xf * 1e-30
+    elif regime == "zero_rows":
+        xf[::2] = 0
+    return xf.to(x.dtype)
+
+
+@pytest.mark.parametrize("regime", ["small", "large", "near_floor", "tiny", "zero_rows"])
+@pytest.mark.parametrize("W,A", [(4, 8), (2, 4), (8, 2)])
+def test_activation_regimes_bit_exact_every_config(regime, W, A):
+    """Activation magnitudes of 1e-4, 1e3, around and below the quantizer's
+    1e-8 scale floor, and all-zero token rows, through every kernel config
+    valid for M = 1, 8 and 80: codes, scales and outputs equal the oracle bit
+    for bit."""
+    k, n = 1024, 96
+    wsets = {}
+    for m in (1, 8, 80):
+        x, w, b = seeded_inputs(m, k, n, seed=31 * m + W + A, bias=True)
+        x = _regime(x, regime)
+        if m not in wsets:
+            wsets[m] = _packed_weight(w, W, A)
+        wc, wsc, w_dev, ws_dev = wsets[m]
+        xd, bd = x.to(DEV), b.to(DEV)
+        want_p, want_s, a_codes = oracle_activation(x, A)
+        p, s = _native.quantize_groups(xd, A)
+        np.testing.assert_array_equal(p.cpu().numpy(), want_p)
+        np.testing.assert_array_equal(s.cpu().numpy(), want_s)
+        want = O.round_out(O.linear(a_codes, want_s, wc, wsc, b.float().numpy(), bounds=canonical_bounds(k // 64)), "bf16")
+        for config in range(_native.num_configs()):
+            if not _native.config_valid(config, m):
+                continue
+            out = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, config=config)
+            np.testing.assert_array_equal(bits(out), want, err_msg=f"m={m} config={config}")
