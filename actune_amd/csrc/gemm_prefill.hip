@@ -18,17 +18,18 @@
 //    row fetch 64 consecutive bytes), swaps halves across lanes with
 //    v_permlane32/16_swap and unpacks sub-byte codes in registers; every
 //    unpacked slot feeds TM MFMAs.
-//  * Activations are staged once per workgroup per quad (4 groups) into LDS
-//    as 16-byte MFMA B slots, unpacked and reordered to the weight width's
-//    element order, with their group scales (2^-(sW+sA) folded in). LDS is
-//    double-buffered: one barrier per quad.
+//  * Activations are staged once per workgroup per stage (KG = 4 or 8
+//    groups) into LDS as 16-byte MFMA B slots, unpacked and reordered to the
+//    weight width's element order, with their group scales (2^-(sW+sA)
+//    folded in). LDS is double-buffered: one barrier per stage.
 //  * The MFMAs of group g are issued in the same block as the rescale of
 //    group g-1, so the matrix and vector pipes of a SIMD run side by side.
-//  * Weight loads run DW = 2 quads ahead in a register ring, activation loads
-//    DA = 1 quad ahead of their LDS store (a quad takes over a microsecond:
-//    enough lead for loads that miss L2). Shallow rings keep the 64x64 tile
-//    at 162 VGPRs, three waves per SIMD; measured on MI355X, the deeper rings
-//    (4 / 2 quads, 204 VGPRs, two waves per SIMD) were 3-11% slower.
+//  * Weight loads run DW = 2 stages of 4 groups ahead in a register ring,
+//    activation loads DA = 1 stage ahead of their LDS store (a stage takes
+//    over a microsecond: enough lead for loads that miss L2). Shallow rings
+//    keep the 64x64 tile at 162 VGPRs, three waves per SIMD; measured on
+//    MI355X, the deeper rings (4 / 2 stages, 204 VGPRs, two waves per SIMD)
+//    were 3-11% slower.
 //  * Tiles are ordered so that the workgroups of one XCD (workgroup ids are
 //    dealt to the 8 XCDs round-robin) cover a contiguous range of weight row
 //    blocks with all of their token blocks: each XCD's L2 holds the rows it
@@ -41,17 +42,20 @@ namespace actune {
 
 constexpr int kXcds = 8;
 // 64x32-tile launches of at most this many workgroups (one per CU) split K
-// in two inside the workgroup; measured on MI355X: 2048x16384 at M=256 43.7 ->
-// 32.9 us, 4096x4096 at M=128 13.6 -> 12.2 us, and slower with more tiles
+// in two inside the workgroup and stage 8 groups per barrier; measured on
+// MI355X (W4A8): 2048x16384 at M=256 45.2 -> 29.4 us, 2048x11008 32.3 -> 22.2
+// us, 4096x4096 at M=128 14.1 -> 11.9 us; slower with more tiles
 constexpr int kPrefillSplitTiles = 256;
 
-// LDS byte offset of B slot `slot` of token row `row` of group `gl` of a quad:
-// each row holds its quad's 16 slots (256 B) with the slot index XORed by
-// row % 16, so that both the 16 rows read by one ds_read_b128 and the 16
-// slots of one row written by 16 lanes fall on distinct 16-byte bank groups
-// (measured 2-4% faster than a [group][row][slot] array swizzled by row / 2).
+// LDS byte offset of B slot `slot` of token row `row` of group `gl` of a
+// stage of KG groups: each row holds its stage's 4*KG slots (64*KG bytes)
+// with the slot index XORed by row % 16, so that both the 16 rows read by
+// one ds_read_b128 and the 16 slots of one row written by 16 lanes fall on
+// distinct 16-byte bank groups (measured 2-4% faster than a
+// [group][row][slot] array swizzled by row / 2).
+template <int KG>
 __device__ __forceinline__ int pf_slot_addr(int gl, int row, int slot) {
-  return (row * 16 + ((gl * 4 + slot) ^ (row & 15))) * 16;
+  return (row * (4 * KG) + ((gl * 4 + slot) ^ (row & 15))) * 16;
 }
 
 // KS > 1 splits K inside the workgroup: KS groups of 4 waves each take
@@ -60,21 +64,21 @@ __device__ __forceinline__ int pf_slot_addr(int gl, int row, int slot) {
 // partial in LDS, and group 0 adds them in chunk order at the end, so the
 // result is the canonical one bit for bit. Shapes with few tiles use it to
 // shorten each wave's serial walk over K.
-template <int W, int A, int TN, int TM, int KS, bool DOTS>
+template <int W, int A, int TN, int TM, int KS, int KG, bool DOTS>
 __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, int tiles_m) {
   constexpr int T = shift_of(W) + shift_of(A);
   constexpr int BN = 64 * TN, BM = 16 * TM;
-  constexpr int KG = 4;                       // groups per stage (one quad)
+  static_assert(KG == 4 || KG == 8, "a stage is one or two quads (KG groups)");
   constexpr int GS = 8 / W;                   // groups per 16-byte weight load per lane
-  constexpr int WST = KG / GS;                // weight load steps per quad
-  constexpr int AROW = KG * 8 * A;            // packed activation bytes per token per quad
-  constexpr int ACH = BM * AROW / 16;         // 16-byte activation chunks per quad
+  constexpr int WST = KG / GS;                // weight load steps per stage
+  constexpr int AROW = KG * 8 * A;            // packed activation bytes per token per stage
+  constexpr int ACH = BM * AROW / 16;         // 16-byte activation chunks per stage
   constexpr int APT = (ACH + 255) / 256;      // per thread
-  constexpr int SPT = (BM * KG + 255) / 256;  // activation scales per thread per quad
+  constexpr int SPT = (BM * KG + 255) / 256;  // activation scales per thread per stage
   constexpr int ABYTES = KG * BM * 64, SBYTES = BM * KG * 4;
-  static_assert(KG % GS == 0, "a weight load never straddles a quad");
-  // ring depths (quads) and quad unroll
-  constexpr int DW = 2, DA = 1, UQ = 4;
+  static_assert(KG % GS == 0, "a weight load never straddles a stage");
+  // ring depths (stages) and stage unroll
+  constexpr int DW = KG == 8 ? 1 : 2, DA = 1, UQ = KG == 8 ? 2 : 4;
   static_assert(UQ % DW == 0 && UQ % DA == 0 && UQ % 2 == 0, "static ring indices");
   constexpr int NC = kChunks / KS;            // canonical chunks per K group
   // chunk partials of K groups 1..KS-1: [group - 1][wave][chunk][tile][lane] x 4
@@ -90,24 +94,25 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
   const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3;
   const int kgrp = __builtin_amdgcn_readfirstlane(tid >> 8), ltid = tid & 255;  // K group, thread in it
   const int i = lane & 15, kb = lane >> 4;
-  // This K group's groups [g_lo, g_hi) and quads [q_begin, q_begin + Qk); chunk
-  // starts are multiples of 4 groups unless clipped to G, and a clipped (empty)
-  // range gets no quads. Qmax: the most quads of any K group (every wave runs
-  // that many barrier rounds).
-  auto k_range = [&](int k, int& glo, int& ghi, int& qb, int& qk) {
+  // This K group's groups [g_lo, g_hi) in Qk stages of KG groups from g_lo
+  // (stage v: groups g_lo + v*KG ...). Groups of the last stage past g_hi
+  // belong to the next K group or lie past K: their activation scales are
+  // loaded as 0, so they add fma(d, 0, p) = p exactly (and the dots mode skips
+  // them). Qmax: the most stages of any K group (every wave runs that many
+  // barrier rounds).
+  auto k_range = [&](int k, int& glo, int& ghi, int& qk) {
     glo = chunk_begin(k * NC, G);
     ghi = chunk_begin((k + 1) * NC, G);
-    qb = glo / KG;
-    qk = glo < ghi ? (ghi + KG - 1) / KG - qb : 0;
+    qk = glo < ghi ? (ghi - glo + KG - 1) / KG : 0;
   };
-  int g_lo, g_hi, q_begin, Qk, Qmax = 0;
+  int g_lo, g_hi, Qk, Qmax = 0;
 #pragma unroll
   for (int k = 0; k < KS; ++k) {
-    int a, b, c, d;
-    k_range(k, a, b, c, d);
+    int a, b, d;
+    k_range(k, a, b, d);
     Qmax = d > Qmax ? d : Qmax;
   }
-  k_range(kgrp, g_lo, g_hi, q_begin, Qk);
+  k_range(kgrp, g_lo, g_hi, Qk);
 
   // XCD-aware tile order: XCD x = id % 8 takes tiles [x*per + min(x, rem), ...)
   // in n-major order (consecutive tiles share a weight row block).
@@ -133,17 +138,17 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
   }
 
   // ---------------------------------------------------------------- operand movers
-  // Register rings: the weight loads of quad v sit in wring[v % DW] (issued DW
-  // quads ahead), the activation chunks of quad v in araw[v % DA] (issued DA
-  // quads ahead of their LDS store). The quad loop is unrolled by UQ so every
+  // Register rings: the weight loads of stage v sit in wring[v % DW] (issued DW
+  // stages ahead), the activation chunks of stage v in araw[v % DA] (issued DA
+  // stages ahead of their LDS store). The stage loop is unrolled by UQ so every
   // ring index is a constant.
   uint32_t wring[DW][WST][TN][4];
   uint32_t araw[DA][APT][4];
   float sraw[DA][SPT];
 
   // Load offsets = a per-lane base (kOff for rows/tokens past the end, so the
-  // sum stays out of range) + a uniform per-quad offset. Bytes past the end
-  // of K (tail quad, prefetch past the last quad) read the following row, or
+  // sum stays out of range) + a uniform per-stage offset. Bytes past the end
+  // of K (tail stage, prefetch past the last stage) read the following row, or
   // zeros past the buffer; their groups have activation scale 0, so they add
   // fma(d, 0, p) = p exactly (and the dots mode skips them).
   uint32_t wbase[TN];
@@ -153,7 +158,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
     wbase[x] = n < N ? (uint32_t)n * wrow_bytes + kb * 16 : kOff;
   }
   auto load_weights = [&](int q, int st, uint32_t (&buf)[TN][4]) {
-    const uint32_t off = (uint32_t)(q * KG + st * GS) * 8 * W;
+    const uint32_t off = (uint32_t)(g_lo + q * KG + st * GS) * 8 * W;
 #pragma unroll
     for (int x = 0; x < TN; ++x) buffer_slot<8>(wres, wbase[x] + off, buf[x]);
   };
@@ -164,15 +169,15 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
     const int m = m_blk + row;
     abase[t] = ch < ACH && m < M ? (uint32_t)m * arow_bytes + cc * 16 : kOff;
   }
-  auto load_acts = [&](int q, int rs) {  // quad q into ring slot rs
+  auto load_acts = [&](int q, int rs) {  // stage q into ring slot rs
 #pragma unroll
-    for (int t = 0; t < APT; ++t) buffer_slot<8>(ares, abase[t] + (uint32_t)q * AROW, araw[rs][t]);
+    for (int t = 0; t < APT; ++t) buffer_slot<8>(ares, abase[t] + (uint32_t)(g_lo + q * KG) * 8 * A, araw[rs][t]);
     if constexpr (!DOTS) {
 #pragma unroll
       for (int t = 0; t < SPT; ++t) {
         const int e = ltid + t * 256, row = e / KG, gl = e % KG;
-        const int m = m_blk + row, g = q * KG + gl;
-        const bool ok = e < BM * KG && m < M && g < G;
+        const int m = m_blk + row, g = g_lo + q * KG + gl;
+        const bool ok = e < BM * KG && m < M && g < g_hi;
         sraw[rs][t] = buffer_f32(sres, ok ? ((uint32_t)m * G + g) * 4u : kOff);
       }
     }
@@ -191,14 +196,14 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
         uint32_t d[4];
         unpack_slot<A>(&araw[rs][t][u * A / 2], d);
         reorder_slot<A, W>(d);
-        *reinterpret_cast<v4u*>(buf + pf_slot_addr(gl, row, slot)) = v4u{d[0], d[1], d[2], d[3]};
+        *reinterpret_cast<v4u*>(buf + pf_slot_addr<KG>(gl, row, slot)) = v4u{d[0], d[1], d[2], d[3]};
       }
     }
     if constexpr (!DOTS) {
 #pragma unroll
       for (int t = 0; t < SPT; ++t) {
         const int e = ltid + t * 256;
-        if (e < BM * KG) sl[e] = sraw[rs][t] * fold;  // [token][group of the quad]
+        if (e < BM * KG) sl[e] = sraw[rs][t] * fold;  // [token][group of the stage]
       }
     }
   };
@@ -212,8 +217,8 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[x][y][r] = p[x][y][r] = 0.f;
   // MFMA results of group g live in D[g & 1] until the block of group g+1
-  // rescales them (no register copies: quads have an even number of groups,
-  // so the parity of g is that of its index in the quad). D[1] starts at zero,
+  // rescales them (no register copies: stages have an even number of groups,
+  // so the parity of g is that of its index in the stage). D[1] starts at zero,
   // so the rescale in the block of group 0 adds fma(0, 0, +0) = +0.
   v4i D[2][TN][TM];
 #pragma unroll
@@ -222,7 +227,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
     for (int x = 0; x < TN; ++x)
 #pragma unroll
       for (int y = 0; y < TM; ++y) D[b][x][y] = v4i{0, 0, 0, 0};
-  float scl[TM];  // token scales of the last group of the previous quad
+  float scl[TM];  // token scales of the last group of the previous stage
 #pragma unroll
   for (int y = 0; y < TM; ++y) scl[y] = 0.0f;
   int c = kgrp * NC, cend = chunk_begin(kgrp * NC + 1, G);  // chunk being accumulated, and its end
@@ -274,19 +279,19 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
 
   // ---------------------------------------------------------------- prologue
 #pragma unroll
-  for (int v = 0; v < DA; ++v) load_acts(q_begin + v, v);
+  for (int v = 0; v < DA; ++v) load_acts(v, v);
 #pragma unroll
   for (int v = 0; v < DW; ++v)
 #pragma unroll
-    for (int st = 0; st < WST; ++st) load_weights(q_begin + v, st, wring[v][st]);
+    for (int st = 0; st < WST; ++st) load_weights(v, st, wring[v][st]);
   store_acts(alds[kgrp][0], 0);
-  load_acts(q_begin + DA, 0);
+  load_acts(DA, 0);
   __syncthreads();
 
   // ---------------------------------------------------------------- main loop
-  // Branch-free per group: groups past G (the tail of the last quad) have
+  // Branch-free per group: groups past G (the tail of the last stage) have
   // activation scale 0, so their rescale fma(d, 0, p) leaves p unchanged.
-  // Every wave runs Qmax barrier rounds; a K group with fewer quads idles
+  // Every wave runs Qmax barrier rounds; a K group with fewer stages idles
   // through the last ones.
   for (int v0 = 0; v0 < Qmax; v0 += UQ) {
 #pragma unroll
@@ -294,7 +299,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
     const int v = v0 + u;
     if (v < Qmax) {  // uniform: false only in the last pass
     if (v < Qk) {    // uniform
-    const int q = q_begin + v;
+    const int q = v;  // stage of this K group
     const int ws_slot = u % DW, as_next = (u + 1) % DA;
     const uint8_t* buf = alds[kgrp][u & 1];
     const float* sl = reinterpret_cast<const float*>(buf + ABYTES);
@@ -302,9 +307,12 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
     if constexpr (!DOTS) {
 #pragma unroll
       for (int y = 0; y < TM; ++y) {
-        const v4u s4 = *reinterpret_cast<const v4u*>(sl + (y * 16 + i) * KG);
 #pragma unroll
-        for (int gl = 0; gl < KG; ++gl) sq[y][gl] = __uint_as_float(s4[gl]);
+        for (int h = 0; h < KG / 4; ++h) {
+          const v4u s4 = *reinterpret_cast<const v4u*>(sl + (y * 16 + i) * KG + 4 * h);
+#pragma unroll
+          for (int gl = 0; gl < 4; ++gl) sq[y][4 * h + gl] = __uint_as_float(s4[gl]);
+        }
       }
     }
     // B fragments of the current group and (read one block ahead) the next
@@ -312,14 +320,14 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
     auto read_b = [&](int gl, uint32_t (&dst)[TM][4]) {
 #pragma unroll
       for (int y = 0; y < TM; ++y) {
-        const v4u b = *reinterpret_cast<const v4u*>(buf + pf_slot_addr(gl, y * 16 + i, slot_b));
+        const v4u b = *reinterpret_cast<const v4u*>(buf + pf_slot_addr<KG>(gl, y * 16 + i, slot_b));
         dst[y][0] = b[0]; dst[y][1] = b[1]; dst[y][2] = b[2]; dst[y][3] = b[3];
       }
     };
     read_b(0, bf[0]);
 #pragma unroll
     for (int gl = 0; gl < KG; ++gl) {
-      const int g = q * KG + gl;
+      const int g = g_lo + q * KG + gl;
       const int st = gl / GS, jj = gl % GS;
       if (jj == 0) {
 #pragma unroll
@@ -347,13 +355,15 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
         }
-        if (gl == 0) {
-          while (g >= cend) close_chunk();  // chunks that end before group g
+        if (gl % 4 == 0) {  // chunks start on quads
+          // chunks that end before group g (the group's own last chunk closes
+          // after the loop: groups past g_hi belong to no chunk of this group)
+          while (g >= cend && c < (kgrp + 1) * NC - 1) close_chunk();
         }
       }
       if constexpr (!DOTS) {
         // Keep the rescale of group g-1 in this block: without a use here the
-        // compiler sinks it to the end of the quad, away from the MFMAs it is
+        // compiler sinks it to the end of the stage, away from the MFMAs it is
         // meant to overlap.
 #pragma unroll
         for (int x = 0; x < TN; ++x)
@@ -375,7 +385,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
     }
   }
   }
-  rescale((KG - 1) & 1, scl, (q_begin + Qk) * KG - 1);  // the last group
+  rescale((KG - 1) & 1, scl, g_lo + Qk * KG - 1);  // the last group
   if constexpr (DOTS) return;
   while (c < (kgrp + 1) * NC) close_chunk();
   if constexpr (KS > 1) {
@@ -425,17 +435,17 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
 // Shapes (TN, TM): 0 = (2, 4) 128x64, 1 = (2, 2) 128x32, 2 = (1, 4) 64x64, 3 = (1, 2) 64x32.
 template <int W, int A, bool DOTS>
 static void launch_prefill_shape(int shape, const LinearArgs& g, hipStream_t st) {
-#define PREFILL(TN, TM, KS)                                                                   \
-  gemm_prefill<W, A, TN, TM, KS, DOTS><<<dim3((unsigned)(tn * tm)), 256 * KS, 0, st>>>(g, tm)
+#define PREFILL(TN, TM, KS, KG)                                                               \
+  gemm_prefill<W, A, TN, TM, KS, KG, DOTS><<<dim3((unsigned)(tn * tm)), 256 * KS, 0, st>>>(g, tm)
   const int TN_ = shape < 2 ? 2 : 1, TM_ = (shape & 1) ? 2 : 4;
   const int tn = (g.prob[0].N + 64 * TN_ - 1) / (64 * TN_), tm = (g.M + 16 * TM_ - 1) / (16 * TM_);
   switch (shape) {
-    case 0: PREFILL(2, 4, 1); break;
-    case 1: PREFILL(2, 2, 1); break;
-    case 2: PREFILL(1, 4, 1); break;
+    case 0: PREFILL(2, 4, 1, 4); break;
+    case 1: PREFILL(2, 2, 1, 4); break;
+    case 2: PREFILL(1, 4, 1, 4); break;
     default:
-      if (tn * tm <= kPrefillSplitTiles) PREFILL(1, 2, 2);
-      else PREFILL(1, 2, 1);
+      if (tn * tm <= kPrefillSplitTiles) PREFILL(1, 2, 2, 8);
+      else PREFILL(1, 2, 1, 4);
       break;
   }
 #undef PREFILL
