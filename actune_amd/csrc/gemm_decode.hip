@@ -472,6 +472,7 @@ static void launch_decode_nw(bool packed, const LinearArgs& g, hipStream_t st) {
   if (packed) {
     if (g.M == 1) launch_decode_one<W, A, NW, 4, true, false, true, false>(g, st);
     else if (g.M <= 4) launch_decode_one<W, A, NW, 4, true, false, false, false>(g, st);
+    else if (full) launch_decode_one<W, A, NW, 8, true, false, false, true>(g, st);
     else launch_decode_one<W, A, NW, 8, true, false, false, false>(g, st);
     return;
   }
