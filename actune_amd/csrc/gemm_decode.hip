@@ -455,12 +455,7 @@ static void launch_decode_one(const LinearArgs& g, hipStream_t st) {
   constexpr int RING = decode_ring(W);
   const size_t lds = decode_lds_bytes(g.K, g.M, NW);
   auto kern = gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL>;
-  static bool attr_set = false;  // allow dynamic LDS beyond the default per-launch limit
-  if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)kStreamLdsMax);
-    attr_set = true;
-  }
+  allow_dynamic_lds<gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL>>();
   int row_tiles = 1;  // grid x: the row tiles of the widest problem; grid y: the problems
   for (int q = 0; q < g.nprob; ++q) row_tiles = std::max(row_tiles, (g.prob[q].N + 15) / 16);
   kern<<<dim3((unsigned)row_tiles, (unsigned)g.nprob), NW * 64, lds, st>>>(g, decode_groups_per_wave(g.K, NW));

@@ -303,12 +303,7 @@ template <int W, int A, int NW, int MODE, int DT, bool SCALE>
 static void launch_one(const LinearArgs& g, hipStream_t st) {
   const size_t lds = stream_lds_bytes(g.K, g.M, NW);
   auto kern = gemm_stream<W, A, NW, MODE, DT, SCALE>;
-  static bool attr_set = false;  // allow dynamic LDS beyond the default per-launch limit
-  if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)kStreamLdsMax);
-    attr_set = true;
-  }
+  allow_dynamic_lds<gemm_stream<W, A, NW, MODE, DT, SCALE>>();
   const int grid = resident_grid(kern, NW * 64, lds, g.tiles);
   const int gw = max_wave_groups(g.K / kGroup, NW);
   kern<<<grid, NW * 64, lds, st>>>(g, gw, (g.M + 3) & ~3);

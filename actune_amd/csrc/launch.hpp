@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace actune {
 
 constexpr int kMaxProblems = 4;
@@ -60,6 +62,21 @@ __device__ __forceinline__ Problem select_problem(const LinearArgs& args, int ti
     pr.tile0 = s ? pp[q].tile0 : pr.tile0;
   }
   return pr;
+}
+
+// Lets kernel KERN take up to kStreamLdsMax bytes of dynamic LDS on the
+// current device (above the default per-launch limit). Done once per
+// (kernel, device); safe to call from several host threads.
+template <auto KERN>
+inline void allow_dynamic_lds() {
+  static std::atomic<uint64_t> done{0};  // bit d: raised on device d
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return;
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(KERN), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)kStreamLdsMax);
+  done.fetch_or(bit, std::memory_order_release);
 }
 
 void launch_quantize(const void* x, int dt, const void* sc, long M, long K, int A, uint8_t* packed,
