@@ -3,6 +3,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <climits>
 
 #include "../../include/actune_hip.h"
@@ -86,17 +87,21 @@ int check_target(const uint8_t* w, const float* ws, const void* out, int64_t N, 
 int packed_default(int64_t M, int64_t N, int64_t K, int W, int A);
 
 // Whether a decode-config call quantizes x inside the GEMM. Every workgroup
-// quantizes the whole activation, so the in-launch work grows as row tiles x
-// groups x tokens; measured on MI355X (W4A8, M = 1..8, N = 2048..22016), past
-// about 180 group-rows per SIMD (1024 SIMDs) the quantizer launch followed by
-// the GEMM on its codes is faster. Where the codes path cannot run the
-// decode kernel (M <= 4), the fused small-M kernel runs instead.
-bool decode_light(int64_t M, int64_t n_total, int64_t K) {
-  return ((n_total + 15) / 16) * (K / kGroup) * M <= 180 * 1024;
+// quantizes the whole activation, so the in-launch work grows as workgroups
+// (row tiles / tiles per workgroup) x groups x tokens; measured on MI355X
+// (W4A8, M = 1..8, N = 2048..22016), past about 180 (4-token tiles) or 160
+// (8-token tiles) group-rows per SIMD (1024 SIMDs) the quantizer launch
+// followed by the GEMM on its codes is faster. Where the codes path cannot
+// run the decode kernel (M <= 4), the fused small-M kernel runs instead.
+bool decode_light(int64_t M, int64_t n_total, int64_t K, int W, int nw) {
+  const int64_t tiles = (n_total + 15) / 16;
+  const int tr = decode_row_tiles((int)K, (int)M, W, nw, (int)std::min<int64_t>(tiles, INT_MAX), 1);
+  const int64_t limit = (M <= kFusedMaxM ? 180 : 160) * 1024;
+  return (tiles + tr - 1) / tr * (K / kGroup) * M <= limit;
 }
 
 bool decode_fused(int64_t M, int64_t n_total, int64_t K, int W, int nw, int x_dt) {
-  if (decode_fits((int)K, (int)M, W, nw, false, x_dt) && decode_light(M, n_total, K)) return true;
+  if (decode_fits((int)K, (int)M, W, nw, false, x_dt) && decode_light(M, n_total, K, W, nw)) return true;
   return M <= kFusedMaxM && !decode_fits((int)K, (int)M, W, nw, true, x_dt);
 }
 
@@ -194,19 +199,30 @@ int actune_config_valid(int config, int64_t M) {
 int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
   // Decode (M <= 8, measured on MI355X at W4A8 Llama/Gemma shapes): the
   // decode kernel beats the small-M and streaming kernels wherever a wave's
-  // K-range fits its load ring. Fewer waves per tile cost less per-workgroup
-  // work, so take the smallest wave count that still gives every SIMD a wave
-  // (tiles x waves >= 1024) and fits K: first with bf16 x quantized in the
-  // launch where that pays (decode_light), then with the quantizer's codes.
-  if (M >= 1 && M <= kDecodeMax) {
+  // K-range fits its load ring. M <= 4: fewer waves per tile cost less
+  // per-workgroup work, so take the smallest wave count that still gives
+  // every SIMD a wave (tiles x waves >= 1024) and fits K: first with bf16 x
+  // quantized in the launch where that pays (decode_light), then with the
+  // quantizer's codes.
+  if (M >= 1 && M <= kFusedMaxM) {
     const int64_t tiles = (N + 15) / 16;
     for (int packed = 0; packed < 2; ++packed)
       for (int c = 0; c < 3; ++c) {
         const int nw = kSmallMWaves[c];
         if (!(tiles * nw >= 1024 || nw == kSmallMWaves[2])) continue;
-        if (decode_fits((int)K, (int)M, W, nw, packed, kBF16) && (packed || decode_light(M, N, K)))
+        if (decode_fits((int)K, (int)M, W, nw, packed, kBF16) && (packed || decode_light(M, N, K, W, nw)))
           return kDecodeFirst + c;
       }
+  } else if (M > kFusedMaxM && M <= kDecodeMax) {
+    // 8-token tiles (measured, W4A8 M = 5..8): x quantized in the launch by
+    // 16 waves, whose short K-ranges let up to four row tiles share a
+    // workgroup and its quantized x, where that stays light; otherwise the
+    // quantizer's codes with 4 waves (8 from 1024 row tiles on)
+    if (decode_fits((int)K, (int)M, W, 16, false, kBF16) && decode_light(M, N, K, W, 16)) return kDecodeFirst + 2;
+    const int64_t tiles = (N + 15) / 16;
+    const int order[3] = {tiles >= 1024 ? 1 : 0, tiles >= 1024 ? 0 : 1, 2};
+    for (int c : order)
+      if (decode_fits((int)K, (int)M, W, kSmallMWaves[c], true, kBF16)) return kDecodeFirst + c;
   }
   return packed_default(M, N, K, W, A);
 }

@@ -61,8 +61,9 @@ static int decode_groups_per_wave(int K, int nw) {
 }
 
 // true when every one of nw waves gets exactly a full ring of weight slots
-static bool decode_full(int K, int W, int nw) {
-  const int G = K / kGroup, cpw = kChunks / nw, per = decode_ring(W) * (8 / W);
+// (decode_ring(W) / tr slots per row tile)
+static bool decode_full(int K, int W, int nw, int tr = 1) {
+  const int G = K / kGroup, cpw = kChunks / nw, per = decode_ring(W) / tr * (8 / W);
   for (int w = 0; w < nw; ++w)
     if (chunk_begin((w + 1) * cpw, G) - chunk_begin(w * cpw, G) != per) return false;
   return true;
@@ -70,10 +71,30 @@ static bool decode_full(int K, int W, int nw) {
 
 // Dynamic LDS: per wave a slab [GW groups][M tokens][64 B] and a scale slab
 // [GW][MT] (fp32, 2^-(sW+sA) folded in; entries of absent tokens unused), the
-// zero region, and the chunk partials red[16][16][MT].
-size_t decode_lds_bytes(int K, int M, int nw) {
+// zero region, and the chunk partials red[16][16 * tr][MT].
+size_t decode_lds_bytes(int K, int M, int nw, int tr) {
   const int gw = decode_groups_per_wave(K, nw), MT = decode_token_tile(M);
-  return (size_t)nw * gw * (M * kGroup + MT * sizeof(float)) + kDecodeZeroBytes + sizeof(float) * kChunks * 16 * MT;
+  return (size_t)nw * gw * (M * kGroup + MT * sizeof(float)) + kDecodeZeroBytes +
+         sizeof(float) * kChunks * 16 * tr * MT;
+}
+
+// At least this many workgroups when several row tiles share one (measured
+// on MI355X, W4A8 M=8: 256 row tiles run best one per workgroup, 688-1376
+// with four).
+constexpr int kDecodeMinGroups = 160;
+
+// Row tiles per workgroup for an 8-token tile: the most (up to 4) whose weight
+// slots still fit the ring, keeping at least kDecodeMinGroups workgroups over
+// the nprob problems of `tiles` row tiles each.
+int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob) {
+  if (decode_token_tile(M) != 8) return 1;
+  const int slots = (decode_groups_per_wave(K, nw) + 8 / W - 1) / (8 / W);
+  int tr = 1;
+  for (int c = 2; c <= 4; c *= 2)
+    if (slots * c <= decode_ring(W) && (tiles + c - 1) / c * nprob >= kDecodeMinGroups &&
+        decode_lds_bytes(K, M, nw, c) <= kStreamLdsMax)
+      tr = c;
+  return tr;
 }
 
 bool decode_fits(int K, int M, int W, int nw, bool packed, int x_dt) {
@@ -83,7 +104,7 @@ bool decode_fits(int K, int M, int W, int nw, bool packed, int x_dt) {
   if ((gw + gps - 1) / gps > decode_ring(W)) return false;
   const int per = packed ? 16 : 8;
   if ((gw * M + per - 1) / per > decode_passes(decode_token_tile(M), packed)) return false;
-  return decode_lds_bytes(K, M, nw) <= kStreamLdsMax;
+  return decode_lds_bytes(K, M, nw, 1) <= kStreamLdsMax;
 }
 
 // chunk_begin in unsigned arithmetic (c, G >= 0): shifts instead of the
@@ -101,8 +122,10 @@ __device__ __forceinline__ int chunk_begin_u(int c, int G) {
 // LDS offsets and keep the group scales in scalar registers. FULL: every
 // wave's K-range is exactly RING slots (decode_full), so the slot pipeline
 // runs without bounds tests (and a fused ONE launch issues exactly the x
-// passes of the range).
-template <int W, int A, int NW, int RING, int MT, bool PACKED, bool SCALE, bool ONE, bool FULL>
+// passes of the range). TR: 16-row tiles per workgroup (M > 1): the tiles share
+// the workgroup's activation slab, so x is read and quantized once per TR
+// tiles; RING is then the weight slots per tile.
+template <int W, int A, int NW, int RING, int MT, bool PACKED, bool SCALE, bool ONE, bool FULL, int TR>
 __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, int GW) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int GS = 8 / W;                // groups per 16-byte weight load per lane
@@ -114,6 +137,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   constexpr int PR = PACKED ? 16 : 8;      // group-rows per activation pass
   constexpr int NPX = FULL && ONE && !PACKED ? (RING * GS + 7) / 8 : decode_passes(MT, PACKED);
   static_assert(!ONE || MT == 4, "M == 1 uses the 4-token tile");
+  static_assert(!ONE || TR == 1, "M == 1 launches own one row tile per workgroup");
+  static_assert(TR <= NW, "waves 0..TR-1 finish one tile each");
 
   const float fold = __builtin_ldexpf(1.0f, -T);
   // Every kernel argument the prologue needs is read here, in one batch of
@@ -129,7 +154,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   asm volatile("" : "+s"(M), "+s"(K), "+s"(bias_dt), "+s"(out_dt), "+s"(m_inv), "+s"(xsrc), "+s"(xaux), "+s"(GW),
                     "+s"(pr.w), "+s"(pr.ws), "+s"(pr.bias), "+s"(pr.out), "+s"(pr.N));
   const int N = pr.N, G = K / kGroup;
-  const int n0 = (int)blockIdx.x * 16;
+  const int n0 = (int)blockIdx.x * 16 * TR;
   // blockIdx.x spans the widest problem of the launch; a narrower one's
   // workgroups past its rows leave at once (whole workgroup, before any
   // barrier)
@@ -249,21 +274,24 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   // stays below 2^31, so the sum cannot wrap).
   const uint32_t wbase = (uint32_t)(n0 + i) * wrow_bytes + kb * 16 + (uint32_t)wg0 * 8 * W;
   // the host guarantees ns <= RING and npass <= NPX (decode_fits)
-  uint32_t ring[RING][4];
+  uint32_t ring[TR][RING][4];
+#pragma unroll
+  for (int t = 0; t < TR; ++t)
 #pragma unroll
   for (int st = 0; st < RING; ++st) {
     // (a runtime test also where every slot is live: with a constant offset
     // the compiler schedules the loads differently and the launch measured
     // 0.4 us slower at one workgroup per CU)
-    const v4u q = __builtin_amdgcn_raw_buffer_load_b128(wres, wbase + (uint32_t)st * 64, st < ns ? 0u : kOff, 0);
-    ring[st][0] = q[0]; ring[st][1] = q[1]; ring[st][2] = q[2]; ring[st][3] = q[3];
+    const v4u q = __builtin_amdgcn_raw_buffer_load_b128(wres, wbase + (uint32_t)(16 * t) * wrow_bytes + (uint32_t)st * 64,
+                                                        st < ns ? 0u : kOff, 0);
+    ring[t][st][0] = q[0]; ring[t][st][1] = q[1]; ring[t][st][2] = q[2]; ring[t][st][3] = q[3];
   }
   // epilogue constants, behind the weights: they are needed last, by wave 0.
   // Every wave issues the two loads (switched off outside wave 0) so that all
   // waves have the same loads in flight: behind a branch, the compiler's
   // waits for the activation passes would count from the shorter path and
   // make wave 0 wait for weight slots before quantizing.
-  const ChannelConst cc = fetch_channel(pr.ws, pr.bias, bias_dt, N, n0 + e_row, wave == 0);
+  const ChannelConst cc = fetch_channel(pr.ws, pr.bias, bias_dt, N, n0 + 16 * wave + e_row, wave < TR);
 
   // ---------------------------------------------------------------- activation slab
   // the zero region: one dword per thread of the first four waves
@@ -287,12 +315,26 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   __syncthreads();
 
   // ---------------------------------------------------------------- stream the K-range
-  float p[4] = {0.f, 0.f, 0.f, 0.f};
+  float p[TR][4];
+#pragma unroll
+  for (int t = 0; t < TR; ++t)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) p[t][q] = 0.f;
   int c = c_first;
-  // partials: lane l holds rows l % 16 of tokens 4*(l/16)..+3; the lanes of
-  // the token tile write them
+  // partials: lane l holds rows l % 16 of tokens 4*(l/16)..+3 of each tile;
+  // the lanes of the token tile write them to red[chunk][tile row][token]
+  constexpr int RS = 16 * TR * MT;  // floats per chunk of red
   const bool writer = lane < 16 * (MT / 4);
   float* red_lane = red + (size_t)(lane & 15) * MT + 4 * ((lane >> 4) & (MT / 4 - 1));
+  auto write_partials = [&](int cc_) {
+#pragma unroll
+    for (int t = 0; t < TR; ++t) {
+      if (writer)
+        *reinterpret_cast<v4f*>(red_lane + (size_t)cc_ * RS + 16 * t * MT) = v4f{p[t][0], p[t][1], p[t][2], p[t][3]};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) p[t][q] = 0.f;
+    }
+  };
   if constexpr (FAST) {
     // M == 1: lanes of token 0 (i == 0) read the wave's slab, the others the
     // zero region, both with stride 64 per group, so every token operand
@@ -310,11 +352,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
 #pragma unroll
     for (int st = 0; st < RA && st < RING; ++st) read_q(st);
     auto mfma_slot = [&](int st) {
-      exchange<W>(ring[st]);
+      exchange<W>(ring[0][st]);
 #pragma unroll
       for (int jj = 0; jj < GS; ++jj) {
         uint32_t wd[4];
-        unpack_slot<W>(&ring[st][jj * W / 2], wd);
+        unpack_slot<W>(&ring[0][st][jj * W / 2], wd);
         const uint32_t bd[4] = {bq[st][jj][0], bq[st][jj][1], bq[st][jj][2], bq[st][jj][3]};
         D[st][jj] = mfma16x16x64(bd, wd, v4i{0, 0, 0, 0});
       }
@@ -333,8 +375,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
       }
       const int g0 = wg0 + st * GS;
       while (g0 >= cend && c < c_last) {  // close finished (possibly empty) chunks
-        if (lane < 16) *reinterpret_cast<v4f*>(red_lane + (size_t)c * 16 * MT) = v4f{p[0], 0.f, 0.f, 0.f};
-        p[0] = 0.f;
+        if (lane < 16) *reinterpret_cast<v4f*>(red_lane + (size_t)c * RS) = v4f{p[0][0], 0.f, 0.f, 0.f};
+        p[0][0] = 0.f;
         ++c;
         cend = chunk_begin_u(c + 1, G);
       }
@@ -344,10 +386,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int jj = 0; jj < GS; ++jj) p[0] = __builtin_fmaf((float)D[st][jj][0], gsc[st * GS + jj], p[0]);
+      for (int jj = 0; jj < GS; ++jj) p[0][0] = __builtin_fmaf((float)D[st][jj][0], gsc[st * GS + jj], p[0][0]);
     }
   } else {
-    // The GS MFMAs of a slot are issued together and folded in group order.
+    // The GS MFMAs of a slot are issued together (for every tile) and folded
+    // in group order.
     const int slot_k = smallm_slot_k<W>(kb);
     // Lanes of absent tokens (i >= M) read the zero row with stride 0. A group
     // past the wave's range (the tail of its last slot, or a slot read ahead
@@ -376,17 +419,20 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
     constexpr int RA = GS == 4 && NW == 16 ? 1 : 3;
     v4u bq[RING][GS];
     v4f bs[RING][GS];
-    v4i D[RING][GS];
+    v4i D[TR][RING][GS];
 #pragma unroll
     for (int st = 0; st < RA && st < RING; ++st) read_b(st, bq[st], bs[st]);
     auto mfma_slot = [&](int st) {
-      exchange<W>(ring[st]);
 #pragma unroll
-      for (int jj = 0; jj < GS; ++jj) {
-        uint32_t wd[4];
-        unpack_slot<W>(&ring[st][jj * W / 2], wd);
-        const uint32_t bd[4] = {bq[st][jj][0], bq[st][jj][1], bq[st][jj][2], bq[st][jj][3]};
-        D[st][jj] = mfma16x16x64(bd, wd, v4i{0, 0, 0, 0});
+      for (int t = 0; t < TR; ++t) {
+        exchange<W>(ring[t][st]);
+#pragma unroll
+        for (int jj = 0; jj < GS; ++jj) {
+          uint32_t wd[4];
+          unpack_slot<W>(&ring[t][st][jj * W / 2], wd);
+          const uint32_t bd[4] = {bq[st][jj][0], bq[st][jj][1], bq[st][jj][2], bq[st][jj][3]};
+          D[t][st][jj] = mfma16x16x64(bd, wd, v4i{0, 0, 0, 0});
+        }
       }
     };
     int cend = chunk_begin(c + 1, G);
@@ -405,9 +451,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
       // start at a multiple of GS, so chunks close only at slot starts.
       const int g0 = wg0 + st * GS;
       while (g0 >= cend && c < c_last) {  // close finished (possibly empty) chunks
-        if (writer) *reinterpret_cast<v4f*>(red_lane + (size_t)c * 16 * MT) = v4f{p[0], p[1], p[2], p[3]};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) p[q] = 0.f;
+        write_partials(c);
         ++c;
         cend = chunk_begin(c + 1, G);
       }
@@ -417,28 +461,27 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
         // unset and their partials never read)
         const v4f sc = bs[st][jj];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) p[q] = __builtin_fmaf((float)D[st][jj][q], sc[q], p[q]);
+        for (int t = 0; t < TR; ++t)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) p[t][q] = __builtin_fmaf((float)D[t][st][jj][q], sc[q], p[t][q]);
       }
     }
   }
-  for (; c < c_first + CPW; ++c) {
-    if (writer) *reinterpret_cast<v4f*>(red_lane + (size_t)c * 16 * MT) = v4f{p[0], p[1], p[2], p[3]};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) p[q] = 0.f;
-  }
+  for (; c < c_first + CPW; ++c) write_partials(c);
   __syncthreads();
 
   // ---------------------------------------------------------------- epilogue
-  if (wave == 0) {
-    const int n = n0 + e_row;
+  // wave t < TR finishes tile t
+  if (wave < TR) {
+    const int n = n0 + 16 * wave + e_row;
 #pragma unroll
     for (int jt = 0; jt < MT / 4; ++jt) {
       const int m = e_m + 4 * jt;
       if (m < M && n < N) {
-        const float* rr = red + (size_t)e_row * MT + m;
+        const float* rr = red + (size_t)(16 * wave + e_row) * MT + m;
         float acc = rr[0];
 #pragma unroll
-        for (int q = 1; q < kChunks; ++q) acc = acc + rr[(size_t)q * 16 * MT];
+        for (int q = 1; q < kChunks; ++q) acc = acc + rr[(size_t)q * RS];
         const float y = finish_const(acc, cc, pr.bias != nullptr, bias_dt);
         const long o = (long)m * N + n;
         if (out_dt == kBF16) store_out<kBF16>(pr.out, o, y);
@@ -450,15 +493,35 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
 }
 
 // ---------------------------------------------------------------------------
-template <int W, int A, int NW, int MT, bool PACKED, bool SCALE, bool ONE, bool FULL>
-static void launch_decode_one(const LinearArgs& g, hipStream_t st) {
-  constexpr int RING = decode_ring(W);
-  const size_t lds = decode_lds_bytes(g.K, g.M, NW);
-  auto kern = gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL>;
-  allow_dynamic_lds<gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL>>();
-  int row_tiles = 1;  // grid x: the row tiles of the widest problem; grid y: the problems
+// grid x: the TR-tile groups of the widest problem; grid y: the problems
+static int decode_max_tiles(const LinearArgs& g) {
+  int row_tiles = 1;
   for (int q = 0; q < g.nprob; ++q) row_tiles = std::max(row_tiles, (g.prob[q].N + 15) / 16);
-  kern<<<dim3((unsigned)row_tiles, (unsigned)g.nprob), NW * 64, lds, st>>>(g, decode_groups_per_wave(g.K, NW));
+  return row_tiles;
+}
+
+template <int W, int A, int NW, int MT, bool PACKED, bool SCALE, bool ONE, bool FULL, int TR = 1>
+static void launch_decode_one(const LinearArgs& g, hipStream_t st) {
+  constexpr int RING = decode_ring(W) / TR;
+  const size_t lds = decode_lds_bytes(g.K, g.M, NW, TR);
+  auto kern = gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL, TR>;
+  allow_dynamic_lds<gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL, TR>>();
+  const int groups = (decode_max_tiles(g) + TR - 1) / TR;
+  kern<<<dim3((unsigned)groups, (unsigned)g.nprob), NW * 64, lds, st>>>(g, decode_groups_per_wave(g.K, NW));
+}
+
+// 8-token launches: TR row tiles per workgroup (decode_row_tiles)
+template <int W, int A, int NW, bool PACKED, bool SCALE>
+static void launch_decode_mt8(const LinearArgs& g, hipStream_t st) {
+  const int tr = decode_row_tiles(g.K, g.M, W, NW, decode_max_tiles(g), g.nprob);
+  const bool full = decode_full(g.K, W, NW, tr);
+#define DEC_TR(TRV)                                                                      \
+  if (full) launch_decode_one<W, A, NW, 8, PACKED, SCALE, false, true, TRV>(g, st);      \
+  else launch_decode_one<W, A, NW, 8, PACKED, SCALE, false, false, TRV>(g, st)
+  if (tr == 4) { DEC_TR(4); }
+  else if (tr == 2) { DEC_TR(2); }
+  else { DEC_TR(1); }
+#undef DEC_TR
 }
 
 template <int W, int A, int NW>
@@ -467,8 +530,7 @@ static void launch_decode_nw(bool packed, const LinearArgs& g, hipStream_t st) {
   if (packed) {
     if (g.M == 1) launch_decode_one<W, A, NW, 4, true, false, true, false>(g, st);
     else if (g.M <= 4) launch_decode_one<W, A, NW, 4, true, false, false, false>(g, st);
-    else if (full) launch_decode_one<W, A, NW, 8, true, false, false, true>(g, st);
-    else launch_decode_one<W, A, NW, 8, true, false, false, false>(g, st);
+    else launch_decode_mt8<W, A, NW, true, false>(g, st);
     return;
   }
 #define DEC_FULL(MTV, SC, ONEV)                                                 \
@@ -481,8 +543,8 @@ static void launch_decode_nw(bool packed, const LinearArgs& g, hipStream_t st) {
     if (scale) { DEC_FULL(4, true, false); }
     else { DEC_FULL(4, false, false); }
   } else {
-    if (scale) launch_decode_one<W, A, NW, 8, false, true, false, false>(g, st);
-    else launch_decode_one<W, A, NW, 8, false, false, false, false>(g, st);
+    if (scale) launch_decode_mt8<W, A, NW, false, true>(g, st);
+    else launch_decode_mt8<W, A, NW, false, false>(g, st);
   }
 #undef DEC_FULL
 }

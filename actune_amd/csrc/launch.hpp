@@ -88,11 +88,14 @@ void launch_prefill(int W, int A, int shape, bool dots, const LinearArgs& g, hip
 // packed: the activations are codes + scales from the quantizer launch
 // (g.a, g.as); otherwise bf16 x is quantized inside the launch (g.x)
 void launch_decode(int W, int A, int nw, bool packed, const LinearArgs& g, hipStream_t st);
-size_t decode_lds_bytes(int K, int M, int nw);
+size_t decode_lds_bytes(int K, int M, int nw, int tr);
 // true when the decode kernel with nw waves takes an M x K problem of width W
 // in the given activation mode (every wave's loads fit its register ring and
 // activation passes; the fused mode takes bf16 x only)
 bool decode_fits(int K, int M, int W, int nw, bool packed, int x_dt);
+// 16-row tiles per workgroup of a decode launch (1, 2 or 4) for nprob
+// problems of `tiles` row tiles each; results do not depend on it
+int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob);
 size_t stream_lds_bytes(int K, int M, int nw);
 
 }  // namespace actune

@@ -334,3 +334,42 @@ def test_activation_regimes_bit_exact_every_config(regime, W, A):
                 continue
             out = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, config=config)
             np.testing.assert_array_equal(bits(out), want, err_msg=f"m={m} config={config}")
+
+
+@pytest.mark.parametrize("W,A", [(4, 8), (2, 4), (8, 2)])
+@pytest.mark.parametrize("m", [5, 8])
+@pytest.mark.parametrize("n", [6000, 10200])
+def test_decode_shared_row_tiles(W, A, m, n):
+    """8-token decode launches wide enough to share a workgroup between two
+    (N = 6000) or four (N = 10200) 16-row tiles, N ragged: x quantized in the
+    launch (with and without the channel scale) and the quantizer's codes
+    both equal the oracle bit for bit, and so do three sibling targets in one
+    launch."""
+    k = 1024
+    x, w, b = seeded_inputs(m, k, n, seed=n + 13 * W + A + m, bias=True)
+    wc, wsc, w_dev, ws_dev = _packed_weight(w, W, A)
+    xd, bd = x.to(DEV), b.to(DEV)
+    scale = torch.linspace(0.5, 2.0, k).to(torch.bfloat16)
+    for sc in (None, scale):
+        sd = None if sc is None else sc.to(DEV)
+        _, a_scales, a_codes = oracle_activation(x, A, sc)
+        want = O.round_out(O.linear(a_codes, a_scales, wc, wsc, b.float().numpy(), bounds=canonical_bounds(k // 64)), "bf16")
+        fused = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, input_scale=sd, config=16)
+        np.testing.assert_array_equal(bits(fused), want, err_msg=f"fused scale={sc is not None}")
+        p, s = _native.quantize_groups(xd, A, sd)
+        for config in (15, 16):
+            packed = _native.grouped_linear(p, s, w_dev, ws_dev, bd, xd, W, A, config)
+            np.testing.assert_array_equal(bits(packed), want, err_msg=f"packed config={config}")
+    # three siblings of width n / 3 (rounded to 8) share one launch
+    nt = (n // 3) // 8 * 8
+    targets, wants = [], []
+    _, a_scales, a_codes = oracle_activation(x, A)
+    for j in range(3):
+        _, wj, bj = seeded_inputs(1, k, nt, seed=500 + j + n, bias=True)
+        wcj, wscj, wdj, wsdj = _packed_weight(wj, W, A)
+        targets.append((wdj, wsdj, bj.to(DEV), None))
+        wants.append(O.round_out(O.linear(a_codes, a_scales, wcj, wscj, bj.float().numpy(),
+                                          bounds=canonical_bounds(k // 64)), "bf16"))
+    outs = _native.grouped_forward_multi(xd, targets, W, A, config=16)
+    for j, (out, want) in enumerate(zip(outs, wants)):
+        np.testing.assert_array_equal(bits(out), want, err_msg=f"sibling {j}")

@@ -53,14 +53,17 @@ def test_config_table():
     assert _native.default_config(1, 4096, 4096, 8, 8) == 15   # W8: 8 groups per ring
     assert _native.default_config(1, 1024, 4096, 4, 8) == 16   # 64 tiles: 16 waves each
     assert _native.default_config(1, 4096, 65536, 4, 8) == 2   # no decode config fits
-    # M = 8: 8 waves quantize their 8 groups x 8 tokens in the launch; for
-    # K = 11008 no wave count both fits its ring and quantizes its range, so
-    # 16 waves take the quantizer's codes
-    assert _native.default_config(8, 4096, 4096, 4, 8) == 15
+    # M = 8: 16 waves quantize x in the launch, up to four row tiles sharing a
+    # workgroup; for K = 11008 no wave count both fits its ring and quantizes
+    # its range, so 16 waves take the quantizer's codes
+    assert _native.default_config(8, 4096, 4096, 4, 8) == 16
+    assert _native.default_config(8, 11008, 4096, 4, 8) == 16
     assert _native.default_config(8, 4096, 11008, 4, 8) == 16
-    # wide N: every workgroup would quantize all of x, so 4 waves take codes
-    assert _native.default_config(8, 11008, 4096, 4, 8) == 14
-    assert _native.default_config(3, 11008, 4096, 4, 8) == 15  # still fused
+    # very wide N: in-launch quantization too heavy even shared by four tiles,
+    # so 8 waves take the codes
+    assert _native.default_config(8, 22016, 4096, 4, 8) == 15
+    assert _native.default_config(3, 11008, 4096, 4, 8) == 15  # fused, 8 waves
+    assert _native.default_config(4, 12288, 4096, 4, 8) == 14  # codes, 4 waves
     assert _native.default_config(9, 4096, 4096, 4, 8) not in (14, 15, 16)
 
 
