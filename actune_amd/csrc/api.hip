@@ -199,30 +199,39 @@ int actune_config_valid(int config, int64_t M) {
 int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
   // Decode (M <= 8, measured on MI355X at W4A8 Llama/Gemma shapes): the
   // decode kernel beats the small-M and streaming kernels wherever a wave's
-  // K-range fits its load ring. M <= 4: fewer waves per tile cost less
-  // per-workgroup work, so take the smallest wave count that still gives
-  // every SIMD a wave (tiles x waves >= 1024) and fits K: first with bf16 x
-  // quantized in the launch where that pays (decode_light), then with the
-  // quantizer's codes.
-  if (M >= 1 && M <= kFusedMaxM) {
-    const int64_t tiles = (N + 15) / 16;
-    for (int packed = 0; packed < 2; ++packed)
-      for (int c = 0; c < 3; ++c) {
-        const int nw = kSmallMWaves[c];
-        if (!(tiles * nw >= 1024 || nw == kSmallMWaves[2])) continue;
-        if (decode_fits((int)K, (int)M, W, nw, packed, kBF16) && (packed || decode_light(M, N, K, W, nw)))
-          return kDecodeFirst + c;
-      }
-  } else if (M > kFusedMaxM && M <= kDecodeMax) {
-    // 8-token tiles (measured, W4A8 M = 5..8): x quantized in the launch by
-    // 16 waves, whose short K-ranges let up to four row tiles share a
-    // workgroup and its quantized x, where that stays light; otherwise the
-    // quantizer's codes with 4 waves (8 from 1024 row tiles on)
-    if (decode_fits((int)K, (int)M, W, 16, false, kBF16) && decode_light(M, N, K, W, 16)) return kDecodeFirst + 2;
-    const int64_t tiles = (N + 15) / 16;
+  // K-range fits its load ring.
+  const int64_t tiles = (N + 15) / 16;
+  auto fused_at = [&](int c) {
+    const int nw = kSmallMWaves[c];
+    return decode_fits((int)K, (int)M, W, nw, false, kBF16) && decode_light(M, N, K, W, nw);
+  };
+  auto packed_at = [&](int c) { return decode_fits((int)K, (int)M, W, kSmallMWaves[c], true, kBF16); };
+  if (M >= 2 && M <= kDecodeMax && tiles > 256) {
+    // Wide N: several row tiles share a workgroup and its quantized x
+    // (decode_row_tiles); 16 waves, whose short K-ranges allow four tiles,
+    // below 1024 row tiles, 8 waves from there on; x quantized in the launch
+    // where that stays light, else the quantizer's codes.
+    const int pref = tiles >= 1024 ? 1 : 2;
+    if (fused_at(pref)) return kDecodeFirst + pref;
     const int order[3] = {tiles >= 1024 ? 1 : 0, tiles >= 1024 ? 0 : 1, 2};
     for (int c : order)
-      if (decode_fits((int)K, (int)M, W, kSmallMWaves[c], true, kBF16)) return kDecodeFirst + c;
+      if (packed_at(c)) return kDecodeFirst + c;
+  } else if (M > kFusedMaxM && M <= kDecodeMax) {
+    // narrow N, 8-token tiles: 16 waves quantize x in the launch where light,
+    // else the quantizer's codes with the fewest waves that fit
+    if (fused_at(2)) return kDecodeFirst + 2;
+    for (int c = 0; c < 3; ++c)
+      if (packed_at(c)) return kDecodeFirst + c;
+  } else if (M >= 1 && M <= kFusedMaxM) {
+    // narrow N, M <= 4: fewer waves per tile cost less per-workgroup work, so
+    // take the smallest wave count that still gives every SIMD a wave (tiles
+    // x waves >= 1024) and fits K: first with bf16 x quantized in the launch
+    // where that pays (decode_light), then with the quantizer's codes.
+    for (int packed = 0; packed < 2; ++packed)
+      for (int c = 0; c < 3; ++c) {
+        if (!(tiles * kSmallMWaves[c] >= 1024 || c == 2)) continue;
+        if (packed ? packed_at(c) : fused_at(c)) return kDecodeFirst + c;
+      }
   }
   return packed_default(M, N, K, W, A);
 }

@@ -83,11 +83,11 @@ size_t decode_lds_bytes(int K, int M, int nw, int tr) {
 // with four).
 constexpr int kDecodeMinGroups = 160;
 
-// Row tiles per workgroup for an 8-token tile: the most (up to 4) whose weight
-// slots still fit the ring, keeping at least kDecodeMinGroups workgroups over
-// the nprob problems of `tiles` row tiles each.
+// Row tiles per workgroup for M > 1: the most (up to 4) whose weight slots
+// still fit the ring, keeping at least kDecodeMinGroups workgroups over the
+// nprob problems of `tiles` row tiles each.
 int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob) {
-  if (decode_token_tile(M) != 8) return 1;
+  if (M < 2) return 1;
   const int slots = (decode_groups_per_wave(K, nw) + 8 / W - 1) / (8 / W);
   int tr = 1;
   for (int c = 2; c <= 4; c *= 2)
@@ -510,14 +510,14 @@ static void launch_decode_one(const LinearArgs& g, hipStream_t st) {
   kern<<<dim3((unsigned)groups, (unsigned)g.nprob), NW * 64, lds, st>>>(g, decode_groups_per_wave(g.K, NW));
 }
 
-// 8-token launches: TR row tiles per workgroup (decode_row_tiles)
-template <int W, int A, int NW, bool PACKED, bool SCALE>
-static void launch_decode_mt8(const LinearArgs& g, hipStream_t st) {
+// M > 1: TR row tiles per workgroup (decode_row_tiles)
+template <int W, int A, int NW, int MT, bool PACKED, bool SCALE>
+static void launch_decode_tr(const LinearArgs& g, hipStream_t st) {
   const int tr = decode_row_tiles(g.K, g.M, W, NW, decode_max_tiles(g), g.nprob);
   const bool full = decode_full(g.K, W, NW, tr);
 #define DEC_TR(TRV)                                                                      \
-  if (full) launch_decode_one<W, A, NW, 8, PACKED, SCALE, false, true, TRV>(g, st);      \
-  else launch_decode_one<W, A, NW, 8, PACKED, SCALE, false, false, TRV>(g, st)
+  if (full) launch_decode_one<W, A, NW, MT, PACKED, SCALE, false, true, TRV>(g, st);     \
+  else launch_decode_one<W, A, NW, MT, PACKED, SCALE, false, false, TRV>(g, st)
   if (tr == 4) { DEC_TR(4); }
   else if (tr == 2) { DEC_TR(2); }
   else { DEC_TR(1); }
@@ -529,8 +529,8 @@ static void launch_decode_nw(bool packed, const LinearArgs& g, hipStream_t st) {
   const bool full = decode_full(g.K, W, NW), scale = g.xscale != nullptr;
   if (packed) {
     if (g.M == 1) launch_decode_one<W, A, NW, 4, true, false, true, false>(g, st);
-    else if (g.M <= 4) launch_decode_one<W, A, NW, 4, true, false, false, false>(g, st);
-    else launch_decode_mt8<W, A, NW, true, false>(g, st);
+    else if (g.M <= 4) launch_decode_tr<W, A, NW, 4, true, false>(g, st);
+    else launch_decode_tr<W, A, NW, 8, true, false>(g, st);
     return;
   }
 #define DEC_FULL(MTV, SC, ONEV)                                                 \
@@ -540,11 +540,11 @@ static void launch_decode_nw(bool packed, const LinearArgs& g, hipStream_t st) {
     if (scale) { DEC_FULL(4, true, true); }
     else { DEC_FULL(4, false, true); }
   } else if (g.M <= 4) {
-    if (scale) { DEC_FULL(4, true, false); }
-    else { DEC_FULL(4, false, false); }
+    if (scale) launch_decode_tr<W, A, NW, 4, false, true>(g, st);
+    else launch_decode_tr<W, A, NW, 4, false, false>(g, st);
   } else {
-    if (scale) launch_decode_mt8<W, A, NW, false, true>(g, st);
-    else launch_decode_mt8<W, A, NW, false, false>(g, st);
+    if (scale) launch_decode_tr<W, A, NW, 8, false, true>(g, st);
+    else launch_decode_tr<W, A, NW, 8, false, false>(g, st);
   }
 #undef DEC_FULL
 }

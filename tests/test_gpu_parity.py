@@ -337,10 +337,10 @@ def test_activation_regimes_bit_exact_every_config(regime, W, A):
 
 
 @pytest.mark.parametrize("W,A", [(4, 8), (2, 4), (8, 2)])
-@pytest.mark.parametrize("m", [5, 8])
+@pytest.mark.parametrize("m", [2, 4, 5, 8])
 @pytest.mark.parametrize("n", [6000, 10200])
 def test_decode_shared_row_tiles(W, A, m, n):
-    """8-token decode launches wide enough to share a workgroup between two
+    """Decode launches (4- and 8-token tiles) wide enough to share a workgroup between two
     (N = 6000) or four (N = 10200) 16-row tiles, N ragged: x quantized in the
     launch (with and without the channel scale) and the quantizer's codes
     both equal the oracle bit for bit, and so do three sibling targets in one

@@ -62,8 +62,12 @@ def test_config_table():
     # very wide N: in-launch quantization too heavy even shared by four tiles,
     # so 8 waves take the codes
     assert _native.default_config(8, 22016, 4096, 4, 8) == 15
-    assert _native.default_config(3, 11008, 4096, 4, 8) == 15  # fused, 8 waves
-    assert _native.default_config(4, 12288, 4096, 4, 8) == 14  # codes, 4 waves
+    # M = 2..4, wide N: 16 waves and four row tiles per workgroup below 1024
+    # row tiles, 8 waves and two tiles from there on
+    assert _native.default_config(3, 11008, 4096, 4, 8) == 16
+    assert _native.default_config(4, 12288, 4096, 4, 8) == 16
+    assert _native.default_config(4, 22016, 4096, 4, 8) == 15
+    assert _native.default_config(2, 4096, 4096, 4, 8) == 14  # narrow N: as for M = 1
     assert _native.default_config(9, 4096, 4096, 4, 8) not in (14, 15, 16)
 
 
