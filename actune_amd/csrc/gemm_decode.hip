@@ -8,11 +8,12 @@
 // canonical chunked order of common.hpp.
 //
 // Structure:
-//  * A workgroup is NW waves and owns one 16-row tile of one problem (up to
-//    kMaxProblems linears that read the same activations share a launch; the
-//    problem is blockIdx.y, so each workgroup reads only its own problem's
-//    kernel arguments, in one batch of scalar loads before its first memory
-//    load). The waves split K along the 16 canonical chunks.
+//  * A workgroup is NW waves and owns TR (1, 2 or 4; 1 at M = 1) consecutive
+//    16-row tiles of one problem (up to kMaxProblems linears that read the
+//    same activations share a launch; the problem is blockIdx.y, so each
+//    workgroup reads only its own problem's kernel arguments, in one batch of
+//    scalar loads before its first memory load). The waves split K along the
+//    16 canonical chunks; the tiles share the activation slab.
 //  * Each wave issues all its loads at entry: its activation passes, then its
 //    whole K-range of weights as RING 16-byte loads per lane at constant
 //    offsets (lanes of a row fetch 64 consecutive bytes; passes and slots
@@ -27,8 +28,8 @@
 //    before slot s's results are rescaled. The tokens are the MFMA A operand
 //    (token m of weight row c lands in lane 16*(m/4) + c, register m%4); one
 //    fp32 FMA per (row, token, group) rescales the exact int32 dot.
-//  * Chunk partials meet in LDS [16 chunks][16 rows][MT tokens] and are added
-//    in chunk order after one barrier.
+//  * Chunk partials meet in LDS [16 chunks][16 * TR rows][MT tokens] and are
+//    added in chunk order after one barrier (wave t finishes tile t).
 #include <algorithm>
 
 #include "common.hpp"
