@@ -340,11 +340,11 @@ def test_activation_regimes_bit_exact_every_config(regime, W, A):
 @pytest.mark.parametrize("m", [2, 4, 5, 8])
 @pytest.mark.parametrize("n", [6000, 10200])
 def test_decode_shared_row_tiles(W, A, m, n):
-    """Decode launches (4- and 8-token tiles) wide enough to share a workgroup between two
-    (N = 6000) or four (N = 10200) 16-row tiles, N ragged: x quantized in the
-    launch (with and without the channel scale) and the quantizer's codes
-    both equal the oracle bit for bit, and so do three sibling targets in one
-    launch."""
+    """Decode launches (4- and 8-token tiles) wide enough to share a
+    workgroup between two (N = 6000) or four (N = 10200) 16-row tiles, N
+    ragged: x quantized in the launch (with and without the channel scale)
+    and the quantizer's codes both equal the oracle bit for bit, and so do
+    three sibling targets of ragged widths in one launch."""
     k = 1024
     x, w, b = seeded_inputs(m, k, n, seed=n + 13 * W + A + m, bias=True)
     wc, wsc, w_dev, ws_dev = _packed_weight(w, W, A)
@@ -360,12 +360,13 @@ def test_decode_shared_row_tiles(W, A, m, n):
         for config in (15, 16):
             packed = _native.grouped_linear(p, s, w_dev, ws_dev, bd, xd, W, A, config)
             np.testing.assert_array_equal(bits(packed), want, err_msg=f"packed config={config}")
-    # three siblings of width n / 3 (rounded to 8) share one launch
+    # three siblings of ragged widths around n / 3 share one launch (the
+    # narrower ones leave workgroups and tiles of the shared grid empty)
     nt = (n // 3) // 8 * 8
     targets, wants = [], []
     _, a_scales, a_codes = oracle_activation(x, A)
-    for j in range(3):
-        _, wj, bj = seeded_inputs(1, k, nt, seed=500 + j + n, bias=True)
+    for j, nj in enumerate((nt, nt // 4 // 8 * 8, nt + 40)):
+        _, wj, bj = seeded_inputs(1, k, nj, seed=500 + j + n, bias=True)
         wcj, wscj, wdj, wsdj = _packed_weight(wj, W, A)
         targets.append((wdj, wsdj, bj.to(DEV), None))
         wants.append(O.round_out(O.linear(a_codes, a_scales, wcj, wscj, bj.float().numpy(),
