@@ -23,8 +23,8 @@ constexpr int kStreamMax = 16;
 constexpr int kStreamConfigs = 3;
 constexpr int kPrefillFirst = kStreamFirst + kStreamConfigs;  // ids 10..13: prefill kernel, any M
 constexpr int kPrefillConfigs = 4;
-constexpr int kDecodeFirst = kPrefillFirst + kPrefillConfigs;  // ids 14..16: decode kernel, M <= 8
-constexpr int kDecodeMax = 8;
+constexpr int kDecodeFirst = kPrefillFirst + kPrefillConfigs;  // ids 14..16: decode kernel, M <= 16
+constexpr int kDecodeMax = 16;
 constexpr int kFusedMaxM = 4;      // small-M and streaming calls up to this M quantize inside the GEMM
 constexpr int kSmallMWaves[kSmallMConfigs] = {4, 8, 16};
 thread_local char g_err[512];
@@ -70,7 +70,7 @@ int check_shape(int64_t M, int64_t K, int W, int A, int out_dt, int bias_dt, int
   if (config < kSmallMConfigs && M > kSmallMMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
   if (config >= kStreamFirst && config < kPrefillFirst && M > kStreamMax)
     return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 16");
-  if (config >= kDecodeFirst && M > kDecodeMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 8");
+  if (config >= kDecodeFirst && M > kDecodeMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 16");
   return ACTUNE_OK;
 }
 
@@ -106,8 +106,8 @@ bool decode_fused(int64_t M, int64_t n_total, int64_t K, int W, int nw, int x_dt
 }
 
 // ACTUNE_CONFIG_AUTO: calls that hand over x (and may fuse the quantizer) use
-// actune_default_config; calls on packed activations use packed_default,
-// which never picks a decode config (those need x).
+// actune_default_config; calls on packed activations use packed_default (the
+// same choice without the in-launch quantization).
 int resolve(int config, int64_t M, int64_t N, int64_t K, int W, int A, bool has_x) {
   if (config != ACTUNE_CONFIG_AUTO) return config;
   return has_x ? actune_default_config(M, N, K, W, A) : packed_default(M, N, K, W, A);
@@ -197,53 +197,68 @@ int actune_config_valid(int config, int64_t M) {
 }
 
 int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
-  // Decode (M <= 8, measured on MI355X at W4A8 Llama/Gemma shapes): the
+  // Decode (M <= 16, measured on MI355X at W4A8 Llama/Gemma shapes): the
   // decode kernel beats the small-M and streaming kernels wherever a wave's
-  // K-range fits its load ring.
+  // K-range fits its load ring. Calls that hand over bf16 x first try to
+  // quantize it inside the launch (M <= 8), then use the quantizer's codes.
   const int64_t tiles = (N + 15) / 16;
   auto fused_at = [&](int c) {
     const int nw = kSmallMWaves[c];
     return decode_fits((int)K, (int)M, W, nw, false, kBF16) && decode_light(M, N, K, W, nw);
   };
-  auto packed_at = [&](int c) { return decode_fits((int)K, (int)M, W, kSmallMWaves[c], true, kBF16); };
   if (M >= 2 && M <= kDecodeMax && tiles > 256) {
     // Wide N: several row tiles share a workgroup and its quantized x
     // (decode_row_tiles); 16 waves, whose short K-ranges allow four tiles,
-    // below 1024 row tiles, 8 waves from there on; x quantized in the launch
-    // where that stays light, else the quantizer's codes.
+    // below 1024 row tiles, 8 waves from there on.
     const int pref = tiles >= 1024 ? 1 : 2;
     if (fused_at(pref)) return kDecodeFirst + pref;
-    const int order[3] = {tiles >= 1024 ? 1 : 0, tiles >= 1024 ? 0 : 1, 2};
-    for (int c : order)
-      if (packed_at(c)) return kDecodeFirst + c;
   } else if (M > kFusedMaxM && M <= kDecodeMax) {
-    // narrow N, 8-token tiles: 16 waves quantize x in the launch where light,
-    // else the quantizer's codes with the fewest waves that fit
+    // narrow N, 8-token tiles: 16 waves quantize x in the launch where light
     if (fused_at(2)) return kDecodeFirst + 2;
-    for (int c = 0; c < 3; ++c)
-      if (packed_at(c)) return kDecodeFirst + c;
   } else if (M >= 1 && M <= kFusedMaxM) {
     // narrow N, M <= 4: fewer waves per tile cost less per-workgroup work, so
     // take the smallest wave count that still gives every SIMD a wave (tiles
-    // x waves >= 1024) and fits K: first with bf16 x quantized in the launch
-    // where that pays (decode_light), then with the quantizer's codes.
-    for (int packed = 0; packed < 2; ++packed)
-      for (int c = 0; c < 3; ++c) {
-        if (!(tiles * kSmallMWaves[c] >= 1024 || c == 2)) continue;
-        if (packed ? packed_at(c) : fused_at(c)) return kDecodeFirst + c;
-      }
+    // x waves >= 1024) and fits K, with x quantized in the launch where that
+    // pays (decode_light)
+    for (int c = 0; c < 3; ++c) {
+      if (!(tiles * kSmallMWaves[c] >= 1024 || c == 2)) continue;
+      if (fused_at(c)) return kDecodeFirst + c;
+    }
   }
   return packed_default(M, N, K, W, A);
 }
 
 namespace {
+// The decode config for a call on packed codes, or -1 where no wave count
+// fits (measured on MI355X, W4A8): M <= 4 and narrow N, the fewest waves
+// that still give every SIMD a wave; wide N (more than 256 row tiles), 4
+// waves (16 above 8 tokens, whose tiles then share workgroups four at a
+// time) below 1024 row tiles and 8 waves from there on; narrow N above 4
+// tokens, the fewest waves that fit.
+int decode_packed_config(int64_t M, int64_t N, int64_t K, int W) {
+  if (M < 1 || M > kDecodeMax) return -1;
+  const int64_t tiles = (N + 15) / 16;
+  auto packed_at = [&](int c) { return decode_fits((int)K, (int)M, W, kSmallMWaves[c], true, kBF16); };
+  int order[3] = {0, 1, 2};
+  if (tiles > 256 && M >= 2) {
+    if (tiles >= 1024) { order[0] = 1; order[1] = M > 8 ? 2 : 0; order[2] = M > 8 ? 0 : 2; }
+    else if (M > 8) { order[0] = 2; order[1] = 1; order[2] = 0; }
+  }
+  for (int c : order) {
+    if (M <= kFusedMaxM && tiles <= 256 && !(tiles * kSmallMWaves[c] >= 1024 || c == 2)) continue;
+    if (packed_at(c)) return kDecodeFirst + c;
+  }
+  return -1;
+}
+
 int packed_default(int64_t M, int64_t N, int64_t K, int W, int A) {
-  (void)K; (void)W; (void)A;
-  // Measured on MI355X (W4A8, Llama/Gemma shapes): the one-tile-per-CU
-  // small-M kernel with 16 waves is fastest for decode shapes of up to ~512
-  // row tiles; beyond that, and for M > 4, the persistent streaming kernel
-  // with 8 waves wins (it keeps the next tile's weights in flight and
-  // quantizes once per workgroup).
+  (void)A;
+  const int dec = decode_packed_config(M, N, K, W);
+  if (dec >= 0) return dec;
+  // Measured on MI355X (W4A8, Llama/Gemma shapes), where the decode kernel
+  // does not fit: the one-tile-per-CU small-M kernel with 16 waves up to
+  // ~512 row tiles; beyond that, and for M > 4, the persistent streaming
+  // kernel with 8 waves (it keeps the next tile's weights in flight).
   const int64_t tiles = (N + 15) / 16;
   if (M <= kFusedMaxM) return tiles >= 512 ? kStreamFirst + 1 : 2;
   if (M <= kStreamMax) return tiles >= 512 ? kStreamFirst + 1 : kStreamFirst + 2;

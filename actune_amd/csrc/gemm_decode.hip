@@ -1,4 +1,4 @@
-// Decode packed group-64 GEMM for gfx950 (M <= 8 tokens): the launch is bound
+// Decode packed group-64 GEMM for gfx950 (M <= 16 tokens): the launch is bound
 // by the HBM read of the packed weights, so the kernel is shaped to start
 // that read early and keep all of it in flight.
 //
@@ -38,17 +38,19 @@
 
 namespace actune {
 
-constexpr int kDecodeMaxM = 8;
+constexpr int kDecodeMaxM = 16;
 // zero region: a wave's widest K-range (16 groups) of 64-byte zero rows
 constexpr int kDecodeZeroBytes = 16 * kGroup;
 
 // 16-byte weight loads per lane: 16 groups of W2 / W4, 8 groups of W8
 __host__ __device__ constexpr int decode_ring(int W) { return W == 2 ? 4 : 8; }
-// token tile: tokens 0..3 land in lanes 0..15, tokens 4..7 in lanes 16..31
-static int decode_token_tile(int M) { return M <= 4 ? 4 : 8; }
+// token tile: tokens 4j..4j+3 land in lanes 16j..16j+15
+static int decode_token_tile(int M) { return M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 // activation passes a wave issues up front: fused passes quantize 8
-// group-rows, packed passes unpack 16
-__host__ __device__ constexpr int decode_passes(int MT, bool packed) { return packed ? MT : (MT == 8 ? 8 : 4); }
+// group-rows (M <= 8 only), packed passes unpack 16
+__host__ __device__ constexpr int decode_passes(int MT, bool packed) {
+  return packed ? (MT < 8 ? MT : 8) : (MT == 8 ? 8 : 4);
+}
 
 // Largest groups per wave of a K split over nw waves.
 static int decode_groups_per_wave(int K, int nw) {
@@ -99,7 +101,7 @@ int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob) {
 }
 
 bool decode_fits(int K, int M, int W, int nw, bool packed, int x_dt) {
-  if (!packed && x_dt != kBF16) return false;  // fused mode quantizes bf16 x
+  if (!packed && (x_dt != kBF16 || M > 8)) return false;  // fused mode: bf16 x, M <= 8
   if (M < 1 || M > kDecodeMaxM || (nw != 4 && nw != 8 && nw != 16)) return false;
   const int gw = decode_groups_per_wave(K, nw), gps = 8 / W;
   if ((gw + gps - 1) / gps > decode_ring(W)) return false;
@@ -137,6 +139,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   constexpr bool FAST = ONE;
   constexpr int PR = PACKED ? 16 : 8;      // group-rows per activation pass
   constexpr int NPX = FULL && ONE && !PACKED ? (RING * GS + 7) / 8 : decode_passes(MT, PACKED);
+  static_assert(MT == 4 || MT == 8 || (MT == 16 && PACKED), "token tiles of 4, 8 or (codes only) 16");
   static_assert(!ONE || MT == 4, "M == 1 uses the 4-token tile");
   static_assert(!ONE || TR == 1, "M == 1 launches own one row tile per workgroup");
   static_assert(TR <= NW, "waves 0..TR-1 finish one tile each");
@@ -531,7 +534,8 @@ static void launch_decode_nw(bool packed, const LinearArgs& g, hipStream_t st) {
   if (packed) {
     if (g.M == 1) launch_decode_one<W, A, NW, 4, true, false, true, false>(g, st);
     else if (g.M <= 4) launch_decode_tr<W, A, NW, 4, true, false>(g, st);
-    else launch_decode_tr<W, A, NW, 8, true, false>(g, st);
+    else if (g.M <= 8) launch_decode_tr<W, A, NW, 8, true, false>(g, st);
+    else launch_decode_tr<W, A, NW, 16, true, false>(g, st);
     return;
   }
 #define DEC_FULL(MTV, SC, ONEV)                                                 \

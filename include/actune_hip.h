@@ -117,15 +117,17 @@ int actune_grouped_dots_i32(const uint8_t* a, const uint8_t* w, int64_t M, int64
  *   7, 8, 9  persistent streaming kernel with 4, 8, 16 waves (M <= 16)
  *   10 .. 13 prefill kernel (weights streamed per wave, activations staged
  *            per workgroup) with tiles 128x64, 128x32, 64x64, 64x32 (any M)
- *   14 .. 16 decode kernel with 4, 8, 16 waves (M <= 8; bf16 x quantized
- *            in the launch, other dtypes and longer K-ranges through the
- *            quantizer launch; a K too long for a wave's load ring and the
- *            dots mode run the small-M kernel with the same waves)
+ *   14 .. 16 decode kernel with 4, 8, 16 waves (M <= 16; bf16 x quantized
+ *            in the launch up to M = 8, other dtypes, more tokens and longer
+ *            K-ranges through the quantizer launch; a K too long for a
+ *            wave's load ring and the dots mode run the small-M kernel with
+ *            the same waves)
  * actune_config_valid: 1 if `config` can run a call with M rows.
  * actune_default_config: the config ACTUNE_CONFIG_AUTO resolves to in
  *   actune_grouped_forward(_multi). actune_grouped_linear and
  *   actune_grouped_dots_i32 (packed activations) resolve AUTO to the same
- *   choice except that they never pick a decode config.
+ *   kernels without the in-launch quantization (a decode config where the
+ *   decode kernel fits the codes).
  */
 int actune_num_configs(void);
 int actune_config_valid(int config, int64_t M);

@@ -185,7 +185,7 @@ def test_full_size_sampled_parity(m, n, k, W, A):
 
 # ---------------------------------------------------------------- fused / siblings
 @pytest.mark.parametrize("W,A", PAIRS)
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 12, 16])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_fused_small_m_equals_two_step(W, A, m, dtype):
     """Small-M (fused for M <= 4) and decode configs (fused for bf16 x up to
@@ -211,7 +211,7 @@ def test_fused_small_m_equals_two_step(W, A, m, dtype):
 
 
 @pytest.mark.parametrize("W,A", [(4, 8), (2, 4), (8, 8), (8, 2)])
-@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("m", [1, 4, 8, 16])
 @pytest.mark.parametrize("k", [4096, 8192, 11008])
 def test_decode_full_ring_equals_small_m(W, A, m, k):
     """Decode configs at K where a wave's weight range fills its load ring
@@ -337,7 +337,7 @@ def test_activation_regimes_bit_exact_every_config(regime, W, A):
 
 
 @pytest.mark.parametrize("W,A", [(4, 8), (2, 4), (8, 2)])
-@pytest.mark.parametrize("m", [2, 4, 5, 8])
+@pytest.mark.parametrize("m", [2, 4, 5, 8, 12, 16])
 @pytest.mark.parametrize("n", [6000, 10200])
 def test_decode_shared_row_tiles(W, A, m, n):
     """Decode launches (4- and 8-token tiles) wide enough to share a

@@ -40,7 +40,7 @@ def test_config_table():
     assert _native.config_valid(0, 64) and not _native.config_valid(0, 65)
     assert all(_native.config_valid(c, 4096) for c in range(3, 7))
     assert all(_native.config_valid(c, 1) and _native.config_valid(c, 4096) for c in range(10, 14))
-    assert all(_native.config_valid(c, 8) and not _native.config_valid(c, 9) for c in range(14, 17))
+    assert all(_native.config_valid(c, 16) and not _native.config_valid(c, 17) for c in range(14, 17))
     assert _native.config_valid(9, 16) and not _native.config_valid(9, 17)
     assert not _native.config_valid(n, 1) and not _native.config_valid(-2, 1)
     for m in (1, 8, 16, 17, 50, 512):
@@ -68,7 +68,14 @@ def test_config_table():
     assert _native.default_config(4, 12288, 4096, 4, 8) == 16
     assert _native.default_config(4, 22016, 4096, 4, 8) == 15
     assert _native.default_config(2, 4096, 4096, 4, 8) == 14  # narrow N: as for M = 1
-    assert _native.default_config(9, 4096, 4096, 4, 8) not in (14, 15, 16)
+    # M = 9..16: the quantizer's codes (16-token tile); 16 waves and shared
+    # row tiles below 1024 row tiles, 8 waves from there on and for narrow N;
+    # K = 11008 fits no wave count at 16 tokens: the streaming kernel
+    assert _native.default_config(16, 12288, 4096, 4, 8) == 16
+    assert _native.default_config(12, 22016, 4096, 4, 8) == 15
+    assert _native.default_config(16, 4096, 4096, 4, 8) == 15
+    assert _native.default_config(16, 4096, 11008, 4, 8) == 9
+    assert _native.default_config(17, 4096, 4096, 4, 8) not in (14, 15, 16)  # decode: M <= 16
 
 
 def _err():
