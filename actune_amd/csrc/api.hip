@@ -23,8 +23,8 @@ constexpr int kStreamMax = 16;
 constexpr int kStreamConfigs = 3;
 constexpr int kPrefillFirst = kStreamFirst + kStreamConfigs;  // ids 10..13: prefill kernel, any M
 constexpr int kPrefillConfigs = 4;
-constexpr int kDecodeFirst = kPrefillFirst + kPrefillConfigs;  // ids 14..16: decode kernel, M <= 16
-constexpr int kDecodeMax = 16;
+constexpr int kDecodeFirst = kPrefillFirst + kPrefillConfigs;  // ids 14..16: decode kernel, M <= 64
+constexpr int kDecodeMax = 64;
 constexpr int kFusedMaxM = 4;      // small-M and streaming calls up to this M quantize inside the GEMM
 constexpr int kSmallMWaves[kSmallMConfigs] = {4, 8, 16};
 thread_local char g_err[512];
@@ -69,8 +69,8 @@ int check_shape(int64_t M, int64_t K, int W, int A, int out_dt, int bias_dt, int
   if (config < 0 || config >= kNumConfigs) return fail(ACTUNE_ERR_INVALID, "invalid configuration");
   if (config < kSmallMConfigs && M > kSmallMMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
   if (config >= kStreamFirst && config < kPrefillFirst && M > kStreamMax)
-    return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 16");
-  if (config >= kDecodeFirst && M > kDecodeMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 16");
+    return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
+  if (config >= kDecodeFirst && M > kDecodeMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
   return ACTUNE_OK;
 }
 
@@ -175,6 +175,8 @@ LinearArgs base_args(int64_t M, int64_t K, int bias_dt, int out_dt) {
   g.bias_dt = bias_dt;
   g.out_dt = out_dt;
   g.m_div = M > 0 ? (uint32_t)((65536 + M - 1) / M) : 0u;
+  const int64_t tail = M > 0 ? M - 16 * ((M - 1) / 16) : 0;
+  g.m_div_tail = tail > 0 ? (uint32_t)((65536 + tail - 1) / tail) : 0u;
   return g;
 }
 
@@ -230,11 +232,12 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
 
 namespace {
 // The decode config for a call on packed codes, or -1 where no wave count
-// fits (measured on MI355X, W4A8): M <= 4 and narrow N, the fewest waves
-// that still give every SIMD a wave; wide N (more than 256 row tiles), 4
-// waves (16 above 8 tokens, whose tiles then share workgroups four at a
-// time) below 1024 row tiles and 8 waves from there on; narrow N above 4
-// tokens, the fewest waves that fit.
+// fits (measured on MI355X, W2/W4/W8 x A4/A8, M = 1..64): M <= 4 and narrow
+// N, the fewest waves that still give every SIMD a wave; wide N (more than
+// 256 row tiles), 4 waves (16 above 8 tokens, whose tiles then share
+// workgroups four at a time) below 1024 row tiles and 8 waves from there on;
+// narrow N above 4 tokens, the fewest waves that fit, except 16 waves for
+// 256 row tiles with K >= 4096 at W8 or above 32 tokens.
 int decode_packed_config(int64_t M, int64_t N, int64_t K, int W) {
   if (M < 1 || M > kDecodeMax) return -1;
   const int64_t tiles = (N + 15) / 16;
@@ -243,6 +246,8 @@ int decode_packed_config(int64_t M, int64_t N, int64_t K, int W) {
   if (tiles > 256 && M >= 2) {
     if (tiles >= 1024) { order[0] = 1; order[1] = M > 8 ? 2 : 0; order[2] = M > 8 ? 0 : 2; }
     else if (M > 8) { order[0] = 2; order[1] = 1; order[2] = 0; }
+  } else if (M > 8 && tiles >= 256 && K >= 4096 && (W == 8 || M > 32)) {
+    order[0] = 2; order[1] = 1; order[2] = 0;
   }
   for (int c : order) {
     if (M <= kFusedMaxM && tiles <= 256 && !(tiles * kSmallMWaves[c] >= 1024 || c == 2)) continue;

@@ -1,4 +1,4 @@
-// Decode packed group-64 GEMM for gfx950 (M <= 16 tokens): the launch is bound
+// Decode packed group-64 GEMM for gfx950 (M <= 64 tokens): the launch is bound
 // by the HBM read of the packed weights, so the kernel is shaped to start
 // that read early and keep all of it in flight.
 //
@@ -38,7 +38,7 @@
 
 namespace actune {
 
-constexpr int kDecodeMaxM = 16;
+constexpr int kDecodeMaxM = 64;
 // zero region: a wave's widest K-range (16 groups) of 64-byte zero rows
 constexpr int kDecodeZeroBytes = 16 * kGroup;
 
@@ -76,6 +76,7 @@ static bool decode_full(int K, int W, int nw, int tr = 1) {
 // [GW][MT] (fp32, 2^-(sW+sA) folded in; entries of absent tokens unused), the
 // zero region, and the chunk partials red[16][16 * tr][MT].
 size_t decode_lds_bytes(int K, int M, int nw, int tr) {
+  M = M > 16 ? 16 : M;  // tokens of one 16-token block
   const int gw = decode_groups_per_wave(K, nw), MT = decode_token_tile(M);
   return (size_t)nw * gw * (M * kGroup + MT * sizeof(float)) + kDecodeZeroBytes +
          sizeof(float) * kChunks * 16 * tr * MT;
@@ -105,8 +106,8 @@ bool decode_fits(int K, int M, int W, int nw, bool packed, int x_dt) {
   if (M < 1 || M > kDecodeMaxM || (nw != 4 && nw != 8 && nw != 16)) return false;
   const int gw = decode_groups_per_wave(K, nw), gps = 8 / W;
   if ((gw + gps - 1) / gps > decode_ring(W)) return false;
-  const int per = packed ? 16 : 8;
-  if ((gw * M + per - 1) / per > decode_passes(decode_token_tile(M), packed)) return false;
+  const int per = packed ? 16 : 8, mb = M > 16 ? 16 : M;  // tokens of one 16-token block
+  if ((gw * mb + per - 1) / per > decode_passes(decode_token_tile(M), packed)) return false;
   return decode_lds_bytes(K, M, nw, 1) <= kStreamLdsMax;
 }
 
@@ -158,6 +159,16 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   asm volatile("" : "+s"(M), "+s"(K), "+s"(bias_dt), "+s"(out_dt), "+s"(m_inv), "+s"(xsrc), "+s"(xaux), "+s"(GW),
                     "+s"(pr.w), "+s"(pr.ws), "+s"(pr.bias), "+s"(pr.out), "+s"(pr.N));
   const int N = pr.N, G = K / kGroup;
+  if constexpr (MT == 16) {
+    // 16-token block blockIdx.z: its tokens, codes, scales and output rows
+    const int m0 = 16 * (int)blockIdx.z;
+    const bool last = m0 + 16 >= M;
+    m_inv = last ? args.m_div_tail : 4096u;
+    M = last ? M - m0 : 16;
+    xsrc = static_cast<const uint8_t*>(xsrc) + (size_t)m0 * (K / 8) * A;
+    xaux = static_cast<const float*>(xaux) + (size_t)m0 * G;
+    pr.out = static_cast<uint8_t*>(pr.out) + (size_t)m0 * N * (out_dt == kF32 ? 4 : 2);
+  }
   const int n0 = (int)blockIdx.x * 16 * TR;
   // blockIdx.x spans the widest problem of the launch; a narrower one's
   // workgroups past its rows leave at once (whole workgroup, before any
@@ -510,14 +521,14 @@ static void launch_decode_one(const LinearArgs& g, hipStream_t st) {
   const size_t lds = decode_lds_bytes(g.K, g.M, NW, TR);
   auto kern = gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL, TR>;
   allow_dynamic_lds<gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL, TR>>();
-  const int groups = (decode_max_tiles(g) + TR - 1) / TR;
-  kern<<<dim3((unsigned)groups, (unsigned)g.nprob), NW * 64, lds, st>>>(g, decode_groups_per_wave(g.K, NW));
+  const int groups = (decode_max_tiles(g) + TR - 1) / TR, blocks = MT == 16 ? (g.M + 15) / 16 : 1;
+  kern<<<dim3((unsigned)groups, (unsigned)g.nprob, (unsigned)blocks), NW * 64, lds, st>>>(g, decode_groups_per_wave(g.K, NW));
 }
 
 // M > 1: TR row tiles per workgroup (decode_row_tiles)
 template <int W, int A, int NW, int MT, bool PACKED, bool SCALE>
 static void launch_decode_tr(const LinearArgs& g, hipStream_t st) {
-  const int tr = decode_row_tiles(g.K, g.M, W, NW, decode_max_tiles(g), g.nprob);
+  const int tr = decode_row_tiles(g.K, g.M, W, NW, decode_max_tiles(g), g.nprob * (MT == 16 ? (g.M + 15) / 16 : 1));
   const bool full = decode_full(g.K, W, NW, tr);
 #define DEC_TR(TRV)                                                                      \
   if (full) launch_decode_one<W, A, NW, MT, PACKED, SCALE, false, true, TRV>(g, st);     \

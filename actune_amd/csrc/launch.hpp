@@ -37,6 +37,7 @@ struct LinearArgs {
   int32_t* dots;        // [M, N, K/64] (dots mode, single problem)
   int M, K, bias_dt, out_dt;
   uint32_t m_div;       // ceil(2^16 / M): idx / M == (idx * m_div) >> 16 for idx < 2^14, M <= 16
+  uint32_t m_div_tail;  // the same for the last 16-token block, M - 16 * ((M - 1) / 16) tokens
 };
 
 // The problem owning row tile `tile`. Every slot is read unconditionally and

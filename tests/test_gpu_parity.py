@@ -374,3 +374,23 @@ def test_decode_shared_row_tiles(W, A, m, n):
     outs = _native.grouped_forward_multi(xd, targets, W, A, config=16)
     for j, (out, want) in enumerate(zip(outs, wants)):
         np.testing.assert_array_equal(bits(out), want, err_msg=f"sibling {j}")
+
+
+@pytest.mark.parametrize("W,A", [(4, 8), (2, 4), (8, 4)])
+@pytest.mark.parametrize("m", [17, 24, 50, 64])
+@pytest.mark.parametrize("k", [1024, 4096])
+def test_decode_token_blocks(W, A, m, k):
+    """M = 17..64 runs the decode kernel in 16-token blocks (the last one
+    ragged): the GEMM on the quantizer's codes with 4, 8 and 16 waves and the
+    default forward equal the oracle bit for bit (N ragged)."""
+    n = 700
+    x, w, b = seeded_inputs(m, k, n, seed=m * 7 + k + W * A, bias=True)
+    wc, wsc, w_dev, ws_dev = _packed_weight(w, W, A)
+    xd, bd = x.to(DEV), b.to(DEV)
+    _, a_scales, a_codes = oracle_activation(x, A)
+    want = O.round_out(O.linear(a_codes, a_scales, wc, wsc, b.float().numpy(), bounds=canonical_bounds(k // 64)), "bf16")
+    p, s = _native.quantize_groups(xd, A)
+    for config in (14, 15, 16):
+        out = _native.grouped_linear(p, s, w_dev, ws_dev, bd, xd, W, A, config)
+        np.testing.assert_array_equal(bits(out), want, err_msg=f"config {config}")
+    np.testing.assert_array_equal(bits(_native.grouped_forward(xd, w_dev, ws_dev, bd, W, A)), want)

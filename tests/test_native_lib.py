@@ -40,7 +40,7 @@ def test_config_table():
     assert _native.config_valid(0, 64) and not _native.config_valid(0, 65)
     assert all(_native.config_valid(c, 4096) for c in range(3, 7))
     assert all(_native.config_valid(c, 1) and _native.config_valid(c, 4096) for c in range(10, 14))
-    assert all(_native.config_valid(c, 16) and not _native.config_valid(c, 17) for c in range(14, 17))
+    assert all(_native.config_valid(c, 64) and not _native.config_valid(c, 65) for c in range(14, 17))
     assert _native.config_valid(9, 16) and not _native.config_valid(9, 17)
     assert not _native.config_valid(n, 1) and not _native.config_valid(-2, 1)
     for m in (1, 8, 16, 17, 50, 512):
@@ -75,7 +75,11 @@ def test_config_table():
     assert _native.default_config(12, 22016, 4096, 4, 8) == 15
     assert _native.default_config(16, 4096, 4096, 4, 8) == 15
     assert _native.default_config(16, 4096, 11008, 4, 8) == 9
-    assert _native.default_config(17, 4096, 4096, 4, 8) not in (14, 15, 16)  # decode: M <= 16
+    # M = 17..64 (16-token blocks): the Gemma-300M expert shapes at M = 50
+    assert _native.default_config(50, 4096, 1024, 4, 4) == 14
+    assert _native.default_config(50, 1024, 4096, 8, 4) == 15
+    assert _native.default_config(50, 4096, 4096, 4, 4) == 16
+    assert _native.default_config(65, 4096, 4096, 4, 8) not in (14, 15, 16)  # decode: M <= 64
 
 
 def _err():
