@@ -64,7 +64,13 @@ __device__ __forceinline__ int pf_slot_addr(int gl, int row, int slot) {
 // partial in LDS, and group 0 adds them in chunk order at the end, so the
 // result is the canonical one bit for bit. Shapes with few tiles use it to
 // shorten each wave's serial walk over K.
-template <int W, int A, int TN, int TM, int KS, int KG, bool DOTS>
+//
+// CPS (one chunk per stage): with Q = ceil(G/4) <= kChunks every canonical
+// chunk holds at most one quad, so with KS = 1 and KG = 4 each stage is
+// exactly one chunk. The stage's first group then starts the chunk partial
+// with p = d * s, which equals fmaf(d, s, +0) bit for bit, and closing the
+// chunk is acc += p with no zeroing of p.
+template <int W, int A, int TN, int TM, int KS, int KG, bool DOTS, bool CPS>
 __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, int tiles_m) {
   constexpr int T = shift_of(W) + shift_of(A);
   constexpr int BN = 64 * TN, BM = 16 * TM;
@@ -84,6 +90,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
   // chunk partials of K groups 1..KS-1: [group - 1][wave][chunk][tile][lane] x 4
   constexpr int CPART = KS > 1 && !DOTS ? (KS - 1) * 4 * NC * TN * TM * 64 * 4 : 1;
   static_assert(KS == 1 || KS * 2 * (ABYTES + SBYTES) + CPART * 4 <= 150 * 1024, "LDS");
+  static_assert(!CPS || (KS == 1 && KG == 4 && !DOTS), "one chunk per stage: one K group of quad stages");
 
   __shared__ __align__(16) uint8_t alds[KS][2][ABYTES + SBYTES];
   __shared__ __align__(16) float cpart[CPART];
@@ -231,8 +238,9 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
 #pragma unroll
   for (int y = 0; y < TM; ++y) scl[y] = 0.0f;
   int c = kgrp * NC, cend = chunk_begin(kgrp * NC + 1, G);  // chunk being accumulated, and its end
-  // p += D[par] * scale for group gq (dots mode: store the dots of gq instead)
-  auto rescale = [&](int par, const float (&sc)[TM], int gq) {
+  // p += D[par] * scale for group gq, or p = D[par] * scale for the first
+  // group of a chunk under CPS (dots mode: store the dots of gq instead)
+  auto rescale = [&](int par, const float (&sc)[TM], int gq, bool first) {
 #pragma unroll
     for (int x = 0; x < TN; ++x)
 #pragma unroll
@@ -247,7 +255,8 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
           }
         } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) p[x][y][r] = __builtin_fmaf((float)D[par][x][y][r], sc[y], p[x][y][r]);
+          for (int r = 0; r < 4; ++r)
+            p[x][y][r] = first ? (float)D[par][x][y][r] * sc[y] : __builtin_fmaf((float)D[par][x][y][r], sc[y], p[x][y][r]);
         }
       }
   };
@@ -275,6 +284,16 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
       }
     ++c;
     cend = chunk_begin(c + 1, G);
+  };
+  // CPS: the chunk of the stage just rescaled ends here; p is overwritten by
+  // the next stage's first rescale, so it is not cleared
+  auto close_stage = [&]() {
+#pragma unroll
+    for (int x = 0; x < TN; ++x)
+#pragma unroll
+      for (int y = 0; y < TM; ++y)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[x][y][r] = acc[x][y][r] + p[x][y][r];
   };
 
   // ---------------------------------------------------------------- prologue
@@ -346,7 +365,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
         float sp[TM];  // scales of group g-1
 #pragma unroll
         for (int y = 0; y < TM; ++y) sp[y] = gl > 0 ? sq[y][gl > 0 ? gl - 1 : 0] : scl[y];
-        rescale((gl + 1) & 1, sp, g - 1);
+        rescale((gl + 1) & 1, sp, g - 1, CPS && gl == 1);
       }
       if constexpr (!DOTS) {
         // one MFMA of group g, then 8 VALU of the rescale of group g-1
@@ -355,7 +374,21 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
         }
-        if (gl % 4 == 0) {  // chunks start on quads
+        if constexpr (CPS) {
+          // the previous stage's chunk (at the first stage: p = acc = +0);
+          // the use of acc keeps the sums in this block, before the next
+          // group's products overwrite p (sunk past them, the old and new p
+          // would both be live and the loop would copy one into the other)
+          if (gl == 0) {
+            close_stage();
+#pragma unroll
+            for (int x = 0; x < TN; ++x)
+#pragma unroll
+              for (int y = 0; y < TM; ++y)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) asm volatile("" ::"v"(acc[x][y][r]));
+          }
+        } else if (gl % 4 == 0) {  // chunks start on quads
           // chunks that end before group g (the group's own last chunk closes
           // after the loop: groups past g_hi belong to no chunk of this group)
           while (g >= cend && c < (kgrp + 1) * NC - 1) close_chunk();
@@ -385,9 +418,10 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
     }
   }
   }
-  rescale((KG - 1) & 1, scl, g_lo + Qk * KG - 1);  // the last group
+  rescale((KG - 1) & 1, scl, g_lo + Qk * KG - 1, false);  // the last group
   if constexpr (DOTS) return;
-  while (c < (kgrp + 1) * NC) close_chunk();
+  if constexpr (CPS) close_stage();  // the remaining chunks are empty
+  else while (c < (kgrp + 1) * NC) close_chunk();
   if constexpr (KS > 1) {
     // group 0 adds the other groups' chunk partials in chunk order
     __syncthreads();
@@ -435,19 +469,26 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
 // Shapes (TN, TM): 0 = (2, 4) 128x64, 1 = (2, 2) 128x32, 2 = (1, 4) 64x64, 3 = (1, 2) 64x32.
 template <int W, int A, bool DOTS>
 static void launch_prefill_shape(int shape, const LinearArgs& g, hipStream_t st) {
-#define PREFILL(TN, TM, KS, KG)                                                               \
-  gemm_prefill<W, A, TN, TM, KS, KG, DOTS><<<dim3((unsigned)(tn * tm)), 256 * KS, 0, st>>>(g, tm)
+#define PREFILL(TN, TM, KS, KG, CPS)                                                          \
+  gemm_prefill<W, A, TN, TM, KS, KG, DOTS, CPS><<<dim3((unsigned)(tn * tm)), 256 * KS, 0, st>>>(g, tm)
+// one K group of quad stages: one chunk per stage when ceil(G/4) <= kChunks
+#define PREFILL4(TN, TM)                                  \
+  if (!DOTS && (g.K / kGroup + 3) / 4 <= kChunks)         \
+    PREFILL(TN, TM, 1, 4, !DOTS);                         \
+  else                                                    \
+    PREFILL(TN, TM, 1, 4, false)
   const int TN_ = shape < 2 ? 2 : 1, TM_ = (shape & 1) ? 2 : 4;
   const int tn = (g.prob[0].N + 64 * TN_ - 1) / (64 * TN_), tm = (g.M + 16 * TM_ - 1) / (16 * TM_);
   switch (shape) {
-    case 0: PREFILL(2, 4, 1, 4); break;
-    case 1: PREFILL(2, 2, 1, 4); break;
-    case 2: PREFILL(1, 4, 1, 4); break;
+    case 0: PREFILL4(2, 4); break;
+    case 1: PREFILL4(2, 2); break;
+    case 2: PREFILL4(1, 4); break;
     default:
-      if (tn * tm <= kPrefillSplitTiles) PREFILL(1, 2, 2, 8);
-      else PREFILL(1, 2, 1, 4);
+      if (tn * tm <= kPrefillSplitTiles) PREFILL(1, 2, 2, 8, false);
+      else PREFILL4(1, 2);
       break;
   }
+#undef PREFILL4
 #undef PREFILL
 }
 
