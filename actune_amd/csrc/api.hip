@@ -271,11 +271,16 @@ int packed_default(int64_t M, int64_t N, int64_t K, int W, int A) {
   if (M <= kSmallMMax) return 1;
   // Prefill (measured on C3/C4 shapes): the prefill kernel with 64x64 tiles
   // when there are at least two tiles per CU, 64x32 tiles below that (more
-  // workgroups for small problems), and the LDS-staged tiled kernel for the
-  // largest problems, whose 4-wave 64x64 tiles share weight fragments in LDS.
+  // workgroups for small problems), 128x64 tiles for W <= 4 from four tiles
+  // per CU (each unpacked weight slot feeds twice the tokens; 2-7% faster at
+  // N=16384 M=256 and N=4096 M=1024; W8's 128x64 tiles hold too many
+  // registers for two waves per SIMD), and the LDS-staged tiled kernel for
+  // the largest problems, whose 4-wave 64x64 tiles share weight fragments in
+  // LDS.
   const int64_t t64 = ((N + 63) / 64) * ((M + 63) / 64);
   if (t64 < 512) return kPrefillFirst + 3;
-  if (t64 < 2048) return kPrefillFirst + 2;
+  if (t64 < 1024) return kPrefillFirst + 2;
+  if (t64 < 2048) return W <= 4 ? kPrefillFirst + 0 : kPrefillFirst + 2;
   return kSmallMConfigs;
 }
 }  // namespace

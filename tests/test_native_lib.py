@@ -80,6 +80,14 @@ def test_config_table():
     assert _native.default_config(50, 1024, 4096, 8, 4) == 15
     assert _native.default_config(50, 4096, 4096, 4, 4) == 16
     assert _native.default_config(65, 4096, 4096, 4, 8) not in (14, 15, 16)  # decode: M <= 64
+    # prefill: 64x32 tiles below two 64x64 tiles per CU, 64x64 below four,
+    # 128x64 from four for W <= 4 (W8 keeps 64x64), the tiled kernel from eight
+    assert _native.default_config(256, 2048, 2048, 4, 4) == 13
+    assert _native.default_config(512, 4096, 4096, 4, 8) == 12
+    assert _native.default_config(256, 16384, 2048, 4, 4) == 10
+    assert _native.default_config(512, 11008, 4096, 2, 8) == 10
+    assert _native.default_config(512, 11008, 4096, 8, 8) == 12
+    assert _native.default_config(2048, 4096, 4096, 4, 8) == 3
 
 
 def _err():
