@@ -183,6 +183,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   const int wg0 = chunk_begin(c_first, G), wg1 = chunk_begin(c_first + CPW, G);
   const int ng = wg1 - wg0;                 // groups of this wave
   const int ns = (ng + GS - 1) / GS;        // weight steps of this wave
+  // A FULL launch holds G = NW * RING * GS groups (every wave a full ring).
+  // When G is a multiple of 4 * kChunks every chunk has GPC = G / kChunks
+  // groups, so the slot loop closes chunk c_first + j after slot
+  // (j + 1) * GPC / GS - 1 with no scalar chunk tracking.
+  constexpr int GF = NW * RING * GS;
+  constexpr bool SC = FULL && GF % (4 * kChunks) == 0;
+  constexpr int GPC = SC ? GF / kChunks : 4;
 
   uint8_t* slab = smem + (size_t)wave * GW * M * kGroup;
   float* sslab = reinterpret_cast<float*>(smem + (size_t)NW * GW * M * kGroup) + (size_t)wave * GW * MT;
@@ -388,12 +395,20 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
         if (st + RA < RING) read_q(st + RA);
         mfma_slot(st + 1);
       }
-      const int g0 = wg0 + st * GS;
-      while (g0 >= cend && c < c_last) {  // close finished (possibly empty) chunks
-        if (lane < 16) *reinterpret_cast<v4f*>(red_lane + (size_t)c * RS) = v4f{p[0][0], 0.f, 0.f, 0.f};
-        p[0][0] = 0.f;
-        ++c;
-        cend = chunk_begin_u(c + 1, G);
+      if constexpr (SC) {
+        if (st > 0 && (st * GS) % GPC == 0) {  // the chunk ending before this slot
+          if (lane < 16)
+            *reinterpret_cast<v4f*>(red_lane + (size_t)(c_first + st * GS / GPC - 1) * RS) = v4f{p[0][0], 0.f, 0.f, 0.f};
+          p[0][0] = 0.f;
+        }
+      } else {
+        const int g0 = wg0 + st * GS;
+        while (g0 >= cend && c < c_last) {  // close finished (possibly empty) chunks
+          if (lane < 16) *reinterpret_cast<v4f*>(red_lane + (size_t)c * RS) = v4f{p[0][0], 0.f, 0.f, 0.f};
+          p[0][0] = 0.f;
+          ++c;
+          cend = chunk_begin_u(c + 1, G);
+        }
       }
       if constexpr (GS == 1) {  // see the general loop
         __builtin_amdgcn_sched_barrier(0);
@@ -464,11 +479,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
       }
       // Chunk boundaries are multiples of 4 groups and a slot's GS groups
       // start at a multiple of GS, so chunks close only at slot starts.
-      const int g0 = wg0 + st * GS;
-      while (g0 >= cend && c < c_last) {  // close finished (possibly empty) chunks
-        write_partials(c);
-        ++c;
-        cend = chunk_begin(c + 1, G);
+      if constexpr (SC) {
+        if (st > 0 && (st * GS) % GPC == 0) write_partials(c_first + st * GS / GPC - 1);
+      } else {
+        const int g0 = wg0 + st * GS;
+        while (g0 >= cend && c < c_last) {  // close finished (possibly empty) chunks
+          write_partials(c);
+          ++c;
+          cend = chunk_begin(c + 1, G);
+        }
       }
 #pragma unroll
       for (int jj = 0; jj < GS; ++jj) {
@@ -482,7 +501,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
       }
     }
   }
-  for (; c < c_first + CPW; ++c) write_partials(c);
+  if constexpr (SC) write_partials(c_first + CPW - 1);  // the wave's last chunk
+  else for (; c < c_first + CPW; ++c) write_partials(c);
   __syncthreads();
 
   // ---------------------------------------------------------------- epilogue
