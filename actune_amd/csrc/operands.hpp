@@ -181,7 +181,20 @@ __device__ __forceinline__ float group_code_bits(const float v[8], uint32_t cb[8
 #pragma unroll
   for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
   amax = fmaxf(seg8_max(amax), 1e-8f);
-  const float s = amax / (float)P;
+  float s;
+  if constexpr (DT == kF32 || P == 1) {
+    s = amax / (float)P;
+  } else {
+    // amax is a 16-bit float value or f32(1e-8): with yp = fl(1/P), the
+    // product q0 = fl(amax * yp) and one FMA correction with the exact
+    // residual give fl(amax / P) for every such amax and P in {7, 127}
+    // (checked for all of them by tests/exhaustive_division.c), without the
+    // IEEE division sequence on the quantizer's serial path
+    constexpr float yp = 1.0f / (float)P;
+    const float q0 = amax * yp;
+    const float r = __builtin_fmaf(-q0, (float)P, amax);
+    s = __builtin_fmaf(r, yp, q0);
+  }
   const float y = 1.0f / s;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {

@@ -8,7 +8,10 @@
  *   q0 = fl(x * y)
  *   r  = fma(-q0, s, x)       (exact residual)
  *   q1 = fma(r, y, q0)        (Markstein's correction)
- * This program checks rint(q1) == rint(x / s) after clamping for every
+ * For p > 1 the kernels form s itself without a division, as
+ *   s = fma(fma(-q, p, amax), yp, q),  q = fl(amax * yp),  yp = fl(1 / p),
+ * and this program checks that it equals fl(amax / p) bit for bit.
+ * It checks rint(q1) == rint(x / s) after clamping for every
  * p in {1, 7, 127}, every positive finite amax of the format (plus the f32
  * 1e-8 floor), s = fl(max(amax, 1e-8) / p), and every x of the format with
  * 0 <= x <= amax (negative x is symmetric under round-to-nearest-even).
@@ -45,14 +48,21 @@ int main(int argc, char** argv) {
   uint32_t top = f16 ? 0x7C00u : 0x7F80u;  /* first non-finite pattern */
   float (*conv)(uint32_t) = f16 ? from_f16 : from_bf16;
   const int ps[3] = {1, 7, 127};
-  long bad = 0, checked = 0;
+  long bad = 0, checked = 0, bad_scale = 0;
   for (int pi = 0; pi < 3; ++pi) {
     const int p = ps[pi];
-#pragma omp parallel for schedule(dynamic, 64) reduction(+ : bad, checked)
+#pragma omp parallel for schedule(dynamic, 64) reduction(+ : bad, checked, bad_scale)
     for (long ab = 1; ab <= (long)top; ab += stride) {
       float amax = ab == (long)top ? 1e-8f : conv((uint32_t)ab);  /* top stands for the floor */
       if (amax < 1e-8f) amax = 1e-8f;
       const float s = amax / (float)p;
+      if (p > 1) {  /* the kernels' constant-divisor form of s for 16-bit inputs */
+        const float yp = 1.0f / (float)p;
+        const float sq0 = amax * yp;
+        const float sr = fmaf(-sq0, (float)p, amax);
+        const float sf = fmaf(sr, yp, sq0);
+        if (memcmp(&sf, &s, 4) != 0) ++bad_scale;
+      }
       const float y = 1.0f / s;
       for (uint32_t xb = 0; xb < top; ++xb) {
         const float x = conv(xb);
@@ -65,6 +75,7 @@ int main(int argc, char** argv) {
       }
     }
   }
-  printf("%s: checked %ld (x, s) pairs, mismatches %ld\n", f16 ? "f16" : "bf16", checked, bad);
-  return bad != 0;
+  printf("%s: checked %ld (x, s) pairs, mismatches %ld, scale mismatches %ld\n", f16 ? "f16" : "bf16", checked, bad,
+         bad_scale);
+  return bad != 0 || bad_scale != 0;
 }
