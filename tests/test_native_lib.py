@@ -62,12 +62,15 @@ def test_config_table():
     # very wide N: in-launch quantization too heavy even shared by four tiles,
     # so 8 waves take the codes
     assert _native.default_config(8, 22016, 4096, 4, 8) == 15
-    # M = 2..4, wide N: 16 waves and four row tiles per workgroup below 1024
-    # row tiles, 8 waves and two tiles from there on
+    # M = 3..4, wide N: 16 waves and four row tiles per workgroup below 1024
+    # row tiles, 8 waves and two tiles from there on (M = 2: 4 waves, one
+    # tile per workgroup, below 1024 row tiles)
     assert _native.default_config(3, 11008, 4096, 4, 8) == 16
     assert _native.default_config(4, 12288, 4096, 4, 8) == 16
     assert _native.default_config(4, 22016, 4096, 4, 8) == 15
     assert _native.default_config(2, 4096, 4096, 4, 8) == 14  # narrow N: as for M = 1
+    assert _native.default_config(2, 11008, 4096, 4, 8) == 14  # two tokens: one tile per workgroup
+    assert _native.default_config(2, 22016, 4096, 4, 8) == 15
     # M = 9..16: the quantizer's codes (16-token tile); 16 waves and shared
     # row tiles below 1024 row tiles, 8 waves from there on and for narrow N;
     # K = 11008 fits no wave count at 16 tokens: the streaming kernel
