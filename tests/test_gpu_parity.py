@@ -89,7 +89,10 @@ def _run_linear(x, w, b, W, A, config, out_dtype=None):
 
 
 @pytest.mark.parametrize("W,A", PAIRS)
-@pytest.mark.parametrize("shape", [(1, 64, 32), (17, 128, 96), (8, 4096, 64), (50, 1024, 48)])
+@pytest.mark.parametrize("shape", [(1, 64, 32), (17, 128, 96), (8, 4096, 64), (50, 1024, 48),
+                                   # G = 21: a ragged last quad, and canonical chunks of 0 or 1 quads
+                                   # (the prefill kernel's one-chunk-per-stage form)
+                                   (12, 1344, 40), (70, 1344, 40)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_output_bit_exact_in_canonical_order(W, A, shape, with_bias):
     m, k, n = shape
