@@ -76,6 +76,58 @@ def _dtype_code(t: torch.Tensor) -> int:
     return DTYPE_CODES[t.dtype]
 
 
+def _bias_code(bias) -> int:
+    """dtype code of a bias (2 when there is none); the reference op accepts
+    floating biases only (grouped_native.cu:97)."""
+    if bias is None:
+        return 2
+    if bias.dtype not in DTYPE_CODES:
+        raise RuntimeError("float scales/bias required")
+    return DTYPE_CODES[bias.dtype]
+
+
+def _check_buffer(t, name, shape, dtype, device):
+    """A caller-supplied buffer must be a contiguous tensor of exactly this
+    shape and dtype on the operation's device: the C ABI takes raw pointers
+    and cannot check sizes itself."""
+    if t.device != device:
+        raise RuntimeError(f"{name} must be on {device}")
+    if t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {dtype}, got {t.dtype}")
+    if tuple(t.shape) != tuple(shape) or not t.is_contiguous():
+        raise RuntimeError(f"{name} must be a contiguous {list(shape)} tensor, got {list(t.shape)}")
+
+
+def _check_weights(w, ws, bias, k, W):
+    """Packed weights u8 [N, K*W/8], float32 scale [N], optional bias [N]."""
+    if w.dtype != torch.uint8:
+        raise RuntimeError("packed uint8 required")
+    if ws.dtype != torch.float32:
+        raise RuntimeError("float scales/bias required")
+    if w.dim() != 2 or w.size(1) != k * W // 8:
+        raise RuntimeError("packed shape mismatch")
+    if not (w.is_contiguous() and ws.is_contiguous() and (bias is None or bias.is_contiguous())):
+        raise RuntimeError("contiguous operands required")
+    n = w.size(0)
+    if ws.numel() != n:
+        raise RuntimeError("scale shape mismatch")
+    if bias is not None and bias.numel() != n:
+        raise RuntimeError("bias shape mismatch")
+    _bias_code(bias)
+    return n
+
+
+def _check_widths(W, A):
+    if W not in (2, 4, 8) or A not in (2, 4, 8):
+        raise ValueError("Unsupported integer width")
+
+
+def _check_flat(flat):
+    if flat.dim() != 2 or not flat.is_contiguous():
+        raise RuntimeError("contiguous [M, K] input required")
+    _dtype_code(flat)
+
+
 def version() -> str:
     return lib().actune_version().decode()
 
@@ -100,20 +152,33 @@ def _require_cuda(*tensors):
         raise RuntimeError("device mismatch")
 
 
+def _check_input_scale(input_scale, x):
+    if input_scale is not None and (input_scale.dtype != x.dtype or input_scale.numel() != x.shape[-1]
+                                    or not input_scale.is_contiguous()):
+        raise RuntimeError("input_scale must be a contiguous [K] tensor of the input dtype")
+
+
+def _act_buffers(packed, scales, m, k, a, device):
+    """Packed activations u8 [M, K*A/8] and scales f32 [M, K/64]: allocated
+    here, or checked when the caller passes them."""
+    if packed is None:
+        packed = torch.empty((m, k * a // 8), device=device, dtype=torch.uint8)
+    if scales is None:
+        scales = torch.empty((m, k // 64), device=device, dtype=torch.float32)
+    _check_buffer(packed, "packed", (m, k * a // 8), torch.uint8, device)
+    _check_buffer(scales, "scales", (m, k // 64), torch.float32, device)
+    return packed, scales
+
+
 def quantize_groups(x: torch.Tensor, a: int, input_scale: torch.Tensor | None = None,
                     packed: torch.Tensor | None = None, scales: torch.Tensor | None = None):
     """Group-64 quantize a contiguous [M, K] tensor; returns (packed, scales)."""
-    _require_cuda(x, input_scale)
-    if x.dim() != 2 or not x.is_contiguous():
-        raise RuntimeError("contiguous [M, K] input required")
+    _require_cuda(x, input_scale, packed, scales)
+    _check_widths(8, a)
+    _check_flat(x)
     m, k = x.shape
-    if input_scale is not None and (input_scale.dtype != x.dtype or input_scale.numel() != k
-                                    or not input_scale.is_contiguous()):
-        raise RuntimeError("input_scale must be a contiguous [K] tensor of the input dtype")
-    if packed is None:
-        packed = torch.empty((m, k * a // 8), device=x.device, dtype=torch.uint8)
-    if scales is None:
-        scales = torch.empty((m, k // 64), device=x.device, dtype=torch.float32)
+    _check_input_scale(input_scale, x)
+    packed, scales = _act_buffers(packed, scales, m, k, a, x.device)
     _check(lib().actune_quantize_groups(_ptr(x), _dtype_code(x), _ptr(input_scale), m, k, a,
                                         _ptr(packed), _ptr(scales), _stream(x.device)))
     return packed, scales
@@ -158,10 +223,12 @@ def grouped_linear(a, as_, w, ws, bias, source_or_shape, W, A, config=CONFIG_AUT
     _check_linear_operands(a, as_, w, ws, bias, m, k, n, W, A)
     if bias is not None and bias.numel() == 0:
         bias = None
+    bias_dt = _bias_code(bias)
     if out is None:
         out = torch.empty((m, n), device=a.device, dtype=dtype)
+    _check_buffer(out, "out", (m, n), dtype, a.device)
     _check(lib().actune_grouped_linear(
-        _ptr(a), _ptr(as_), _ptr(w), _ptr(ws), _ptr(bias), DTYPE_CODES.get(bias.dtype, 2) if bias is not None else 2,
+        _ptr(a), _ptr(as_), _ptr(w), _ptr(ws), _ptr(bias), bias_dt,
         _ptr(out), _dtype_code(out), m, n, k, W, A, config, _stream(a.device)))
     return out
 
@@ -171,18 +238,17 @@ def grouped_forward(flat, w, ws, bias, W, A, input_scale=None, config=CONFIG_AUT
     """Quantize + GEMM for a contiguous [M, K] input (GroupedLinear.forward's
     device work, grouped.py:127-143); returns [M, N] in flat.dtype.
     packed [M, K*A/8] / scales [M, K/64] / out may be preallocated."""
-    _require_cuda(flat, w, ws, bias, input_scale)
+    _require_cuda(flat, w, ws, bias, input_scale, out, packed, scales)
+    _check_widths(W, A)
+    _check_flat(flat)
     m, k = flat.shape
-    n = w.size(0)
-    if w.size(1) != k * W // 8:
-        raise RuntimeError("packed shape mismatch")
-    if packed is None:
-        packed = torch.empty((m, k * A // 8), device=flat.device, dtype=torch.uint8)
-    if scales is None:
-        scales = torch.empty((m, k // 64), device=flat.device, dtype=torch.float32)
+    n = _check_weights(w, ws, bias, k, W)
+    _check_input_scale(input_scale, flat)
+    packed, scales = _act_buffers(packed, scales, m, k, A, flat.device)
     if out is None:
         out = torch.empty((m, n), device=flat.device, dtype=flat.dtype)
-    bias_dt = 2 if bias is None else _dtype_code(bias)
+    _check_buffer(out, "out", (m, n), flat.dtype, flat.device)
+    bias_dt = _bias_code(bias)
     _check(lib().actune_grouped_forward(
         _ptr(flat), _dtype_code(flat), _ptr(input_scale), _ptr(packed), _ptr(scales), _ptr(w), _ptr(ws),
         _ptr(bias), bias_dt, _ptr(out), m, n, k, W, A, config, _stream(flat.device)))
@@ -196,26 +262,25 @@ def grouped_forward_multi(flat, targets, W, A, input_scale=None, config=CONFIG_A
     to allocate). Returns the list of outputs."""
     if not 1 <= len(targets) <= MAX_TARGETS:
         raise ValueError("between 1 and 4 targets required")
+    _require_cuda(flat, input_scale, packed, scales, *[t for tgt in targets for t in tgt])
+    _check_widths(W, A)
+    _check_flat(flat)
     m, k = flat.shape
-    _require_cuda(flat, input_scale, *[t for tgt in targets for t in tgt[:3]])
+    _check_input_scale(input_scale, flat)
     biases = [t[2] for t in targets]
-    if any(b is not None for b in biases) and len({(b.dtype if b is not None else None) for b in biases}) != 1:
+    if len({(b.dtype if b is not None else None) for b in biases}) != 1:
         raise ValueError("all targets must share one bias dtype (or none)")
-    bias_dt = 2 if biases[0] is None else _dtype_code(biases[0])
+    bias_dt = _bias_code(biases[0])
     arr = (_Target * len(targets))()
     outs = []
     for j, (w, ws, bias, out) in enumerate(targets):
-        if w.size(1) != k * W // 8:
-            raise RuntimeError("packed shape mismatch")
+        n = _check_weights(w, ws, bias, k, W)
         if out is None:
-            out = torch.empty((m, w.size(0)), device=flat.device, dtype=flat.dtype)
+            out = torch.empty((m, n), device=flat.device, dtype=flat.dtype)
+        _check_buffer(out, f"out[{j}]", (m, n), flat.dtype, flat.device)
         outs.append(out)
-        arr[j] = _Target(w.data_ptr(), ws.data_ptr(), None if bias is None else bias.data_ptr(), out.data_ptr(),
-                         w.size(0))
-    if packed is None:
-        packed = torch.empty((m, k * A // 8), device=flat.device, dtype=torch.uint8)
-    if scales is None:
-        scales = torch.empty((m, k // 64), device=flat.device, dtype=torch.float32)
+        arr[j] = _Target(w.data_ptr(), ws.data_ptr(), None if bias is None else bias.data_ptr(), out.data_ptr(), n)
+    packed, scales = _act_buffers(packed, scales, m, k, A, flat.device)
     _check(lib().actune_grouped_forward_multi(_ptr(flat), _dtype_code(flat), _ptr(input_scale), _ptr(packed),
                                               _ptr(scales), arr, len(targets), bias_dt, m, k, W, A, config,
                                               _stream(flat.device)))

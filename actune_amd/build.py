@@ -1,6 +1,7 @@
 """Builds libactune_hip.so in-tree with hipcc for gfx950.
 
-Usage: ``python -m actune_amd.build`` (or ``__graft_entry__.build()``).
+Usage: ``python -m actune_amd.build [--incremental]`` (or
+``__graft_entry__.build()``, which always compiles everything).
 Objects go to ``actune_amd/_build/``, the library to ``actune_amd/lib/``.
 """
 from __future__ import annotations
@@ -42,8 +43,18 @@ def flags() -> list[str]:
     ]
 
 
-def _compile(src: str) -> Path:
+def _stale(src: str, out: Path) -> bool:
+    """True when `out` is missing or older than the source or any header."""
+    if not out.exists():
+        return True
+    deps = [CSRC / src, *CSRC.glob("*.hpp"), PKG.parent / "include" / "actune_hip.h", Path(__file__)]
+    return any(d.exists() and d.stat().st_mtime > out.stat().st_mtime for d in deps)
+
+
+def _compile(src: str, incremental: bool = False) -> Path:
     out = OBJ / (Path(src).stem + ".o")
+    if incremental and not _stale(src, out):
+        return out
     cmd = [hipcc(), *flags(), "-c", str(CSRC / src), "-o", str(out)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode:
@@ -51,11 +62,13 @@ def _compile(src: str) -> Path:
     return out
 
 
-def build(verbose: bool = False) -> Path:
+def build(verbose: bool = False, incremental: bool = False) -> Path:
+    """Compile every source (or, incremental, only the out-of-date ones) and
+    link the library."""
     OBJ.mkdir(exist_ok=True)
     LIB_DIR.mkdir(exist_ok=True)
     with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
-        objs = list(pool.map(_compile, SOURCES))
+        objs = list(pool.map(lambda src: _compile(src, incremental), SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -68,4 +81,4 @@ def build(verbose: bool = False) -> Path:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv)

@@ -69,7 +69,7 @@ int check_shape(int64_t M, int64_t K, int W, int A, int out_dt, int bias_dt, int
   if (config < 0 || config >= kNumConfigs) return fail(ACTUNE_ERR_INVALID, "invalid configuration");
   if (config < kSmallMConfigs && M > kSmallMMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
   if (config >= kStreamFirst && config < kPrefillFirst && M > kStreamMax)
-    return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
+    return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 16");
   if (config >= kDecodeFirst && M > kDecodeMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
   return ACTUNE_OK;
 }
@@ -181,6 +181,8 @@ LinearArgs base_args(int64_t M, int64_t K, int bias_dt, int out_dt) {
 }
 
 }  // namespace
+
+void actune::set_last_error(const char* msg) { snprintf(g_err, sizeof g_err, "%s", msg); }
 
 extern "C" {
 

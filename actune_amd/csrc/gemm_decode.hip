@@ -107,6 +107,9 @@ bool decode_fits(int K, int M, int W, int nw, bool packed, int x_dt) {
   const int gw = decode_groups_per_wave(K, nw), gps = 8 / W;
   if ((gw + gps - 1) / gps > decode_ring(W)) return false;
   const int per = packed ? 16 : 8, mb = M > 16 ? 16 : M;  // tokens of one 16-token block
+  // group-row indices gl * M + m are divided by M through LinearArgs::m_div,
+  // which is exact below kDecodeMaxGroupRows
+  if (gw * mb > kDecodeMaxGroupRows) return false;
   if ((gw * mb + per - 1) / per > decode_passes(decode_token_tile(M), packed)) return false;
   return decode_lds_bytes(K, M, nw, 1) <= kStreamLdsMax;
 }

@@ -9,6 +9,9 @@
 namespace actune {
 
 constexpr int kMaxProblems = 4;
+// Group-row indices (group of a wave's K-range x token of a 16-token block)
+// of the decode kernel stay below this; LinearArgs::m_div is exact there.
+constexpr int kDecodeMaxGroupRows = 256;
 // LDS budget of the streaming kernel (gfx950 has 160 KiB per CU)
 constexpr size_t kStreamLdsMax = 144 * 1024;
 
@@ -36,7 +39,12 @@ struct LinearArgs {
   int x_dt;
   int32_t* dots;        // [M, N, K/64] (dots mode, single problem)
   int M, K, bias_dt, out_dt;
-  uint32_t m_div;       // ceil(2^16 / M): idx / M == (idx * m_div) >> 16 for idx < 2^14, M <= 16
+  // ceil(2^16 / M). With e = m_div * M - 2^16 (0 <= e < M), idx / M ==
+  // (idx * m_div) >> 16 whenever idx * e < 2^16, so for every idx < 2^16 / 16
+  // = 4096 when M <= 16 (it fails first at idx 4694 for M = 15). The decode
+  // kernel, its only user, divides group-row indices below
+  // kDecodeMaxGroupRows = 16 groups x 16 tokens (decode_fits enforces it).
+  uint32_t m_div;
   uint32_t m_div_tail;  // the same for the last 16-token block, M - 16 * ((M - 1) / 16) tokens
 };
 
@@ -79,6 +87,9 @@ inline void allow_dynamic_lds() {
                             (int)kStreamLdsMax);
   done.fetch_or(bit, std::memory_order_release);
 }
+
+// Sets the calling thread's actune_last_error() message.
+void set_last_error(const char* msg);
 
 void launch_quantize(const void* x, int dt, const void* sc, long M, long K, int A, uint8_t* packed,
                      float* scales, hipStream_t stream);

@@ -12,6 +12,7 @@ from contextlib import contextmanager
 from contextvars import ContextVar
 from dataclasses import dataclass
 import math
+import sys
 
 CONFIGURATIONS = ("q00", "q01", "q11", "q10")
 _WIDTHS = (2, 4, 8)
@@ -31,8 +32,22 @@ def pair(mode):
 
 
 def active_precision_profile():
-    """The configuration of the request being served, or None."""
-    return _active.get()
+    """The configuration of the request being served, or None.
+
+    When the reference's own ``actune.precision`` is loaded as a separate
+    module (a deployment that changed its imports to this package but kept
+    the reference Controller, whose runtime.py:9 binds the reference's
+    ``precision_profile``), a configuration set there is honoured too, so
+    dispatch never silently falls back to the default profile.
+    """
+    current = _active.get()
+    if current is None:
+        other = sys.modules.get("actune.precision")
+        if other is not None and other is not sys.modules.get(__name__):
+            getter = getattr(other, "active_precision_profile", None)
+            if callable(getter):
+                current = getter()
+    return current
 
 
 @contextmanager

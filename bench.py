@@ -41,7 +41,7 @@ import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0
-INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
+INT8_PEAK_TOPS = 5033.0  # dense int8 MFMA, MI355X: 256 CU x 2.4 GHz x 8192 ops/clk
 PAIRS = [(w, a) for w in (8, 4, 2) for a in (8, 4, 2)]
 GEMMA_SHAPES = [("q", 2048, 2048), ("kv", 256, 2048), ("gate_up", 16384, 2048), ("down", 2048, 16384)]
 SHAPES = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
@@ -153,36 +153,87 @@ def gemm_bytes(n, k, m, W, A):
     return n * k * W // 8 + 4 * n + m * k * A // 8 + 4 * m * (k // 64) + 2 * m * n
 
 
+def host_cpu():
+    """CPU model and core counts of this host: lscpu's model name and
+    physical cores, the logical CPUs this process may run on, and the thread
+    share the box grants one GPU job (OMP_NUM_THREADS when set)."""
+    import subprocess
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            info[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        physical = int(info["Socket(s)"]) * int(info["Core(s) per socket"])
+    except (KeyError, ValueError):
+        physical = os.cpu_count() or 1
+    affinity = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS") or affinity)
+    return dict(model=info.get("Model name", "unknown"), physical_cores=physical, logical_cpus_available=affinity,
+                thread_share=share)
+
+
 def cpu_baseline(seconds, W, A):
-    """Reference dequant-then-matmul (hoisted weight dequant) on one decoder
-    layer's 7 linears at M=1, repeated for about `seconds`."""
+    """The reference's dequantize-then-matmul path (oracle/cpu_path.py, a
+    torch-CPU restatement of tests/test_kernels.py:42-44) on this host:
+    config C1 (M=16, 4096x4096) and one Llama-2-7B layer's 7 linears at M=1,
+    each in variant (i) weight dequant per call and (ii) weight dequant
+    hoisted, at the host's usable cores and at 1 thread. Warm-up 3, then the
+    median of at least 15 timed calls (one call = one linear for C1, one
+    pass over the layer for the layer), each case capped near `seconds` / 8.
+    `value` is variant (ii) of the layer on all usable cores."""
+    import statistics
+
     import torch
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import cpu_path
-    cores = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(cores)
+    host = host_cpu()
+    cores = max(1, min(host["physical_cores"], host["logical_cpus_available"], host["thread_share"]))
     g = torch.Generator().manual_seed(0)
     lo = -(1 << (W - 1))
-    layer = []
-    for _, n, k in SHAPES:
+
+    def linear_case(m, n, k, outliers):
         codes = torch.randint(lo, -lo, (n, k), generator=g, dtype=torch.int8)
         scale = torch.rand(n, generator=g) * 0.01 + 0.005
-        x = torch.randn(1, k, generator=g).to(torch.bfloat16)
-        layer.append((x, cpu_path.dequantize_weight(codes, scale), n * k * W // 8))
-    for x, wd, _ in layer:  # warm-up
-        cpu_path.linear(x, A, wd)
-    passes, nbytes, t0 = 0, 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        for x, wd, b in layer:
-            cpu_path.linear(x, A, wd)
-            nbytes += b
-        passes += 1
-    dt = time.perf_counter() - t0
-    return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s (packed weight bytes)", cores=cores,
-                kind="port",
-                sample=f"{passes} passes over one Llama-2-7B layer's 7 linears at M=1, W{W}A{A}, "
-                       f"torch-CPU fp32 dequant-then-matmul with hoisted weight dequant, "
-                       f"{dt:.1f} s, {dt / passes / 7 * 1e6:.0f} us/linear")
+        x = torch.randn(m, k, generator=g)
+        if outliers:
+            x[:, torch.randperm(k, generator=g)[: k // 100]] *= 10
+        return x.to(torch.bfloat16), codes, scale, cpu_path.dequantize_weight(codes, scale)
+
+    cases = {"C1_M16_4096x4096": [linear_case(16, 4096, 4096, True)],
+             "layer_M1_7_linears": [linear_case(1, n, k, True) for _, n, k in SHAPES]}
+    wbytes = {name: sum(c[1].numel() * W // 8 for c in lins) for name, lins in cases.items()}
+
+    def run(lins, hoisted):
+        for x, codes, scale, wd in lins:
+            cpu_path.linear(x, A, wd if hoisted else cpu_path.dequantize_weight(codes, scale))
+
+    budget = seconds / 8
+    results = {}
+    for threads in (cores, 1):
+        torch.set_num_threads(threads)
+        for name, lins in cases.items():
+            for variant, hoisted in (("i_dequant_per_call", False), ("ii_dequant_hoisted", True)):
+                for _ in range(3):
+                    run(lins, hoisted)
+                times, t_end = [], time.perf_counter() + budget
+                while len(times) < 15 or time.perf_counter() < t_end and len(times) < 200:
+                    t0 = time.perf_counter()
+                    run(lins, hoisted)
+                    times.append(time.perf_counter() - t0)
+                med = statistics.median(times)
+                results[f"{name}/{variant}/{threads}t"] = dict(
+                    ms_per_call=round(med * 1e3, 3), weight_GBps=round(wbytes[name] / med / 1e9, 3),
+                    calls=len(times))
+    head = results[f"layer_M1_7_linears/ii_dequant_hoisted/{cores}t"]
+    return dict(value=head["weight_GBps"], unit="GB/s (packed weight bytes)", cores=cores, kind="port",
+                sample=f"one Llama-2-7B layer's 7 linears at M=1, W{W}A{A}, torch-CPU fp32 dequant-then-matmul "
+                       f"with hoisted weight dequant, median of {head['calls']} passes, "
+                       f"{head['ms_per_call'] / 7 * 1e3:.0f} us/linear",
+                host=host, torch_version=torch.__version__, variants=results)
 
 
 def run_schedule(torch, _native, stack, W, A, siblings, steps, warmup):
@@ -240,7 +291,9 @@ def packed_set(torch, n, k, W, copies, g):
 
 def bench_prefill(torch, _native, steps, warmup):
     """C3: the stack's three distinct shapes at M=512, all nine W/A pairs;
-    default kernel config (the prefill kernel), packed activations given."""
+    default kernel config (the prefill kernel). `us` times the GEMM on
+    packed activations (the roofline figure), `us_with_quantizer` the whole
+    forward on bf16 x (quantizer launch + GEMM)."""
     g = torch.Generator(device="cuda").manual_seed(3)
     m, out = 512, {}
     for W, A in PAIRS:
@@ -256,8 +309,15 @@ def bench_prefill(torch, _native, steps, warmup):
                     _native.grouped_linear(a, s, w, sc, None, x, W, A, out=y)
 
             us = time_launches(torch, fn, steps, warmup) / len(ws)
+
+            def fwd(ws=ws, a=a, s=s, x=x, y=y):
+                for w, sc in ws:
+                    _native.grouped_forward(x, w, sc, None, W, A, out=y, packed=a, scales=s)
+
+            us_q = time_launches(torch, fwd, steps, warmup) / len(ws)
             tops = 2 * m * n * k / us / 1e6
             row[f"{n}x{k}"] = dict(us=round(us, 2), TOPS=round(tops, 1), frac=round(tops / INT8_PEAK_TOPS, 4),
+                                   us_with_quantizer=round(us_q, 2),
                                    config=_native.default_config(m, n, k, W, A))
             del ws
         out[f"W{W}A{A}"] = row

@@ -125,8 +125,19 @@ int oracle_quantize_groups(const void* x, int dtype, const void* input_scale, in
  * amax = max|v| clamped to >= f32(1e-8). ratios (nullable) is per row, already
  * validated to lie in (0,1]. w is the fp32 image of the weight, [N,K].
  */
-int oracle_weight_codes(const float* w, int64_t N, int64_t K, int W, int A, const float* ratios,
-                        int8_t* codes, float* scale) {
+/* amax / p: the IEEE quotient (recip == 0: torch-CPU, and torch-GPU
+ * tensor/tensor division), or amax times the fp32 reciprocal of p (recip ==
+ * 1: torch-GPU division of a tensor by a Python scalar, which multiplies by
+ * 1.0f / p computed in fp32; the reference's note, w4a8_triton.py:33-36). */
+static float div_const(float amax, float p, int recip) {
+  if (!recip) return amax / p;
+  volatile float one = 1.0f;
+  const float r = one / p;
+  return amax * r;
+}
+
+static int weight_codes_impl(const float* w, int64_t N, int64_t K, int W, int A, const float* ratios,
+                             int recip, int8_t* codes, float* scale) {
   if ((W != 2 && W != 4 && W != 8) || (A != 2 && A != 4 && A != 8)) return -1;
   for (int64_t n = 0; n < N; ++n) {
     const float* v = w + n * K;
@@ -135,7 +146,7 @@ int oracle_weight_codes(const float* w, int64_t N, int64_t K, int W, int A, cons
     for (int64_t k = 0; k < K; ++k) { float a = fabsf(v[k]); if (a > amax) amax = a; }
     if (amax < 1e-8f) amax = 1e-8f;
     if (W == 8 && A != 4) {
-      const float s = amax / 127.0f;
+      const float s = div_const(amax, 127.0f, recip);
       scale[n] = s;
       for (int64_t k = 0; k < K; ++k) {
         float q = rintf(v[k] / s);
@@ -155,7 +166,7 @@ int oracle_weight_codes(const float* w, int64_t N, int64_t K, int W, int A, cons
       }
       continue;
     }
-    const float s4 = amax / 7.0f;
+    const float s4 = div_const(amax, 7.0f, recip);
     for (int64_t k = 0; k < K; ++k) {
       const float t = v[k] / s4;
       float q = rintf(t);
@@ -176,6 +187,19 @@ int oracle_weight_codes(const float* w, int64_t N, int64_t K, int W, int A, cons
     scale[n] = W == 4 ? s4 : s4 / 16.0f;
   }
   return 0;
+}
+
+int oracle_weight_codes(const float* w, int64_t N, int64_t K, int W, int A, const float* ratios,
+                        int8_t* codes, float* scale) {
+  return weight_codes_impl(w, N, K, W, A, ratios, 0, codes, scale);
+}
+
+/* The same codebooks as computed by torch on a GPU-resident weight: the two
+ * divisions by the constants 7 and 127 multiply by their fp32 reciprocals
+ * (every other division is tensor / tensor, IEEE on both devices). */
+int oracle_weight_codes_recip(const float* w, int64_t N, int64_t K, int W, int A, const float* ratios,
+                              int8_t* codes, float* scale) {
+  return weight_codes_impl(w, N, K, W, A, ratios, 1, codes, scale);
 }
 
 /* Row-major, K-contiguous little-endian packing (grouped.py:108-111). */

@@ -63,6 +63,13 @@ def lib():
         so.oracle_round_out.restype = None
         so.oracle_f32_to_bf16.argtypes = [ctypes.c_float]
         so.oracle_f32_to_bf16.restype = ctypes.c_uint16
+        so.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+        so.oracle_f16_to_f32.restype = ctypes.c_float
+        so.oracle_weight_codes_recip.argtypes = [_P, _I, _I, ctypes.c_int, ctypes.c_int, _P, _P, _P]
+        so.oracle_tw_recip.argtypes = [ctypes.c_int]
+        so.oracle_tw_recip.restype = ctypes.c_float
+        so.oracle_tw_quantize_rows.argtypes = [_P, ctypes.c_int, _I, _I, ctypes.c_int, _P, _P]
+        so.oracle_tw_epilogue.argtypes = [_P, _I, _I, _P, _P, _P, ctypes.c_int, _P]
         _LIB = so
     return _LIB
 
@@ -78,6 +85,14 @@ def _c(a, dtype):
 # ---------------------------------------------------------------- dtype bits
 def bf16_bits_to_f32(bits):
     return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f16_bits_to_f32(bits):
+    """The C oracle's f16 -> f32 widening (used for f16 activations and
+    channel scales), element by element."""
+    b = np.asarray(bits, dtype=np.uint16).reshape(-1)
+    f = lib().oracle_f16_to_f32
+    return np.array([f(int(v)) for v in b], dtype=np.float32).reshape(np.shape(bits))
 
 
 def f32_to_bf16_bits(x):
@@ -142,9 +157,11 @@ def validate_clip_ratios(clip_ratios, out_features):
     return np.ascontiguousarray(ratio)
 
 
-def weight_codes(w_f32, W, A, clip_ratios=None):
+def weight_codes(w_f32, W, A, clip_ratios=None, gpu_division=False):
     """Per-row weight codebook (quantizers.py:83-94) on the fp32 weight image.
-    Returns (codes int8 [N,K], scale f32 [N])."""
+    gpu_division: the divisions by the constants 7 and 127 as torch performs
+    them on a GPU-resident weight (multiply by the fp32 reciprocal) instead of
+    the IEEE quotient torch-CPU computes. Returns (codes int8 [N,K], scale f32 [N])."""
     w = _c(w_f32, np.float32)
     N, K = w.shape
     ratios = None
@@ -152,7 +169,8 @@ def weight_codes(w_f32, W, A, clip_ratios=None):
         ratios = validate_clip_ratios(clip_ratios, N)
     codes = np.empty((N, K), np.int8)
     scale = np.empty(N, np.float32)
-    if lib().oracle_weight_codes(_ptr(w), N, K, W, A, _ptr(ratios), _ptr(codes), _ptr(scale)):
+    fn = lib().oracle_weight_codes_recip if gpu_division else lib().oracle_weight_codes
+    if fn(_ptr(w), N, K, W, A, _ptr(ratios), _ptr(codes), _ptr(scale)):
         raise ValueError("Unsupported integer width")
     return codes, scale
 
@@ -237,3 +255,86 @@ def chunk_bounds(G, steps_groups, chunks):
     S = math.ceil(G / steps_groups)
     b = [min(G, (c * S // chunks) * steps_groups) for c in range(chunks)] + [G]
     return np.asarray(b, np.int64)
+
+
+# ---------------------------------------------------------------- tokenwise family
+# Per-row (tokenwise) quantization with full-K int32 accumulation:
+# actune/kernels/w4a8_triton.py, w8a8_triton.py, w2a8_triton.py,
+# decode_w4a8_triton.py and wxa4_native.py (arithmetic in tokenwise_oracle.c).
+
+def tw_recip(p):
+    """The fp32 reciprocal 1/p the reference's per-row quantizers multiply by."""
+    return np.float32(lib().oracle_tw_recip(int(p)))
+
+
+def tw_quantize_rows(x, bits, dtype="bf16"):
+    """Per-row dynamic A8 (bits 8) or A4 (bits 4) codes and scales
+    (w4a8_triton.py:161-201, wxa4_native.py:28-65). x: [M, K] bit patterns
+    (uint16) for bf16/f16, float32 for f32. Returns (codes int8 [M, K],
+    scales f32 [M])."""
+    store = np.float32 if dtype == "f32" else np.uint16
+    x = _c(x, store)
+    M, K = x.shape
+    codes = np.empty((M, K), np.int8)
+    scales = np.empty(M, np.float32)
+    if lib().oracle_tw_quantize_rows(_ptr(x), DTYPES[dtype], M, K, bits, _ptr(codes), _ptr(scales)):
+        raise ValueError("bad per-row quantizer arguments")
+    return codes, scales
+
+
+def tw_dots(a_codes, w_codes):
+    """Exact full-K int32 dots acc[m, n] = sum_k a[m, k] * w[n, k] (int64
+    brute force, checked to fit int32)."""
+    acc = a_codes.astype(np.int64) @ w_codes.astype(np.int64).T
+    if np.abs(acc).max(initial=0) >= 2**31:
+        raise OverflowError("accumulator exceeds int32")
+    return acc.astype(np.int32)
+
+
+def tw_epilogue(acc, a_scales, w_scale, bias=None, mode=0):
+    """fp32 output from int32 accumulators: mode 0 = the A8 family's
+    (acc * as) * ws (+ bias), mode 1 = the native A4 kernels' acc * (as * ws)
+    (+ bias); see tokenwise_oracle.c."""
+    acc = _c(acc, np.int32)
+    M, N = acc.shape
+    out = np.empty((M, N), np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    if lib().oracle_tw_epilogue(_ptr(acc), M, N, _ptr(_c(a_scales, np.float32)), _ptr(_c(w_scale, np.float32)),
+                                _ptr(b), mode, _ptr(out)):
+        raise ValueError("bad epilogue mode")
+    return out
+
+
+def pack_kmajor(codes, bits):
+    """The tokenwise family's K-major weight layouts (int8 codes [N, K]):
+    bits 8: int8 [K, N] (w8a8_triton.py:106, wxa4_native.py:334);
+    bits 4: u8 [K/2, N], byte j of column n = code j (low nibble) and code
+            j + K/2 (high nibble) (w4a8_triton.py:380-383);
+    bits 2: u8 [K/4, N], byte j = codes j, j + K/4, j + K/2, j + 3K/4 at bits
+            0, 2, 4, 6 (w2a8_triton.py:149-159)."""
+    c = _c(codes, np.int8)
+    N, K = c.shape
+    if bits == 8:
+        return np.ascontiguousarray(c.T)
+    per = 8 // bits
+    part = K // per
+    fields = [(c[:, i * part:(i + 1) * part].astype(np.int16) & ((1 << bits) - 1)) << (i * bits)
+              for i in range(per)]
+    packed = np.zeros((N, part), np.int16)
+    for f in fields:
+        packed |= f
+    return np.ascontiguousarray(packed.astype(np.uint8).T)
+
+
+def unpack_kmajor(packed, bits, K):
+    """Inverse of pack_kmajor: int8 codes [N, K]."""
+    p = _c(packed, np.uint8 if bits != 8 else np.int8)
+    if bits == 8:
+        return np.ascontiguousarray(p.T.astype(np.int8))
+    per = 8 // bits
+    half = 1 << (bits - 1)
+    cols = []
+    for i in range(per):
+        u = ((p.T.astype(np.int16) >> (i * bits)) & ((1 << bits) - 1))
+        cols.append(((u ^ half) - half).astype(np.int8))
+    return np.ascontiguousarray(np.concatenate(cols, axis=1))

@@ -130,3 +130,27 @@ def test_zero_rows_is_a_no_op_without_a_gpu():
     lib = _native.lib()
     assert lib.actune_grouped_linear(None, None, None, None, None, 2, None, 0, 0, 32, 128, 4, 8, -1, None) == 0
     assert lib.actune_quantize_groups(None, 0, None, 0, 128, 8, None, None, None) == 0
+
+
+def test_streaming_config_reports_its_own_limit():
+    rc = _native.lib().actune_grouped_linear(None, None, None, None, None, 2, None, 0, 17, 32, 128, 4, 8, 8, None)
+    assert rc == 1 and "M <= 16" in _err()
+
+
+@pytest.mark.parametrize("M", range(1, 17))
+def test_decode_row_division_is_exact_over_its_range(M):
+    """gemm_decode divides group-row indices r = group * M + token by M as
+    (r * ceil(2^16 / M)) >> 16 (launch.hpp, LinearArgs::m_div); decode_fits
+    keeps r below 16 groups x 16 tokens. Exact over that range for every M of
+    a 16-token block and for every ragged tail, and the stated first failure
+    (r = 4694 at M = 15) is where the identity r * e < 2^16 says."""
+    d = (65536 + M - 1) // M
+    assert all((r * d) >> 16 == r // M for r in range(256))
+    e = d * M - 65536
+    bad = [r for r in range(1 << 16) if (r * d) >> 16 != r // M]
+    if e == 0:
+        assert not bad
+    else:
+        assert bad and bad[0] >= 65536 // e
+    if M == 15:
+        assert bad[0] == 4694

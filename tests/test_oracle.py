@@ -311,3 +311,28 @@ def test_oracle_meets_reference_float_criterion(shape, W, A):
     out = O.bf16_bits_to_f32(O.round_out(y, "bf16"))
     exp = O.bf16_bits_to_f32(bf16(O.reference_float_linear(x, A, q, ws, bias)))
     np.testing.assert_allclose(out, exp, rtol=0.02, atol=0.02)
+
+
+def test_f16_widening_known_answers():
+    """oracle_f16_to_f32 (f16 x and channel scales): normals, subnormals,
+    signed zero, infinities and NaN, each against its value fixed by the
+    IEEE binary16 definition."""
+    cases = {0x3C00: 1.0, 0xC000: -2.0, 0x0001: 2.0**-24, 0x03FF: 1023 * 2.0**-24, 0x0400: 2.0**-14,
+             0x7BFF: 65504.0, 0x3555: (1 + 0x155 / 1024) * 2.0**-2,
+             0x7C00: float("inf"), 0xFC00: float("-inf"), 0x0000: 0.0}
+    got = O.f16_bits_to_f32(np.array(list(cases), np.uint16))
+    for (b, want), g in zip(cases.items(), got):
+        assert g == np.float32(want), hex(b)
+    neg_zero = O.f16_bits_to_f32(np.array([0x8000], np.uint16))[0]
+    assert neg_zero == 0.0 and np.signbit(neg_zero)
+    assert np.isnan(O.f16_bits_to_f32(np.array([0x7E00, 0xFE01], np.uint16))).all()
+
+
+def test_f16_widening_all_patterns_match_ieee_conversion():
+    """Every finite f16 bit pattern widens to the value numpy's binary16
+    conversion gives (an exact conversion: every f16 is an f32)."""
+    b = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    finite = (b & 0x7C00) != 0x7C00
+    want = b[finite].view(np.float16).astype(np.float32)
+    got = O.f16_bits_to_f32(b[finite])
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
