@@ -18,7 +18,8 @@ CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libactune_hip.so"
-SOURCES = ["api.hip", "quantize.hip", "gemm_smallm.hip", "gemm_tiled.hip", "gemm_stream.hip", "gemm_prefill.hip", "gemm_decode.hip"]
+SOURCES = ["api.hip", "quantize.hip", "gemm_smallm.hip", "gemm_tiled.hip", "gemm_stream.hip", "gemm_prefill.hip", "gemm_decode.hip",
+           "noalloc.hip"]
 ARCH = "gfx950"
 
 

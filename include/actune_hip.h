@@ -101,6 +101,21 @@ int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_s
                                  void* stream);
 
 /*
+ * actune_grouped_forward without caller-owned scratch: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under
+ * stream capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The packed activation codes and group scales live in a static device array
+ * of 8 MiB per GPU that the library holds until the process ends; calls with
+ * M*K*A/8 (rounded up to 256) + M*K/16 bytes above 8388608 are rejected
+ * (ACTUNE_ERR_INVALID). All calls on one GPU share that array: calls that
+ * overlap on one GPU (two streams or two threads) race. Results equal
+ * actune_grouped_forward's bit for bit; nothing is allocated.
+ */
+int actune_grouped_forward_noalloc(const void* x, int x_dtype, const void* input_scale, const uint8_t* w,
+                                   const float* w_scale, const void* bias, int bias_dtype, void* out,
+                                   int64_t M, int64_t N, int64_t K, int W, int A, int config, void* stream);
+
+/*
  * Exact per-group int32 dots dots[m][n][g] = sum_{k in g} a[m,k] * w[n,k]
  * computed by the integer path of kernel config `config` (test/debug; the
  * reference has no counterpart, it checks dots only through its float
