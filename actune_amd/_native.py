@@ -50,6 +50,11 @@ def lib():
         so.actune_grouped_forward_multi.argtypes = [_P, _I, _P, _P, _P, ctypes.POINTER(_Target), _I, _I,
                                                     _I64, _I64, _I, _I, _I, _P]
         so.actune_grouped_dots_i32.argtypes = [_P, _P, _I64, _I64, _I64, _I, _I, _I, _P, _P]
+        so.actune_tokenwise_quantize.argtypes = [_P, _I, _I64, _I64, _I, _P, _P, _P]
+        so.actune_tokenwise_workspace_bytes.argtypes = [_I64, _I64, _I64, _I, _I]
+        so.actune_tokenwise_workspace_bytes.restype = _I64
+        so.actune_tokenwise_linear.argtypes = [_P, _I, _P, _P, _I, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I, _P,
+                                               _I64, _P]
         so.actune_config_valid.argtypes = [_I, _I64]
         so.actune_default_config.argtypes = [_I64, _I64, _I64, _I, _I]
         _LIB = so
@@ -309,3 +314,68 @@ class Extension:
 def extension() -> Extension:
     lib()
     return Extension()
+
+
+# ---------------------------------------------------------------- tokenwise family
+TW_KMAJOR_W8, TW_KMAJOR_W4, TW_KMAJOR_W2, TW_ROWS_S4, TW_ROWS_S2 = 0, 1, 2, 3, 4
+TW_ACT_A8, TW_ACT_A4 = 0, 1
+TW_EPI_A8, TW_EPI_A4 = 0, 1
+
+
+def tokenwise_quantize(x, bits, codes=None, scales=None):
+    """Per-row dynamic A8 (int8 [M, K]) or A4 (packed u8 [M, K/2]) codes and
+    f32 [M] scales of a contiguous [M, K] tensor."""
+    _require_cuda(x, codes, scales)
+    _check_flat(x)
+    if bits not in (8, 4):
+        raise ValueError("tokenwise activations are A8 or A4")
+    m, k = x.shape
+    if codes is None:
+        codes = torch.empty((m, k) if bits == 8 else (m, k // 2), device=x.device,
+                            dtype=torch.int8 if bits == 8 else torch.uint8)
+    if scales is None:
+        scales = torch.empty(m, device=x.device, dtype=torch.float32)
+    _check_buffer(codes, "codes", (m, k) if bits == 8 else (m, k // 2), torch.int8 if bits == 8 else torch.uint8,
+                  x.device)
+    _check_buffer(scales, "scales", (m,), torch.float32, x.device)
+    _check(lib().actune_tokenwise_quantize(_ptr(x), _dtype_code(x), m, k, bits, _ptr(codes), _ptr(scales),
+                                           _stream(x.device)))
+    return codes, scales
+
+
+def tokenwise_workspace_bytes(m, n, k, w_layout, a_layout):
+    need = lib().actune_tokenwise_workspace_bytes(m, n, k, w_layout, a_layout)
+    if need < 0:
+        raise ValueError(lib().actune_last_error().decode())
+    return need
+
+
+def tokenwise_linear(a, a_layout, as_, w, w_layout, ws, bias, n, k, epilogue, out, workspace=None):
+    """out[m, n] = epilogue(exact int32 sum_k a[m, k] w[n, k]) through
+    actune_tokenwise_linear. a: int8 [M, K] (A8) or u8 [M, K/2] (A4); w in
+    layout w_layout; out: preallocated [M, N]; workspace: u8 tensor of at
+    least tokenwise_workspace_bytes() bytes (None when that is 0)."""
+    _require_cuda(a, as_, w, ws, bias, out, workspace)
+    m = a.shape[0]
+    if not (a.is_contiguous() and as_.is_contiguous() and w.is_contiguous() and ws.is_contiguous()
+            and (bias is None or bias.is_contiguous())):
+        raise RuntimeError("contiguous operands required")
+    if as_.dtype != torch.float32 or ws.dtype != torch.float32:
+        raise RuntimeError("float scales/bias required")
+    if as_.numel() != m or ws.numel() != n or (bias is not None and bias.numel() != n):
+        raise RuntimeError("scale shape mismatch")
+    abytes = k if a_layout == TW_ACT_A8 else k // 2
+    if a.dim() != 2 or a.shape[1] != abytes or a.element_size() != 1:
+        raise RuntimeError("packed activation shape mismatch")
+    wbytes = {TW_KMAJOR_W8: k * n, TW_KMAJOR_W4: k // 2 * n, TW_KMAJOR_W2: k // 4 * n,
+              TW_ROWS_S4: n * k // 2, TW_ROWS_S2: n * k // 4}[w_layout]
+    if w.numel() != wbytes or w.element_size() != 1:
+        raise RuntimeError("packed weight shape mismatch")
+    _check_buffer(out, "out", (m, n), out.dtype, a.device)
+    need = tokenwise_workspace_bytes(m, n, k, w_layout, a_layout)
+    if need and (workspace is None or workspace.numel() < need or workspace.dtype != torch.uint8):
+        raise RuntimeError(f"workspace of at least {need} bytes required")
+    _check(lib().actune_tokenwise_linear(
+        _ptr(a), a_layout, _ptr(as_), _ptr(w), w_layout, _ptr(ws), _ptr(bias), _bias_code(bias), _ptr(out),
+        _dtype_code(out), m, n, k, epilogue, _ptr(workspace) if need else None, need, _stream(a.device)))
+    return out

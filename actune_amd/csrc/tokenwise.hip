@@ -1,0 +1,615 @@
+// Tokenwise (per-row) packed-integer linears for gfx950: the per-row dynamic
+// A8 / A4 quantizer and one int8-MFMA GEMM for every weight layout of the
+// reference's tokenwise family, with exact full-K int32 accumulation and an
+// optional exact split-K across workgroups.
+//
+// Restates (zanehpn/Actune):
+//   per-row A8 quantizer  actune/kernels/w4a8_triton.py:161-201 (also
+//                         decode_w4a8_triton.py:21-28, resident_a8_triton.py:13-21)
+//   per-row A4 quantizer  actune/kernels/wxa4_native.py:28-65
+//   W4A8  K-major nibble pairs     w4a8_triton.py:57-114, 380-383
+//   W8A8  K-major int8             w8a8_triton.py:21-77, 100-107
+//   W2A8  K-major quarters         w2a8_triton.py:24-112, 149-159
+//   W4A4 / W2A4 row-major S4 / S2  native_s4_extension_kernel.cu:239-481
+//   W8A4  K-major nested int8 x A4 wxa4_native.py:315-391
+//   exact split-K, integer reduce  decode_w4a8_triton.py:31-110
+//
+// Arithmetic. Codes of width b are held as int8 c * 2^(8-b) (the field at the
+// top of its byte), so an int8 MFMA returns 2^T times the true dot, T = the
+// two operands' shifts; |every product| <= 2^14, so the int32 sum over K is
+// exact for K < 2^17 and the arithmetic shift by T recovers the true
+// accumulator. Integer sums do not depend on order: split-K partials are
+// added in any order and the result is still bit-exact. The fp32 epilogue
+// is then one fixed sequence per output (tokenwise_oracle.c):
+//   A8 family: t = f32(acc) * as[m]; y = bias ? fmaf(t, ws[n], bias[n]) : t * ws[n]
+//   native A4: q = as[m] * ws[n];    y = bias ? fmaf(f32(acc), q, bias[n]) : f32(acc) * q
+//
+// MFMA operands (v_mfma_i32_16x16x64_i8): tokens are the A operand, output
+// channels the B operand; lane l holds row l % 16 and the 16 k-slots of
+// group kb = l / 16. The k index behind each slot only has to be the same
+// for both operands, so each weight layout uses the slot order its bytes
+// give cheapest:
+//   K-major layouts (rows of the buffer run along K, columns along N): the
+//     weight tile is staged in LDS as buffer rows and read back transposed
+//     with ds_read_b64_tr_b8 (in each 16-lane group, lane 2i + h points at
+//     row i, bytes 8h..8h+7 of 16 columns; lane c receives column c of the
+//     8 rows). One read gives a lane 8 consecutive buffer rows of its column:
+//     8 k (W8), 16 k (nibble pairs: k = j and j + K/2) or 32 k (quarters:
+//     j + f K/4 for f = 0..3, two MFMAs).
+//   row-major S4 / S2 (the group-64 packing): a lane's 16 k-slots are one
+//     8- (S4) or 4-byte (S2) run of its row, unpacked in the width's native
+//     element order (common.hpp), and the activation slot is reordered to it.
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <climits>
+
+#include "../../include/actune_hip.h"
+#include "common.hpp"
+#include "launch.hpp"
+#include "operands.hpp"
+
+namespace actune {
+namespace {
+
+constexpr int kThreads = 256;
+
+template <int WL> struct WTraits;
+// U: MFMAs per K-step (64 k each); TW: shift of the weight codes;
+// rows(TN): rows of the staged weight tile; row_bytes(TN): bytes per staged row
+template <> struct WTraits<ACTUNE_TW_KMAJOR_W8> {
+  static constexpr int U = 1, TW = 0;
+  static constexpr bool KM = true;
+  static constexpr int rows(int) { return 64; }
+  static constexpr int row_bytes(int tn) { return tn; }
+};
+template <> struct WTraits<ACTUNE_TW_KMAJOR_W4> {
+  static constexpr int U = 1, TW = 4;
+  static constexpr bool KM = true;
+  static constexpr int rows(int) { return 32; }
+  static constexpr int row_bytes(int tn) { return tn; }
+};
+template <> struct WTraits<ACTUNE_TW_KMAJOR_W2> {
+  static constexpr int U = 2, TW = 6;
+  static constexpr bool KM = true;
+  static constexpr int rows(int) { return 32; }
+  static constexpr int row_bytes(int tn) { return tn; }
+};
+template <> struct WTraits<ACTUNE_TW_ROWS_S4> {
+  static constexpr int U = 1, TW = 4;
+  static constexpr bool KM = false;
+  static constexpr int rows(int tn) { return tn; }
+  static constexpr int row_bytes(int) { return 32; }
+};
+template <> struct WTraits<ACTUNE_TW_ROWS_S2> {
+  static constexpr int U = 1, TW = 6;
+  static constexpr bool KM = false;
+  static constexpr int rows(int tn) { return tn; }
+  static constexpr int row_bytes(int) { return 16; }
+};
+
+// Padded LDS row strides: the transposed reads of 8 weight rows and the
+// 16-row activation reads each touch distinct banks.
+constexpr int w_stride(int wl, int tn) {
+  return wl <= ACTUNE_TW_KMAJOR_W2 ? tn + 16 : (wl == ACTUNE_TW_ROWS_S4 ? 40 : 20);
+}
+// activation bytes per staged row and K-step: int8 codes 64 per MFMA (the
+// nibble-pair layout stages k = j.. and K/2 + j.. as two 32-byte pieces, the
+// quarter layout four), packed A4 codes 32 bytes
+constexpr int a_row_bytes(int wl, int al) { return al == ACTUNE_TW_ACT_A4 ? 32 : (wl == ACTUNE_TW_KMAJOR_W2 ? 128 : 64); }
+constexpr int a_stride(int wl, int al) { return al == ACTUNE_TW_ACT_A4 ? 40 : a_row_bytes(wl, al) + 16; }
+
+struct TwArgs {
+  const uint8_t* a;     // int8 codes [M, K] or packed A4 [M, K/2]
+  const float* as;      // [M]
+  const uint8_t* w;     // weight buffer (layout WL)
+  const float* ws;      // [N]
+  const void* bias;     // [N] or nullptr
+  void* out;            // [M, N]
+  int32_t* partial;     // [S, M, N] int32 (S > 1)
+  uint32_t* counters;   // [tiles_m * tiles_n] (S > 1), zero between launches
+  int M, N, K, bias_dt, out_dt, splits, steps;
+};
+
+__device__ __forceinline__ v2u tr8(const uint8_t* p) {
+  typedef int v2i_t __attribute__((ext_vector_type(2)));
+  auto lp = (__attribute__((address_space(3))) v2i_t*)((__attribute__((address_space(3))) uint8_t*)p);
+  const v2i_t r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(lp);
+  return v2u{(uint32_t)r[0], (uint32_t)r[1]};
+}
+
+// 16-byte store to LDS at an address aligned to ALIGN bytes (16, 8 or 4)
+template <int ALIGN>
+__device__ __forceinline__ void lds_store16(uint8_t* p, const v4u& v) {
+  if constexpr (ALIGN >= 16) {
+    *reinterpret_cast<v4u*>(p) = v;
+  } else if constexpr (ALIGN >= 8) {
+    reinterpret_cast<v2u*>(p)[0] = v2u{v[0], v[1]};
+    reinterpret_cast<v2u*>(p)[1] = v2u{v[2], v[3]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) reinterpret_cast<uint32_t*>(p)[i] = v[i];
+  }
+}
+
+constexpr int align_of_stride(int s) { return s % 16 == 0 ? 16 : (s % 8 == 0 ? 8 : 4); }
+
+// WM waves along M (1 or 2), the rest along N; each wave owns MT x NT
+// 16x16 output tiles. Workgroup tile: TM = 16 MT WM rows, TN = 16 NT (4/WM)
+// columns. Grid: x = column tiles, y = row tiles, z = K splits.
+template <int WL, int AL, int EPI, int WM, int MT, int NT>
+__global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
+  using T = WTraits<WL>;
+  constexpr int WN = 4 / WM;
+  constexpr int TM = 16 * MT * WM, TN = 16 * NT * WN;
+  constexpr int U = T::U;
+  constexpr int WROWS = T::rows(TN), WRB = T::row_bytes(TN), WSTR = w_stride(WL, TN);
+  constexpr int ARB = a_row_bytes(WL, AL), ASTR = a_stride(WL, AL);
+  constexpr int WBUF = WROWS * WSTR, ABUF = TM * ASTR;
+  constexpr int WCH = WROWS * WRB / 16, ACH = TM * ARB / 16;       // 16-byte chunks per step
+  constexpr int NWC = (WCH + kThreads - 1) / kThreads, NAC = (ACH + kThreads - 1) / kThreads;
+  constexpr int SHIFT = T::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0);
+  __shared__ __align__(16) uint8_t smem[2 * (WBUF + ABUF)];
+  __shared__ int s_last;
+
+  const int M = args.M, N = args.N, K = args.K;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int n0 = (int)blockIdx.x * TN, m0 = (int)blockIdx.y * TM;
+  const int S = args.splits, z = (int)blockIdx.z;
+  const int g0 = (int)((long)z * args.steps / S), g1 = (int)((long)(z + 1) * args.steps / S);
+
+  // buffer resources: reads past the end return zeros
+  uint32_t wbytes;
+  if constexpr (WL == ACTUNE_TW_KMAJOR_W8) wbytes = (uint32_t)K * N;
+  else if constexpr (WL == ACTUNE_TW_KMAJOR_W4) wbytes = (uint32_t)(K / 2) * N;
+  else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) wbytes = (uint32_t)(K / 4) * N;
+  else if constexpr (WL == ACTUNE_TW_ROWS_S4) wbytes = (uint32_t)N * (K / 2);
+  else wbytes = (uint32_t)N * (K / 4);
+  const uint32_t arow = AL == ACTUNE_TW_ACT_A4 ? (uint32_t)K / 2 : (uint32_t)K;
+  const Rsrc wr = make_rsrc(args.w, wbytes);
+  const Rsrc ar = make_rsrc(args.a, (uint32_t)M * arow);
+
+  // global byte offset of weight chunk c of step g (kOff: nothing to load)
+  auto w_off = [&](int g, int c) -> uint32_t {
+    if (c >= WCH) return kOff;
+    const int row = c / (WRB / 16), cb = c % (WRB / 16);
+    if constexpr (T::KM) {
+      const int col = n0 + 16 * cb;
+      const long r = (long)g * WROWS + row;   // buffer row (k, or j of K/2 / K/4)
+      if (col >= N) return kOff;
+      return (uint32_t)(r * N + col);
+    } else {
+      const int n = n0 + row;
+      if (n >= N) return kOff;
+      return (uint32_t)((long)n * (WL == ACTUNE_TW_ROWS_S4 ? K / 2 : K / 4) + (long)g * WRB + 16 * cb);
+    }
+  };
+  // global byte offset of activation chunk c of step g
+  auto a_off = [&](int g, int c) -> uint32_t {
+    if (c >= ACH) return kOff;
+    const int row = c / (ARB / 16), cb = c % (ARB / 16);
+    const int m = m0 + row;
+    if (m >= M) return kOff;
+    long k;
+    if constexpr (AL == ACTUNE_TW_ACT_A4) {
+      k = (long)g * 32 + 16 * cb;                            // bytes of the packed row
+    } else if constexpr (WL == ACTUNE_TW_KMAJOR_W4) {
+      k = (long)(cb >> 1) * (K / 2) + (long)g * 32 + 16 * (cb & 1);
+    } else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) {
+      k = (long)(cb >> 1) * (K / 4) + (long)g * 32 + 16 * (cb & 1);
+    } else {
+      k = (long)g * 64 + 16 * cb;
+    }
+    return (uint32_t)((long)m * arow + k);
+  };
+
+  v4u wreg[NWC], areg[NAC];
+  auto issue = [&](int g) {
+#pragma unroll
+    for (int i = 0; i < NWC; ++i) wreg[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, w_off(g, tid + i * kThreads), 0, 0);
+#pragma unroll
+    for (int i = 0; i < NAC; ++i) areg[i] = __builtin_amdgcn_raw_buffer_load_b128(ar, a_off(g, tid + i * kThreads), 0, 0);
+  };
+  auto stage = [&](int buf) {
+    uint8_t* wt = smem + buf * (WBUF + ABUF);
+    uint8_t* at = wt + WBUF;
+#pragma unroll
+    for (int i = 0; i < NWC; ++i) {
+      const int c = tid + i * kThreads;
+      if (c < WCH) lds_store16<align_of_stride(WSTR)>(wt + (c / (WRB / 16)) * WSTR + 16 * (c % (WRB / 16)), wreg[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < NAC; ++i) {
+      const int c = tid + i * kThreads;
+      if (c < ACH) lds_store16<align_of_stride(ASTR)>(at + (c / (ARB / 16)) * ASTR + 16 * (c % (ARB / 16)), areg[i]);
+    }
+  };
+
+  v4i acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  const int r16 = lane & 15, kb = lane >> 4;
+  // transposed-read lane address inside a 16-lane group: row i, half h
+  const int tr_row = (lane & 15) >> 1, tr_half = lane & 1;
+
+  auto compute = [&](int buf) {
+    const uint8_t* wt = smem + buf * (WBUF + ABUF);
+    const uint8_t* at = wt + WBUF;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      uint32_t bf[NT][4];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int cn = wn * 16 * NT + nt * 16;
+        if constexpr (WL == ACTUNE_TW_KMAJOR_W8) {
+          const v2u lo = tr8(wt + (16 * kb + tr_row) * WSTR + cn + 8 * tr_half);
+          const v2u hi = tr8(wt + (16 * kb + 8 + tr_row) * WSTR + cn + 8 * tr_half);
+          bf[nt][0] = lo[0]; bf[nt][1] = lo[1]; bf[nt][2] = hi[0]; bf[nt][3] = hi[1];
+        } else if constexpr (WL == ACTUNE_TW_KMAJOR_W4) {
+          const v2u b = tr8(wt + (8 * kb + tr_row) * WSTR + cn + 8 * tr_half);
+          bf[nt][0] = (b[0] << 4) & 0xF0F0F0F0u; bf[nt][1] = (b[1] << 4) & 0xF0F0F0F0u;
+          bf[nt][2] = b[0] & 0xF0F0F0F0u;        bf[nt][3] = b[1] & 0xF0F0F0F0u;
+        } else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) {
+          const v2u b = tr8(wt + (8 * kb + tr_row) * WSTR + cn + 8 * tr_half);
+          // fields 2u (k = j + 2u K/4) and 2u + 1 (k = j + (2u+1) K/4)
+          const int s0 = 6 - 4 * u, s1 = 4 - 4 * u;  // u = 0: 6, 4; u = 1: 2, 0
+          bf[nt][0] = (b[0] << s0) & 0xC0C0C0C0u;
+          bf[nt][1] = (b[1] << s0) & 0xC0C0C0C0u;
+          bf[nt][2] = (b[0] << s1) & 0xC0C0C0C0u;
+          bf[nt][3] = (b[1] << s1) & 0xC0C0C0C0u;
+        } else if constexpr (WL == ACTUNE_TW_ROWS_S4) {
+          const v2u p = *reinterpret_cast<const v2u*>(wt + (cn + r16) * WSTR + 8 * kb);
+          const uint32_t pp[2] = {p[0], p[1]};
+          unpack_slot<4>(pp, bf[nt]);
+        } else {
+          const uint32_t p = *reinterpret_cast<const uint32_t*>(wt + (cn + r16) * WSTR + 4 * kb);
+          unpack_slot<2>(&p, bf[nt]);
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint8_t* arow_l = at + (wm * 16 * MT + mt * 16 + r16) * ASTR;
+        uint32_t af[4];
+        if constexpr (AL == ACTUNE_TW_ACT_A4) {
+          const v2u p = *reinterpret_cast<const v2u*>(arow_l + 8 * kb);
+          const uint32_t pp[2] = {p[0], p[1]};
+          unpack_slot<4>(pp, af);
+          if constexpr (WL == ACTUNE_TW_ROWS_S2) reorder_slot<4, 2>(af);
+          else if constexpr (T::KM) reorder_slot<4, 8>(af);
+        } else if constexpr (WL == ACTUNE_TW_KMAJOR_W4 || WL == ACTUNE_TW_KMAJOR_W2) {
+          const v2u lo = *reinterpret_cast<const v2u*>(arow_l + 64 * u + 8 * kb);
+          const v2u hi = *reinterpret_cast<const v2u*>(arow_l + 64 * u + 32 + 8 * kb);
+          af[0] = lo[0]; af[1] = lo[1]; af[2] = hi[0]; af[3] = hi[1];
+        } else {
+          const v4u q = *reinterpret_cast<const v4u*>(arow_l + 16 * kb);
+          af[0] = q[0]; af[1] = q[1]; af[2] = q[2]; af[3] = q[3];
+          if constexpr (WL == ACTUNE_TW_ROWS_S4) reorder_slot<8, 4>(af);
+          else if constexpr (WL == ACTUNE_TW_ROWS_S2) reorder_slot<8, 2>(af);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma16x16x64(af, bf[nt], acc[mt][nt]);
+      }
+    }
+  };
+
+  // two-buffer pipeline: step g+1's loads are in flight while step g computes
+  if (g0 < g1) {
+    issue(g0);
+    stage(0);
+    __syncthreads();
+    for (int g = g0; g < g1; ++g) {
+      const int buf = (g - g0) & 1;
+      if (g + 1 < g1) issue(g + 1);
+      compute(buf);
+      if (g + 1 < g1) stage(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // ---------------------------------------------------------------- split-K
+  const int row_base = m0 + wm * 16 * MT + 4 * kb, col_base = n0 + wn * 16 * NT + r16;
+  if (S > 1) {
+    int32_t* part = args.partial + (size_t)z * M * N;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = row_base + mt * 16 + i, n = col_base + nt * 16;
+          if (m < M && n < N) part[(size_t)m * N + n] = acc[mt][nt][i];
+        }
+    __threadfence();
+    __syncthreads();
+    const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x;
+    if (tid == 0) s_last = atomicAdd(&args.counters[tile], 1u) == (uint32_t)(S - 1);
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = row_base + mt * 16 + i, n = col_base + nt * 16;
+          int32_t sum = 0;
+          if (m < M && n < N)
+            for (int s = 0; s < S; ++s) sum += __builtin_nontemporal_load(args.partial + ((size_t)s * M + m) * N + n);
+          acc[mt][nt][i] = sum;
+        }
+    if (tid == 0) args.counters[tile] = 0u;  // ready for the next launch
+  }
+
+  // ---------------------------------------------------------------- epilogue
+  const bool has_bias = args.bias != nullptr;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int n = col_base + nt * 16;
+    if (n >= N) continue;
+    const float ws = args.ws[n];
+    const float b = has_bias ? load_bias(args.bias, args.bias_dt, n) : 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = row_base + mt * 16 + i;
+        if (m >= M) continue;
+        const float a = (float)(acc[mt][nt][i] >> SHIFT);
+        const float as = args.as[m];
+        float y;
+        if constexpr (EPI == ACTUNE_TW_EPI_A8) {
+          const float t = a * as;
+          y = has_bias ? __builtin_fmaf(t, ws, b) : t * ws;
+        } else {
+          const float q = as * ws;
+          y = has_bias ? __builtin_fmaf(a, q, b) : a * q;
+        }
+        const size_t o = (size_t)m * N + n;
+        if (args.out_dt == kBF16) store_out<kBF16>(args.out, o, y);
+        else if (args.out_dt == kF16) store_out<kF16>(args.out, o, y);
+        else store_out<kF32>(args.out, o, y);
+      }
+  }
+}
+
+// ---------------------------------------------------------------- quantizer
+// One workgroup per row: amax over the row (wave shuffles, then LDS across
+// the 4 waves), s = fl(max(amax, f32(1e-8)) * fl(1/p)), codes rint(v / s)
+// (IEEE division) clamped to [-p-1, p]. A8 writes int8 codes, A4 packs two
+// codes per byte (low nibble = even k). Each lane handles 8 consecutive
+// elements per pass; the second pass re-reads the row (L2-resident).
+template <int A, int DT>
+__global__ __launch_bounds__(kThreads) void tw_quantize_kernel(const void* __restrict__ x, int K,
+                                                               uint8_t* __restrict__ codes,
+                                                               float* __restrict__ scales) {
+  constexpr int P = (1 << (A - 1)) - 1;
+  constexpr float R = 1.0f / (float)P;
+  constexpr int ESZ = DT == kF32 ? 4 : 2;
+  __shared__ float red[kThreads / 64];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const char* row = static_cast<const char*>(x) + (size_t)m * K * ESZ;
+  float amax = 0.0f;
+  for (int e = tid * 8; e < K; e += kThreads * 8) {
+    float v[8];
+    load8<DT>(row, e, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) amax = fmaxf(amax, red[w]);
+  const float s = fmaxf(amax, 1e-8f) * R;
+  if (tid == 0) scales[m] = s;
+  for (int e = tid * 8; e < K; e += kThreads * 8) {
+    float v[8];
+    load8<DT>(row, e, v);
+    int c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = (int)fminf(fmaxf(rintf(v[i] / s), (float)(-P - 1)), (float)P);
+    if constexpr (A == 8) {
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { lo |= ((uint32_t)c[i] & 0xffu) << (8 * i); hi |= ((uint32_t)c[4 + i] & 0xffu) << (8 * i); }
+      *reinterpret_cast<v2u*>(codes + (size_t)m * K + e) = v2u{lo, hi};
+    } else {
+      uint32_t w = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) w |= ((uint32_t)c[i] & 0xfu) << (4 * i);
+      *reinterpret_cast<uint32_t*>(codes + (size_t)m * (K / 2) + e / 2) = w;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- host side
+struct Geometry {
+  int wm, mt, nt;
+  int tm() const { return 16 * mt * wm; }
+  int tn() const { return 16 * nt * (4 / wm); }
+};
+
+// M <= 32: 16-row tiles, 128 columns per workgroup, K split across
+// workgroups until the grid holds about 2 workgroups per CU; above: 128 x
+// 128 tiles (2 x 2 waves of 64 x 64).
+Geometry pick_geometry(int64_t M) { return M <= 32 ? Geometry{1, 1, 2} : Geometry{2, 4, 4}; }
+
+int kps_of(int wl) { return wl == ACTUNE_TW_KMAJOR_W2 ? 128 : 64; }
+
+// K splits: small-M tiles split until the grid holds about two workgroups
+// per CU (the weight stream is the cost; partials are M x N int32 per
+// split); large-M tiles only below one workgroup per CU, and only while the
+// partials stay small against the operands. Every split keeps >= 2 K-steps.
+int pick_splits(int64_t M, int64_t N, int64_t K, int wl, const Geometry& g) {
+  const int64_t tiles = ((N + g.tn() - 1) / g.tn()) * ((M + g.tm() - 1) / g.tm());
+  const int64_t steps = (K + kps_of(wl) - 1) / kps_of(wl);
+  const int64_t target = g.wm == 1 ? 512 : 256;
+  int64_t s = 1;
+  while (tiles * s < target && s * 4 <= steps && s < 64 && (g.wm == 1 || 2 * s * M * N * 4 <= (int64_t)8 << 20))
+    s *= 2;
+  return (int)s;
+}
+
+template <int WL, int AL, int EPI, int WM, int MT, int NT>
+void launch_gemm_t(const TwArgs& a, hipStream_t st) {
+  constexpr int TM = 16 * MT * WM, TN = 16 * NT * (4 / WM);
+  const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM), (unsigned)a.splits);
+  tw_gemm<WL, AL, EPI, WM, MT, NT><<<grid, kThreads, 0, st>>>(a);
+}
+
+template <int WL, int AL, int EPI>
+void launch_gemm_g(const TwArgs& a, const Geometry& g, hipStream_t st) {
+  if (g.wm == 1) launch_gemm_t<WL, AL, EPI, 1, 1, 2>(a, st);
+  else launch_gemm_t<WL, AL, EPI, 2, 4, 4>(a, st);
+}
+
+// the six (weight layout, activation layout) pairs of the reference family
+bool pair_ok(int wl, int al) {
+  if (al == ACTUNE_TW_ACT_A8) return wl <= ACTUNE_TW_KMAJOR_W2;
+  if (al == ACTUNE_TW_ACT_A4) return wl == ACTUNE_TW_KMAJOR_W8 || wl == ACTUNE_TW_ROWS_S4 || wl == ACTUNE_TW_ROWS_S2;
+  return false;
+}
+
+void launch_gemm(int wl, int al, int epi, const TwArgs& a, const Geometry& g, hipStream_t st) {
+#define TW_CASE(W_, A_)                                                            \
+  if (wl == W_ && al == A_) {                                                      \
+    if (epi == ACTUNE_TW_EPI_A8) launch_gemm_g<W_, A_, ACTUNE_TW_EPI_A8>(a, g, st); \
+    else launch_gemm_g<W_, A_, ACTUNE_TW_EPI_A4>(a, g, st);                        \
+    return;                                                                        \
+  }
+  TW_CASE(ACTUNE_TW_KMAJOR_W8, ACTUNE_TW_ACT_A8)
+  TW_CASE(ACTUNE_TW_KMAJOR_W4, ACTUNE_TW_ACT_A8)
+  TW_CASE(ACTUNE_TW_KMAJOR_W2, ACTUNE_TW_ACT_A8)
+  TW_CASE(ACTUNE_TW_KMAJOR_W8, ACTUNE_TW_ACT_A4)
+  TW_CASE(ACTUNE_TW_ROWS_S4, ACTUNE_TW_ACT_A4)
+  TW_CASE(ACTUNE_TW_ROWS_S2, ACTUNE_TW_ACT_A4)
+#undef TW_CASE
+}
+
+int64_t round256(int64_t v) { return (v + 255) / 256 * 256; }
+
+int fail(const char* msg) {
+  set_last_error(msg);
+  return ACTUNE_ERR_INVALID;
+}
+
+thread_local char g_tw_msg[128];
+
+// Shape checks shared by the workspace query and the linear.
+int check_tw_shape(int64_t M, int64_t N, int64_t K, int wl, int al) {
+  if (!pair_ok(wl, al)) return fail("unsupported tokenwise weight/activation layout pair");
+  if (M < 0 || N <= 0 || K <= 0) return fail("invalid dimensions");
+  if (K >= (1 << 17)) return fail("K must stay below 131072 (exact int32 accumulation)");
+  const int kq = wl == ACTUNE_TW_KMAJOR_W4 ? 32 : (wl == ACTUNE_TW_KMAJOR_W2 ? 128 : 64);
+  if (K % kq) {
+    snprintf(g_tw_msg, sizeof g_tw_msg, "in_features must be divisible by %d for this layout", kq);
+    return fail(g_tw_msg);
+  }
+  if (wl <= ACTUNE_TW_KMAJOR_W2 && N % 16) return fail("K-major weight layouts need out_features divisible by 16");
+  if (N > INT_MAX / 2 || M > INT_MAX / 2 || M * K >= ((int64_t)1 << 31) || N * K >= ((int64_t)1 << 31) ||
+      M * N * 4 >= ((int64_t)1 << 31))
+    return fail("operand too large (each buffer must stay below 2 GiB)");
+  return ACTUNE_OK;
+}
+
+}  // namespace
+}  // namespace actune
+
+using namespace actune;
+
+extern "C" {
+
+int actune_tokenwise_quantize(const void* x, int x_dtype, int64_t M, int64_t K, int A, void* codes,
+                              float* scales, void* stream) {
+  set_last_error("");
+  if (A != 8 && A != 4) return fail("tokenwise activations are A8 or A4");
+  if (x_dtype != kBF16 && x_dtype != kF16 && x_dtype != kF32) return fail("unsupported activation dtype");
+  if (M < 0 || K <= 0 || K % 8) return fail("in_features must be a positive multiple of 8");
+  if (M > INT_MAX || M * K >= ((int64_t)1 << 31)) return fail("activation too large");
+  if (M == 0) return ACTUNE_OK;
+  if (!x || !codes || !scales) return fail("null pointer");
+  if (((uintptr_t)x % 16) || ((uintptr_t)codes % 8) || ((uintptr_t)scales % 4))
+    return fail("misaligned operand (x needs 16 B, codes 8 B)");
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)M);
+  uint8_t* c = static_cast<uint8_t*>(codes);
+#define TWQ(A_, DT_) tw_quantize_kernel<A_, DT_><<<grid, kThreads, 0, st>>>(x, (int)K, c, scales)
+  if (A == 8) {
+    if (x_dtype == kBF16) TWQ(8, kBF16); else if (x_dtype == kF16) TWQ(8, kF16); else TWQ(8, kF32);
+  } else {
+    if (x_dtype == kBF16) TWQ(4, kBF16); else if (x_dtype == kF16) TWQ(4, kF16); else TWQ(4, kF32);
+  }
+#undef TWQ
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_last_error(hipGetErrorString(e));
+    return ACTUNE_ERR_DEVICE;
+  }
+  return ACTUNE_OK;
+}
+
+int64_t actune_tokenwise_workspace_bytes(int64_t M, int64_t N, int64_t K, int w_layout, int a_layout) {
+  if (check_tw_shape(M, N, K, w_layout, a_layout)) return -1;
+  const Geometry g = pick_geometry(M);
+  const int S = pick_splits(M, N, K, w_layout, g);
+  if (S == 1) return 0;
+  const int64_t tiles = ((N + g.tn() - 1) / g.tn()) * ((M + g.tm() - 1) / g.tm());
+  return round256(tiles * 4) + (int64_t)S * M * N * 4;
+}
+
+int actune_tokenwise_linear(const void* a, int a_layout, const float* a_scales, const void* w, int w_layout,
+                            const float* w_scale, const void* bias, int bias_dtype, void* out, int out_dtype,
+                            int64_t M, int64_t N, int64_t K, int epilogue, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  set_last_error("");
+  int rc = check_tw_shape(M, N, K, w_layout, a_layout);
+  if (rc) return rc;
+  if (epilogue != ACTUNE_TW_EPI_A8 && epilogue != ACTUNE_TW_EPI_A4) return fail("unknown epilogue");
+  if ((bias && bias_dtype != kBF16 && bias_dtype != kF16 && bias_dtype != kF32) ||
+      (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32))
+    return fail("unsupported output/bias dtype");
+  if (M == 0) return ACTUNE_OK;
+  if (!a || !a_scales || !w || !w_scale || !out) return fail("null pointer");
+  if (((uintptr_t)a % 16) || ((uintptr_t)w % 16) || ((uintptr_t)a_scales % 4) || ((uintptr_t)w_scale % 4))
+    return fail("misaligned operand (packed data needs 16 B)");
+  const Geometry g = pick_geometry(M);
+  const int S = pick_splits(M, N, K, w_layout, g);
+  TwArgs args{};
+  args.a = static_cast<const uint8_t*>(a);
+  args.as = a_scales;
+  args.w = static_cast<const uint8_t*>(w);
+  args.ws = w_scale;
+  args.bias = bias;
+  args.out = out;
+  args.M = (int)M;
+  args.N = (int)N;
+  args.K = (int)K;
+  args.bias_dt = bias_dtype;
+  args.out_dt = out_dtype;
+  args.splits = S;
+  args.steps = (int)((K + kps_of(w_layout) - 1) / kps_of(w_layout));
+  if (S > 1) {
+    const int64_t need = actune_tokenwise_workspace_bytes(M, N, K, w_layout, a_layout);
+    if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 256))
+      return fail("workspace missing, misaligned or smaller than actune_tokenwise_workspace_bytes()");
+    const int64_t tiles = ((N + g.tn() - 1) / g.tn()) * ((M + g.tm() - 1) / g.tm());
+    args.counters = static_cast<uint32_t*>(workspace);
+    args.partial = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + round256(tiles * 4));
+  }
+  launch_gemm(w_layout, a_layout, epilogue, args, g, (hipStream_t)stream);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_last_error(hipGetErrorString(e));
+    return ACTUNE_ERR_DEVICE;
+  }
+  return ACTUNE_OK;
+}
+
+}  // extern "C"

@@ -36,6 +36,14 @@ ALIASES = {
     "actune.kernels.grouped": "actune_amd.kernels.grouped",
     "actune.kernels.quantizers": "actune_amd.kernels.quantizers",
     "actune.kernels.tuning": "actune_amd.kernels.tuning",
+    # the tokenwise family: one module serves the five reference modules
+    "actune.kernels.w4a8_triton": "actune_amd.kernels.tokenwise",
+    "actune.kernels.w8a8_triton": "actune_amd.kernels.tokenwise",
+    "actune.kernels.w2a8_triton": "actune_amd.kernels.tokenwise",
+    "actune.kernels.wxa4_native": "actune_amd.kernels.tokenwise",
+    "actune.kernels.decode_w4a8_triton": "actune_amd.kernels.tokenwise",
+    "actune.kernels.resident_a8_triton": "actune_amd.kernels.tokenwise",
+    "actune.kernels.runtime_options": "actune_amd.kernels.tokenwise",
 }
 
 

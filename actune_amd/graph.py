@@ -35,8 +35,6 @@ def _literal(data):
 
 class GraphReplay:
     def __init__(self, function, layers, *, shared_a8=False, max_graphs=12):
-        if shared_a8:
-            raise NotImplementedError("the tokenwise shared-A8 cache is not part of the group-64 backend")
         self.function = function
         self.layers = layers
         self.shared_a8 = shared_a8
@@ -51,7 +49,9 @@ class GraphReplay:
     def scope(self):
         """Serve small literal GPU constants built inside the function from a
         cache filled during warm-up (a fresh host->device copy cannot be
-        captured); each use gets a clone because callers update in place."""
+        captured); each use gets a clone because callers update in place.
+        Also bounds the tokenwise shared-activation cache to the call,
+        enabled when shared_a8 is set (graph.py:18-42)."""
         make = torch.tensor
 
         def cached_tensor(data, *args, **kwargs):
@@ -66,7 +66,8 @@ class GraphReplay:
                 self.constants[key] = make(data, **kwargs)
             return self.constants[key].clone()
 
-        with patch.object(torch, "tensor", cached_tensor):
+        from .kernels.tokenwise import shared_a8_cache_scope
+        with shared_a8_cache_scope(enabled=self.shared_a8), patch.object(torch, "tensor", cached_tensor):
             yield
 
     def _key(self, leaves, spec):

@@ -42,15 +42,26 @@ def _clipped_absmax(value, clip_ratios):
     return amax * _validate_clip_ratios(clip_ratios, out_features=value.shape[0], device=value.device)
 
 
+def _div_const(value, constant, gpu_division):
+    """value / constant in fp32: the IEEE quotient (torch-CPU), or, with
+    gpu_division, value times the fp32 reciprocal 1.0f / constant, which is
+    what torch computes for a GPU tensor divided by a Python scalar (the
+    reference's own note, w4a8_triton.py:33-36)."""
+    if not gpu_division:
+        return value / constant
+    reciprocal = torch.tensor(1.0, dtype=torch.float32) / constant
+    return value * reciprocal
+
+
 def _round_clamp(value, scale, lo, hi):
     """rint_half_even(value / scale[:, None]) clamped to [lo, hi], as int8."""
     return torch.clamp(torch.round(value / scale[:, None]), lo, hi).to(torch.int8)
 
 
-def symmetric_int4_quantize(weight, *, clip_ratios=None):
+def symmetric_int4_quantize(weight, *, clip_ratios=None, gpu_division=False):
     """W4 codes in [-8, 7] and the row scale (amax * r) / 7."""
     value = _fp32_cpu(weight)
-    scale = _clipped_absmax(value, clip_ratios) / 7.0
+    scale = _div_const(_clipped_absmax(value, clip_ratios), 7.0, gpu_division)
     codes = _round_clamp(value, scale, -8, 7)
     return codes.to(weight.device), scale.contiguous().to(weight.device)
 
@@ -79,18 +90,21 @@ def symmetric_int2_quantize(weight, *, clip_ratios=None):
     return codes.to(weight.device), scale.contiguous().to(weight.device)
 
 
-def weight_codes(weight, w, a, *, clip_ratios=None):
+def weight_codes(weight, w, a, *, clip_ratios=None, gpu_division=False):
     """(int8 codes [N, K], fp32 scale [N]) for weight width w used with
-    activation width a (quantizers.py:83-94)."""
+    activation width a (quantizers.py:83-94). gpu_division: divide by the
+    constants 7 and 127 as torch does on a GPU (see _div_const); the
+    group-64 backend keeps the IEEE quotient, the tokenwise modules follow
+    the device of the layer they are built from."""
     if w == 2:
         return symmetric_int2_quantize(weight, clip_ratios=clip_ratios)
     if w == 4:
-        return symmetric_int4_quantize(weight, clip_ratios=clip_ratios)
+        return symmetric_int4_quantize(weight, clip_ratios=clip_ratios, gpu_division=gpu_division)
     if a == 4:
-        q4, s4 = symmetric_int4_quantize(weight, clip_ratios=clip_ratios)
+        q4, s4 = symmetric_int4_quantize(weight, clip_ratios=clip_ratios, gpu_division=gpu_division)
         _, nested = signed_r4_refine(weight, q4, s4)
         return nested, s4 / 16.0
     value = _fp32_cpu(weight)
-    scale = value.abs().amax(dim=1).clamp_min(1e-8) / 127.0
+    scale = _div_const(value.abs().amax(dim=1).clamp_min(1e-8), 127.0, gpu_division)
     codes = _round_clamp(value, scale, -128, 127)
     return codes.to(weight.device), scale.to(weight.device)

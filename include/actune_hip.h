@@ -149,6 +149,72 @@ int actune_num_configs(void);
 int actune_config_valid(int config, int64_t M);
 int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A);
 
+/* ------------------------------------------------------------------------
+ * Tokenwise family: per-row dynamic activation scales, full-K int32
+ * accumulation. Replaces the reference's tokenwise Triton and CUDA kernels
+ * (actune/kernels/w4a8_triton.py, w8a8_triton.py, w2a8_triton.py,
+ * decode_w4a8_triton.py, resident_a8_triton.py, wxa4_native.py and
+ * native_s4_extension_kernel.cu) with one quantizer and one GEMM over the
+ * reference's own weight layouts:
+ *   ACTUNE_TW_KMAJOR_W8  int8 [K, N]                  (w8a8_triton.py:106; W8A4 nested codes, wxa4_native.py:334)
+ *   ACTUNE_TW_KMAJOR_W4  u8 [K/2, N], byte j = codes j | (j + K/2) << 4   (w4a8_triton.py:380-383)
+ *   ACTUNE_TW_KMAJOR_W2  u8 [K/4, N], byte j = codes j + f K/4 at bits 2f (w2a8_triton.py:149-159)
+ *   ACTUNE_TW_ROWS_S4    u8 [N, K/2], consecutive nibbles               (wxa4_native.py:206-211)
+ *   ACTUNE_TW_ROWS_S2    u8 [N, K/4], consecutive 2-bit fields          (wxa4_native.py:212-219)
+ * Activations: ACTUNE_TW_ACT_A8 int8 codes [M, K]; ACTUNE_TW_ACT_A4 packed
+ * [M, K/2] (low nibble = even k). Supported pairs: the three K-major
+ * layouts with A8, and KMAJOR_W8 / ROWS_S4 / ROWS_S2 with A4.
+ * Epilogues (fp32, then rounded to out_dtype):
+ *   ACTUNE_TW_EPI_A8  t = f32(acc) * as[m]; y = bias ? fmaf(t, ws[n], bias[n]) : t * ws[n]
+ *                     (w4a8_triton.py:105-113, decode_w4a8_triton.py:102-110)
+ *   ACTUNE_TW_EPI_A4  q = as[m] * ws[n]; y = bias ? fmaf(f32(acc), q, bias[n]) : f32(acc) * q
+ *                     (native_s4_extension_kernel.cu:224-229)
+ */
+enum {
+  ACTUNE_TW_KMAJOR_W8 = 0, ACTUNE_TW_KMAJOR_W4 = 1, ACTUNE_TW_KMAJOR_W2 = 2,
+  ACTUNE_TW_ROWS_S4 = 3, ACTUNE_TW_ROWS_S2 = 4
+};
+enum { ACTUNE_TW_ACT_A8 = 0, ACTUNE_TW_ACT_A4 = 1 };
+enum { ACTUNE_TW_EPI_A8 = 0, ACTUNE_TW_EPI_A4 = 1 };
+
+/*
+ * Per-row dynamic quantizer. Replaces _quantize_rows_kernel
+ * (actune/kernels/w4a8_triton.py:161-201; the same arithmetic as
+ * _quantize_decode_kernel, decode_w4a8_triton.py:21-28, and
+ * _resident_a8_kernel, resident_a8_triton.py:13-21) for A = 8 and
+ * _quantize_rows_a4_kernel (wxa4_native.py:28-65) for A = 4:
+ *   s = fl(max(max|x|, f32(1e-8)) * fl(1/p)), p = 127 or 7,
+ *   c = clamp(rint(x / s), -p-1, p).
+ * x: [M, K] (K % 8 == 0, 16-byte aligned); codes: int8 [M, K] (A = 8) or
+ * u8 [M, K/2] (A = 4); scales: f32 [M].
+ */
+int actune_tokenwise_quantize(const void* x, int x_dtype, int64_t M, int64_t K, int A, void* codes,
+                              float* scales, void* stream);
+
+/*
+ * Bytes of workspace actune_tokenwise_linear needs for this shape (0 when
+ * it runs without a K split), or -1 for an invalid shape. The workspace
+ * holds per-tile counters, which must be zero before its first use (the
+ * kernel leaves them zero), and the int32 split-K partials.
+ */
+int64_t actune_tokenwise_workspace_bytes(int64_t M, int64_t N, int64_t K, int w_layout, int a_layout);
+
+/*
+ * Tokenwise packed linear: out[m, n] = epilogue(sum_k a[m, k] w[n, k]) with
+ * the exact int32 sum. Replaces _w4a8_gemm_kernel (w4a8_triton.py:57-114),
+ * _w8a8_gemm_kernel (w8a8_triton.py:21-77), _w2a8_gemm_kernel
+ * (w2a8_triton.py:24-112), the split-K decode pair _decode_partial_kernel +
+ * _decode_reduce_kernel (decode_w4a8_triton.py:31-149) and the native
+ * linear op (native_s4_extension_kernel.cu:483-573). a_scales: [M];
+ * w_scale: [N]; bias: [N] or NULL; out: [M, N]. workspace: 256-byte aligned,
+ * at least actune_tokenwise_workspace_bytes(); calls sharing one workspace
+ * must not overlap in time. Results do not depend on the split.
+ */
+int actune_tokenwise_linear(const void* a, int a_layout, const float* a_scales, const void* w, int w_layout,
+                            const float* w_scale, const void* bias, int bias_dtype, void* out, int out_dtype,
+                            int64_t M, int64_t N, int64_t K, int epilogue, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
 /*
  * Host-only check of the operand element orders the kernels rely on
  * (sub-byte unpack and cross-width reorder for every (W, A) pair). Returns 0

@@ -115,3 +115,31 @@ def test_install_refuses_after_reference_import(tmp_path):
     res = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
     assert res.returncode == 0, res.stderr[-3000:]
     assert "REFUSED" in res.stdout and "actune.precision" in res.stdout
+
+
+def test_alias_serves_tokenwise_modules(tmp_path):
+    """The tokenwise family's five reference module paths resolve to the one
+    tokenwise module of this package after install()."""
+    for rel, text in STANDIN.items():
+        path = tmp_path / rel
+        path.parent.mkdir(parents=True, exist_ok=True)
+        path.write_text(text)
+    code = textwrap.dedent("""
+        import actune_amd.dropin
+        actune_amd.dropin.install()
+        import actune
+        from actune.kernels.w4a8_triton import W4A8TritonLinear, shared_a8_cache_scope
+        from actune.kernels.w8a8_triton import W8A8TritonLinear
+        from actune.kernels.w2a8_triton import W2A8TritonLinear
+        from actune.kernels.wxa4_native import W4A4NativeLinear, W2A4NativeLinear, W8A4NativeLinear
+        from actune.kernels.decode_w4a8_triton import decode_optimization_scope, DecodeGraphPlan
+        from actune.kernels.runtime_options import runtime_optimization_scope
+        import actune_amd.kernels.tokenwise as T
+        assert W4A8TritonLinear is T.W4A8TritonLinear and W8A4NativeLinear is T.W8A4NativeLinear
+        assert decode_optimization_scope is T.decode_optimization_scope
+        print("TOKENWISE OK")
+    """)
+    env = {"PYTHONPATH": f"{tmp_path}:{ROOT}", "PATH": "/usr/bin:/bin"}
+    res = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stderr[-3000:]
+    assert "TOKENWISE OK" in res.stdout

@@ -265,9 +265,22 @@ def test_graph_replay_limit_falls_back_to_eager():
     assert not torch.equal(outs["q00"], outs["q11"])  # the profiles really differ
 
 
-def test_graph_replay_rejects_shared_a8():
-    with pytest.raises(NotImplementedError):
-        GraphReplay(lambda x: x, {}, shared_a8=True)
+def test_graph_replay_shared_a8_scope():
+    """shared_a8=True binds the tokenwise shared-activation cache to each call
+    (graph.py:18-42): inside the function the cache scope is enabled, and
+    the replayed output of tokenwise siblings equals eager."""
+    from actune_amd.kernels import tokenwise as T
+    seen = []
+
+    def fn(x):
+        seen.append(T._SHARED_A8_STATE.get().enabled)
+        return x * 2
+
+    for flag in (False, True):
+        seen.clear()
+        with GraphReplay(fn, {}, shared_a8=flag).scope():
+            fn(torch.ones(2))
+        assert seen == [flag]
 
 
 def test_channel_scaled_bank_matches_eager_under_replay():

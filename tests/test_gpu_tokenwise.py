@@ -1,0 +1,209 @@
+"""GPU parity of the tokenwise family against the CPU oracle, through the
+C ABI (actune_tokenwise_quantize / actune_tokenwise_linear) and the modules.
+
+Bar: per-row activation codes and scales bit-exact; outputs bit-exact
+against oracle/tokenwise_oracle.c (exact int32 accumulation, then the
+family's fixed fp32 epilogue) for every layout pair, row counts from 1 to
+200, ragged N tiles, K splits and biases; the oracle's torch-GPU division
+semantics pinned against torch on the GPU itself.
+"""
+import numpy as np
+import pytest
+import torch
+
+from actune_amd import _native
+from actune_amd.kernels import tokenwise as T
+from oracle import oracle as O
+from tests.helpers import bits, dtype_name, seeded_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+# (module class, weight bits, activation bits, epilogue mode)
+FAMILY = [(T.W4A8TritonLinear, 4, 8, 0), (T.W8A8TritonLinear, 8, 8, 0), (T.W2A8TritonLinear, 2, 8, 0),
+          (T.W4A4NativeLinear, 4, 4, 1), (T.W2A4NativeLinear, 2, 4, 1), (T.W8A4NativeLinear, 8, 4, 0)]
+
+
+# ---------------------------------------------------------------- quantizer
+@pytest.mark.parametrize("A", [8, 4])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("shape", [(1, 64), (7, 4096), (33, 11008), (3, 16384), (2, 96)])
+def test_row_quantizer_bit_exact(A, dtype, shape):
+    m, k = shape
+    x, _, _ = seeded_inputs(m, k, 1, seed=m + k + A, dtype=dtype)
+    if m > 1:
+        x[1] = 0  # an all-zero row: the 1e-8 floor
+    codes, scales = _native.tokenwise_quantize(x.to(DEV), A)
+    want_c, want_s = O.tw_quantize_rows(bits(x), A, dtype_name(dtype))
+    np.testing.assert_array_equal(scales.cpu().numpy(), want_s)
+    got = codes.cpu().numpy()
+    if A == 4:
+        np.testing.assert_array_equal(got, O.pack_rows(want_c, 4))
+    else:
+        np.testing.assert_array_equal(got, want_c)
+
+
+def test_row_quantizer_equals_torch_gpu_eager_formula():
+    """The reference's unfused path (w4a8_triton.py:400-401) run by torch on
+    the GPU: amax.clamp_min(1e-8) / 127.0 (a reciprocal multiply there) and
+    (x / scale).round().clamp(). Pins the oracle's reciprocal semantics on
+    the hardware the product runs on."""
+    x, _, _ = seeded_inputs(64, 4096, 1, seed=11)
+    xd = x.to(DEV)
+    scale = xd.float().abs().amax(dim=1).clamp_min(1e-8) / 127.0
+    act = (xd.float() / scale[:, None]).round().clamp(-128, 127).to(torch.int8)
+    codes, scales = _native.tokenwise_quantize(xd, 8)
+    assert torch.equal(scales, scale) and torch.equal(codes, act)
+    want_c, want_s = O.tw_quantize_rows(bits(x), 8)
+    np.testing.assert_array_equal(scale.cpu().numpy(), want_s)
+    scale4 = xd.float().abs().amax(dim=1).clamp_min(1e-8) / 7.0
+    np.testing.assert_array_equal(scale4.cpu().numpy(), O.tw_quantize_rows(bits(x), 4)[1])
+
+
+def test_weight_codes_on_gpu_follow_torch_gpu():
+    """A module built from a GPU-resident layer has the scales torch computes
+    there (w4a8_triton.py:370-371: amax.clamp_min(1e-8) / 7.0 on the GPU)."""
+    torch.manual_seed(3)
+    lin = torch.nn.Linear(512, 256, bias=False, dtype=torch.bfloat16, device=DEV)
+    w = lin.weight.detach().float()
+    s4 = w.abs().amax(dim=1).clamp_min(1e-8) / 7.0
+    q4 = (w / s4[:, None]).round().clamp(-8, 7).to(torch.int8)
+    mod = T.W4A8TritonLinear(lin)
+    assert torch.equal(mod.weight_scale, s4)
+    half = 256
+    packed = ((q4[:, :half].to(torch.int16) & 15) | ((q4[:, half:].to(torch.int16) & 15) << 4)).to(torch.uint8)
+    assert torch.equal(mod.packed_weight, packed.t().contiguous())
+    s8 = w.abs().amax(dim=1).clamp_min(1e-8) / 127.0
+    assert torch.equal(T.W8A8TritonLinear(lin).weight_scale, s8)
+
+
+# ---------------------------------------------------------------- modules vs oracle
+def _oracle_out(x, lin, W, A, mode, dtype):
+    codes, scale = O.weight_codes(lin.weight.detach().float().cpu().numpy(), W, A, gpu_division=True)
+    a_codes, a_scales = O.tw_quantize_rows(bits(x), A, dtype_name(dtype))
+    acc = O.tw_dots(a_codes, codes)
+    bias = None if lin.bias is None else lin.bias.detach().float().cpu().numpy()
+    return O.round_out(O.tw_epilogue(acc, a_scales, scale, bias, mode), dtype_name(dtype))
+
+
+@pytest.mark.parametrize("cls,W,A,mode", FAMILY)
+@pytest.mark.parametrize("m,k,n", [(1, 256, 48), (3, 512, 80), (16, 1024, 128), (17, 384, 16),
+                                   (40, 256, 96), (130, 512, 144), (200, 128, 32), (1, 4096, 256)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_modules_bit_exact(cls, W, A, mode, m, k, n, bias):
+    if k % (128 if cls in (T.W8A8TritonLinear, T.W2A8TritonLinear, T.W8A4NativeLinear) else 64):
+        pytest.skip("in_features not allowed for this module")
+    torch.manual_seed(m + k + n)
+    lin = torch.nn.Linear(k, n, bias=bias, dtype=torch.bfloat16, device=DEV)
+    x, _, _ = seeded_inputs(m, k, 1, seed=m * 3 + k)
+    mod = cls(lin)
+    with torch.inference_mode():
+        out = mod(x.to(DEV))
+    torch.cuda.synchronize()
+    want = _oracle_out(x, lin, W, A, mode, torch.bfloat16)
+    np.testing.assert_array_equal(bits(out), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_output_dtypes(dtype):
+    torch.manual_seed(1)
+    lin = torch.nn.Linear(256, 64, bias=True, dtype=dtype, device=DEV)
+    x, _, _ = seeded_inputs(5, 256, 1, seed=2, dtype=dtype)
+    for cls, W, A, mode in FAMILY:
+        if cls in (T.W8A8TritonLinear, T.W2A8TritonLinear, T.W8A4NativeLinear) and 256 % 128:
+            continue
+        out = cls(lin)(x.to(DEV))
+        np.testing.assert_array_equal(bits(out), _oracle_out(x, lin, W, A, mode, dtype), err_msg=cls.__name__)
+
+
+def test_w4a8_ragged_k_tail():
+    """in_features = 96 (divisible by 32, not 64): the last K-step of the
+    nibble-pair layout is half empty."""
+    torch.manual_seed(4)
+    lin = torch.nn.Linear(96, 32, bias=True, dtype=torch.bfloat16, device=DEV)
+    for m in (1, 3, 40):
+        x, _, _ = seeded_inputs(m, 96, 1, seed=m)
+        out = T.W4A8TritonLinear(lin)(x.to(DEV))
+        np.testing.assert_array_equal(bits(out), _oracle_out(x, lin, 4, 8, 0, torch.bfloat16))
+
+
+# ---------------------------------------------------------------- split-K and decode
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (1, 11008, 4096), (1, 4096, 11008), (8, 4096, 4096),
+                                   (2, 256, 2048), (64, 512, 4096)])
+def test_split_k_full_size_sampled(m, n, k):
+    """Llama-2-7B / Gemma shapes through the C ABI with every layout pair;
+    the K split the library picks is exact (checked on 64 sampled columns)."""
+    x, w, _ = seeded_inputs(m, k, n, seed=m + n + k)
+    xd = x.to(DEV)
+    cols = np.sort(np.random.default_rng(n).choice(n, size=64, replace=False))
+    for W, A, wl, mode in ((4, 8, _native.TW_KMAJOR_W4, 0), (8, 8, _native.TW_KMAJOR_W8, 0),
+                           (2, 8, _native.TW_KMAJOR_W2, 0), (4, 4, _native.TW_ROWS_S4, 1),
+                           (2, 4, _native.TW_ROWS_S2, 1), (8, 4, _native.TW_KMAJOR_W8, 0)):
+        codes, scale = O.weight_codes(w.float().numpy(), W, A, gpu_division=True)
+        packed = O.pack_kmajor(codes, W) if wl <= _native.TW_KMAJOR_W2 else O.pack_rows(codes, W)
+        a_layout = _native.TW_ACT_A8 if A == 8 else _native.TW_ACT_A4
+        act, s = _native.tokenwise_quantize(xd, A)
+        need = _native.tokenwise_workspace_bytes(m, n, k, wl, a_layout)
+        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=DEV)
+        out = torch.empty(m, n, device=DEV, dtype=torch.bfloat16)
+        for _ in range(2):  # the second call reuses the counters the first left at zero
+            _native.tokenwise_linear(act, a_layout, s, torch.from_numpy(packed).to(DEV), wl,
+                                     torch.from_numpy(scale).to(DEV), None, n, k, mode, out,
+                                     workspace=ws if need else None)
+        a_codes, a_scales = O.tw_quantize_rows(bits(x), A)
+        acc = O.tw_dots(a_codes, codes[cols])
+        want = O.round_out(O.tw_epilogue(acc, a_scales, scale[cols], None, mode), "bf16")
+        np.testing.assert_array_equal(bits(out)[:, cols], want, err_msg=f"W{W}A{A}")
+        if need:
+            assert not ws[:256].any()  # counters back at zero
+
+
+def test_w4a8_decode_graph_plan_and_counters():
+    """M = 1 bf16: the module replays its DecodeGraphPlan (quantizer + split-K
+    GEMM in one hipGraph); outputs equal the direct path and the oracle, and
+    the decode counters advance as the reference's do."""
+    torch.manual_seed(6)
+    lin = torch.nn.Linear(4096, 4096, bias=False, dtype=torch.bfloat16, device=DEV)
+    mod = T.W4A8TritonLinear(lin)
+    x, _, _ = seeded_inputs(1, 4096, 1, seed=6)
+    xd = x.to(DEV)
+    with T.decode_optimization_scope() as stats:
+        a = mod(xd)
+        b = mod(xd[None])  # [1, 1, K] takes the same plan
+    assert stats.graph_replays == 2 and stats.split_k_calls == 2
+    assert T.decode_workspace_summary(mod)["decode_graph_plan_count"] == 1
+    with T.decode_optimization_scope(enabled=False):
+        direct = mod(xd)
+    assert torch.equal(a, direct) and torch.equal(b.reshape(1, -1), direct)
+    np.testing.assert_array_equal(bits(a), _oracle_out(x, lin, 4, 8, 0, torch.bfloat16))
+
+
+def test_shared_a8_cache_reuses_one_quantization():
+    """q/k/v siblings on the same input quantize once inside a scope
+    (w4a8_triton.py:270-325), and the outputs are unchanged."""
+    torch.manual_seed(7)
+    mods = [T.W4A8TritonLinear(torch.nn.Linear(512, n, bias=False, dtype=torch.bfloat16, device=DEV))
+            for n in (512, 128, 128)] + [T.W8A8TritonLinear(torch.nn.Linear(512, 64, bias=False,
+                                                                              dtype=torch.bfloat16, device=DEV))]
+    x = torch.randn(9, 512, device=DEV).to(torch.bfloat16)
+    alone = [m(x) for m in mods]
+    with T.shared_a8_cache_scope() as state:
+        shared = [m(x) for m in mods]
+    assert state.misses == 1 and state.hits == 3
+    assert all(torch.equal(a, b) for a, b in zip(alone, shared))
+
+
+def test_launch_decode_into_caller_buffers():
+    """launch_decode with a torch.empty partial buffer (its counters are
+    cleared by the call), as benchmarks use it (decode_w4a8_triton.py:113-149)."""
+    torch.manual_seed(8)
+    n, k = 4096, 4096
+    mod = T.W4A8TritonLinear(torch.nn.Linear(k, n, bias=True, dtype=torch.bfloat16, device=DEV))
+    x = torch.randn(1, k, device=DEV).to(torch.bfloat16)
+    act, s = _native.tokenwise_quantize(x, 8)
+    out = torch.empty(1, n, device=DEV, dtype=torch.bfloat16)
+    partial = torch.full((32, n), 7, dtype=torch.int32, device=DEV)
+    T.launch_decode(act, mod.packed_weight, None, s, mod.weight_scale, mod.bias, out, partial)
+    with T.decode_optimization_scope(enabled=False):
+        want = mod(x)
+    assert torch.equal(out, want)
