@@ -107,10 +107,29 @@ struct TwArgs {
   const float* ws;      // [N]
   const void* bias;     // [N] or nullptr
   void* out;            // [M, N]
-  int32_t* partial;     // [S, M, N] int32 (S > 1)
-  uint32_t* counters;   // [tiles_m * tiles_n] (S > 1), zero between launches
+  int32_t* partial;     // [S, M, N] int32 raw (shifted) partial sums (S > 1)
   int M, N, K, bias_dt, out_dt, splits, steps;
 };
+
+// y for output (m, n) from the true int32 accumulator, in the family's
+// fixed fp32 sequence, stored in out_dt.
+template <int EPI>
+__device__ __forceinline__ void store_result(const TwArgs& a, int m, int n, int32_t acc) {
+  const float x = (float)acc;
+  const float as = a.as[m], ws = a.ws[n];
+  float y;
+  if constexpr (EPI == ACTUNE_TW_EPI_A8) {
+    const float t = x * as;
+    y = a.bias ? __builtin_fmaf(t, ws, load_bias(a.bias, a.bias_dt, n)) : t * ws;
+  } else {
+    const float q = as * ws;
+    y = a.bias ? __builtin_fmaf(x, q, load_bias(a.bias, a.bias_dt, n)) : x * q;
+  }
+  const size_t o = (size_t)m * a.N + n;
+  if (a.out_dt == kBF16) store_out<kBF16>(a.out, o, y);
+  else if (a.out_dt == kF16) store_out<kF16>(a.out, o, y);
+  else store_out<kF32>(a.out, o, y);
+}
 
 __device__ __forceinline__ v2u tr8(const uint8_t* p) {
   typedef int v2i_t __attribute__((ext_vector_type(2)));
@@ -137,8 +156,14 @@ constexpr int align_of_stride(int s) { return s % 16 == 0 ? 16 : (s % 8 == 0 ? 8
 
 // WM waves along M (1 or 2), the rest along N; each wave owns MT x NT
 // 16x16 output tiles. Workgroup tile: TM = 16 MT WM rows, TN = 16 NT (4/WM)
-// columns. Grid: x = column tiles, y = row tiles, z = K splits.
-template <int WL, int AL, int EPI, int WM, int MT, int NT>
+// columns. Grid: x = column tiles, y = row tiles, z = K splits (each split
+// writes its int32 partial sums; tw_reduce adds them and finishes).
+// K-steps move in batches of NB: a batch's loads are all issued together
+// (registers), staged into NB LDS buffers and computed after one barrier.
+// ONE (small M): a workgroup's K-range is a single batch (the host keeps it
+// at most NB steps), so every load is in flight at once. Otherwise two LDS
+// halves alternate: batch b + 1 loads while batch b computes.
+template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, bool ONE>
 __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   using T = WTraits<WL>;
   constexpr int WN = 4 / WM;
@@ -150,8 +175,9 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   constexpr int WCH = WROWS * WRB / 16, ACH = TM * ARB / 16;       // 16-byte chunks per step
   constexpr int NWC = (WCH + kThreads - 1) / kThreads, NAC = (ACH + kThreads - 1) / kThreads;
   constexpr int SHIFT = T::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0);
-  __shared__ __align__(16) uint8_t smem[2 * (WBUF + ABUF)];
-  __shared__ int s_last;
+  constexpr int NBUF = ONE ? NB : 2 * NB;
+  static_assert(NBUF * (WBUF + ABUF) <= 64 * 1024, "LDS tile buffers exceed 64 KiB");
+  __shared__ __align__(16) uint8_t smem[NBUF * (WBUF + ABUF)];
 
   const int M = args.M, N = args.N, K = args.K;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -171,59 +197,63 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   const Rsrc wr = make_rsrc(args.w, wbytes);
   const Rsrc ar = make_rsrc(args.a, (uint32_t)M * arow);
 
-  // global byte offset of weight chunk c of step g (kOff: nothing to load)
-  auto w_off = [&](int g, int c) -> uint32_t {
-    if (c >= WCH) return kOff;
-    const int row = c / (WRB / 16), cb = c % (WRB / 16);
+  // Per-thread base offsets of its weight / activation chunks (step 0) and
+  // the per-step byte strides, all 32-bit: a step's loads are then one add
+  // each, in straight-line code. Chunks past the tile or the operand use
+  // kOff (the load returns zeros and moves no data).
+  uint32_t wbase[NWC], abase[NAC];
+#pragma unroll
+  for (int i = 0; i < NWC; ++i) {
+    const int c = tid + i * kThreads, row = c / (WRB / 16), cb = c % (WRB / 16);
+    bool live = c < WCH;
     if constexpr (T::KM) {
-      const int col = n0 + 16 * cb;
-      const long r = (long)g * WROWS + row;   // buffer row (k, or j of K/2 / K/4)
-      if (col >= N) return kOff;
-      return (uint32_t)(r * N + col);
+      live = live && n0 + 16 * cb < N;
+      wbase[i] = live ? (uint32_t)row * (uint32_t)N + (uint32_t)(n0 + 16 * cb) : kOff;
     } else {
-      const int n = n0 + row;
-      if (n >= N) return kOff;
-      return (uint32_t)((long)n * (WL == ACTUNE_TW_ROWS_S4 ? K / 2 : K / 4) + (long)g * WRB + 16 * cb);
+      live = live && n0 + row < N;
+      wbase[i] = live ? (uint32_t)(n0 + row) * (uint32_t)(WL == ACTUNE_TW_ROWS_S4 ? K / 2 : K / 4) + (uint32_t)(16 * cb)
+                      : kOff;
     }
-  };
-  // global byte offset of activation chunk c of step g
-  auto a_off = [&](int g, int c) -> uint32_t {
-    if (c >= ACH) return kOff;
-    const int row = c / (ARB / 16), cb = c % (ARB / 16);
-    const int m = m0 + row;
-    if (m >= M) return kOff;
-    long k;
-    if constexpr (AL == ACTUNE_TW_ACT_A4) {
-      k = (long)g * 32 + 16 * cb;                            // bytes of the packed row
-    } else if constexpr (WL == ACTUNE_TW_KMAJOR_W4) {
-      k = (long)(cb >> 1) * (K / 2) + (long)g * 32 + 16 * (cb & 1);
-    } else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) {
-      k = (long)(cb >> 1) * (K / 4) + (long)g * 32 + 16 * (cb & 1);
-    } else {
-      k = (long)g * 64 + 16 * cb;
-    }
-    return (uint32_t)((long)m * arow + k);
-  };
+  }
+  const uint32_t wstep = T::KM ? (uint32_t)WROWS * (uint32_t)N : (uint32_t)WRB;
+#pragma unroll
+  for (int i = 0; i < NAC; ++i) {
+    const int c = tid + i * kThreads, row = c / (ARB / 16), cb = c % (ARB / 16);
+    const bool live = c < ACH && m0 + row < M;
+    uint32_t k;
+    if constexpr (AL == ACTUNE_TW_ACT_A4) k = 16 * cb;                                   // packed row bytes
+    else if constexpr (WL == ACTUNE_TW_KMAJOR_W4) k = (uint32_t)(cb >> 1) * (K / 2) + 16 * (cb & 1);
+    else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) k = (uint32_t)(cb >> 1) * (K / 4) + 16 * (cb & 1);
+    else k = 16 * cb;
+    abase[i] = live ? (uint32_t)(m0 + row) * arow + k : kOff;
+  }
+  constexpr uint32_t astep = (AL == ACTUNE_TW_ACT_A4 || WL == ACTUNE_TW_KMAJOR_W4 || WL == ACTUNE_TW_KMAJOR_W2) ? 32 : 64;
 
-  v4u wreg[NWC], areg[NAC];
-  auto issue = [&](int g) {
+  // loads of step g; a step outside [g0, g1) is switched off through the
+  // scalar offset (reads zeros)
+  auto issue = [&](int g, v4u (&wreg)[NWC], v4u (&areg)[NAC]) {
+    const uint32_t soff = g < g1 ? 0u : kOff;
 #pragma unroll
-    for (int i = 0; i < NWC; ++i) wreg[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, w_off(g, tid + i * kThreads), 0, 0);
+    for (int i = 0; i < NWC; ++i)
+      wreg[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, wbase[i] == kOff ? kOff : wbase[i] + (uint32_t)g * wstep, soff, 0);
 #pragma unroll
-    for (int i = 0; i < NAC; ++i) areg[i] = __builtin_amdgcn_raw_buffer_load_b128(ar, a_off(g, tid + i * kThreads), 0, 0);
+    for (int i = 0; i < NAC; ++i)
+      areg[i] = __builtin_amdgcn_raw_buffer_load_b128(ar, abase[i] == kOff ? kOff : abase[i] + (uint32_t)g * astep, soff, 0);
   };
-  auto stage = [&](int buf) {
+  auto stage = [&](int buf, const v4u (&wreg)[NWC], const v4u (&areg)[NAC]) {
     uint8_t* wt = smem + buf * (WBUF + ABUF);
     uint8_t* at = wt + WBUF;
 #pragma unroll
     for (int i = 0; i < NWC; ++i) {
       const int c = tid + i * kThreads;
-      if (c < WCH) lds_store16<align_of_stride(WSTR)>(wt + (c / (WRB / 16)) * WSTR + 16 * (c % (WRB / 16)), wreg[i]);
+      if (WCH % kThreads == 0 || c < WCH)
+        lds_store16<align_of_stride(WSTR)>(wt + (c / (WRB / 16)) * WSTR + 16 * (c % (WRB / 16)), wreg[i]);
     }
 #pragma unroll
     for (int i = 0; i < NAC; ++i) {
       const int c = tid + i * kThreads;
-      if (c < ACH) lds_store16<align_of_stride(ASTR)>(at + (c / (ARB / 16)) * ASTR + 16 * (c % (ARB / 16)), areg[i]);
+      if (ACH % kThreads == 0 || c < ACH)
+        lds_store16<align_of_stride(ASTR)>(at + (c / (ARB / 16)) * ASTR + 16 * (c % (ARB / 16)), areg[i]);
     }
   };
 
@@ -297,23 +327,49 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
     }
   };
 
-  // two-buffer pipeline: step g+1's loads are in flight while step g computes
-  if (g0 < g1) {
-    issue(g0);
-    stage(0);
+  // (steps past g1 load zeros and add nothing, so batches are straight-line
+  // code with no bounds tests)
+  auto issue_batch = [&](int g, v4u (&wreg)[NB][NWC], v4u (&areg)[NB][NAC]) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) issue(g + i, wreg[i], areg[i]);
+  };
+  auto stage_batch = [&](int half, const v4u (&wreg)[NB][NWC], const v4u (&areg)[NB][NAC]) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) stage(half * NB + i, wreg[i], areg[i]);
+  };
+  auto compute_batch = [&](int half) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) compute(half * NB + i);
+  };
+  if constexpr (ONE) {
+    v4u wreg[NB][NWC], areg[NB][NAC];
+    issue_batch(g0, wreg, areg);
+    stage_batch(0, wreg, areg);
     __syncthreads();
-    for (int g = g0; g < g1; ++g) {
-      const int buf = (g - g0) & 1;
-      if (g + 1 < g1) issue(g + 1);
-      compute(buf);
-      if (g + 1 < g1) stage(buf ^ 1);
+    compute_batch(0);
+  } else if (g0 < g1) {
+    v4u w0[NB][NWC], a0[NB][NAC], w1[NB][NWC], a1[NB][NAC];
+    issue_batch(g0, w0, a0);
+    stage_batch(0, w0, a0);
+    __syncthreads();
+    for (int g = g0; g < g1; g += 2 * NB) {
+      const bool more1 = g + NB < g1, more2 = g + 2 * NB < g1;
+      if (more1) issue_batch(g + NB, w1, a1);
+      compute_batch(0);
+      if (more1) stage_batch(1, w1, a1);
+      __syncthreads();
+      if (!more1) break;
+      if (more2) issue_batch(g + 2 * NB, w0, a0);
+      compute_batch(1);
+      if (more2) stage_batch(0, w0, a0);
       __syncthreads();
     }
   }
 
-  // ---------------------------------------------------------------- split-K
   const int row_base = m0 + wm * 16 * MT + 4 * kb, col_base = n0 + wn * 16 * NT + r16;
   if (S > 1) {
+    // raw partial sums of this split; tw_reduce adds the splits (integer
+    // addition: any order gives the same sum) and finishes
     int32_t* part = args.partial + (size_t)z * M * N;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -324,66 +380,52 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
           const int m = row_base + mt * 16 + i, n = col_base + nt * 16;
           if (m < M && n < N) part[(size_t)m * N + n] = acc[mt][nt][i];
         }
-    __threadfence();
-    __syncthreads();
-    const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x;
-    if (tid == 0) s_last = atomicAdd(&args.counters[tile], 1u) == (uint32_t)(S - 1);
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = row_base + mt * 16 + i, n = col_base + nt * 16;
-          int32_t sum = 0;
-          if (m < M && n < N)
-            for (int s = 0; s < S; ++s) sum += __builtin_nontemporal_load(args.partial + ((size_t)s * M + m) * N + n);
-          acc[mt][nt][i] = sum;
-        }
-    if (tid == 0) args.counters[tile] = 0u;  // ready for the next launch
+    return;
   }
-
-  // ---------------------------------------------------------------- epilogue
-  const bool has_bias = args.bias != nullptr;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int n = col_base + nt * 16;
     if (n >= N) continue;
-    const float ws = args.ws[n];
-    const float b = has_bias ? load_bias(args.bias, args.bias_dt, n) : 0.0f;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = row_base + mt * 16 + i;
-        if (m >= M) continue;
-        const float a = (float)(acc[mt][nt][i] >> SHIFT);
-        const float as = args.as[m];
-        float y;
-        if constexpr (EPI == ACTUNE_TW_EPI_A8) {
-          const float t = a * as;
-          y = has_bias ? __builtin_fmaf(t, ws, b) : t * ws;
-        } else {
-          const float q = as * ws;
-          y = has_bias ? __builtin_fmaf(a, q, b) : a * q;
-        }
-        const size_t o = (size_t)m * N + n;
-        if (args.out_dt == kBF16) store_out<kBF16>(args.out, o, y);
-        else if (args.out_dt == kF16) store_out<kF16>(args.out, o, y);
-        else store_out<kF32>(args.out, o, y);
+        if (m < M) store_result<EPI>(args, m, n, acc[mt][nt][i] >> SHIFT);
       }
   }
+}
+
+// Adds the K splits' partial sums of one output each and finishes it.
+template <int EPI>
+__global__ __launch_bounds__(kThreads) void tw_reduce(const TwArgs args, int shift) {
+  const long total = (long)args.M * args.N;
+  const long idx = (long)blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= total) return;
+  // all splits' loads in flight at once (splits past S read zeros), one
+  // round trip for up to 32 splits
+  const Rsrc pr = make_rsrc(args.partial, (uint32_t)((size_t)args.splits * total * 4));
+  int32_t sum = 0;
+  for (int s0 = 0; s0 < args.splits; s0 += 32) {
+    int32_t v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+      v[j] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(
+          pr, s0 + j < args.splits ? (uint32_t)(((size_t)(s0 + j) * total + idx) * 4) : kOff, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) sum += v[j];
+  }
+  store_result<EPI>(args, (int)(idx / args.N), (int)(idx % args.N), sum >> shift);
 }
 
 // ---------------------------------------------------------------- quantizer
 // One workgroup per row: amax over the row (wave shuffles, then LDS across
 // the 4 waves), s = fl(max(amax, f32(1e-8)) * fl(1/p)), codes rint(v / s)
 // (IEEE division) clamped to [-p-1, p]. A8 writes int8 codes, A4 packs two
-// codes per byte (low nibble = even k). Each lane handles 8 consecutive
-// elements per pass; the second pass re-reads the row (L2-resident).
+// codes per byte (low nibble = even k). Each lane owns 8 consecutive
+// elements per 2048-element pass and keeps up to RC passes in registers
+// between the amax and the code pass (K <= 2048 RC); longer rows re-read
+// the rest (L2-resident).
 template <int A, int DT>
 __global__ __launch_bounds__(kThreads) void tw_quantize_kernel(const void* __restrict__ x, int K,
                                                                uint8_t* __restrict__ codes,
@@ -391,15 +433,27 @@ __global__ __launch_bounds__(kThreads) void tw_quantize_kernel(const void* __res
   constexpr int P = (1 << (A - 1)) - 1;
   constexpr float R = 1.0f / (float)P;
   constexpr int ESZ = DT == kF32 ? 4 : 2;
+  constexpr int RC = 8, PASS = kThreads * 8;
   __shared__ float red[kThreads / 64];
   const int m = blockIdx.x, tid = threadIdx.x;
   const char* row = static_cast<const char*>(x) + (size_t)m * K * ESZ;
+  const Rsrc xr = make_rsrc(row, (uint32_t)K * ESZ);
+  float v[RC][8];
   float amax = 0.0f;
-  for (int e = tid * 8; e < K; e += kThreads * 8) {
-    float v[8];
-    load8<DT>(row, e, v);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  for (int p = 0; p < RC; ++p) {
+    const int e = p * PASS + tid * 8;
+    buffer_load8<DT>(xr, e < K ? (uint32_t)e * ESZ : kOff, v[p]);
+  }
+#pragma unroll
+  for (int p = 0; p < RC; ++p)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[p][i]));
+  for (int e = RC * PASS + tid * 8; e < K; e += PASS) {
+    float w[8];
+    load8<DT>(row, e, w);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(w[i]));
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
@@ -409,12 +463,10 @@ __global__ __launch_bounds__(kThreads) void tw_quantize_kernel(const void* __res
   for (int w = 0; w < kThreads / 64; ++w) amax = fmaxf(amax, red[w]);
   const float s = fmaxf(amax, 1e-8f) * R;
   if (tid == 0) scales[m] = s;
-  for (int e = tid * 8; e < K; e += kThreads * 8) {
-    float v[8];
-    load8<DT>(row, e, v);
+  auto emit = [&](int e, const float (&vv)[8]) {
     int c[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) c[i] = (int)fminf(fmaxf(rintf(v[i] / s), (float)(-P - 1)), (float)P);
+    for (int i = 0; i < 8; ++i) c[i] = (int)fminf(fmaxf(rintf(vv[i] / s), (float)(-P - 1)), (float)P);
     if constexpr (A == 8) {
       uint32_t lo = 0, hi = 0;
 #pragma unroll
@@ -426,48 +478,77 @@ __global__ __launch_bounds__(kThreads) void tw_quantize_kernel(const void* __res
       for (int i = 0; i < 8; ++i) w |= ((uint32_t)c[i] & 0xfu) << (4 * i);
       *reinterpret_cast<uint32_t*>(codes + (size_t)m * (K / 2) + e / 2) = w;
     }
+  };
+#pragma unroll
+  for (int p = 0; p < RC; ++p) {
+    const int e = p * PASS + tid * 8;
+    if (e < K) emit(e, v[p]);
+  }
+  for (int e = RC * PASS + tid * 8; e < K; e += PASS) {
+    float w[8];
+    load8<DT>(row, e, w);
+    emit(e, w);
   }
 }
 
 // ---------------------------------------------------------------- host side
 struct Geometry {
-  int wm, mt, nt;
+  int wm, mt, nt, ns;
   int tm() const { return 16 * mt * wm; }
   int tn() const { return 16 * nt * (4 / wm); }
 };
 
-// M <= 32: 16-row tiles, 128 columns per workgroup, K split across
-// workgroups until the grid holds about 2 workgroups per CU; above: 128 x
-// 128 tiles (2 x 2 waves of 64 x 64).
-Geometry pick_geometry(int64_t M) { return M <= 32 ? Geometry{1, 1, 2} : Geometry{2, 4, 4}; }
-
 int kps_of(int wl) { return wl == ACTUNE_TW_KMAJOR_W2 ? 128 : 64; }
+int64_t steps_of(int64_t K, int wl) { return (K + kps_of(wl) - 1) / kps_of(wl); }
+// K-steps a small-M workgroup loads at entry: the int8 K-major tile is twice
+// the others, so it keeps half as many steps to stay inside the LDS
+int small_ns(int wl) { return wl == ACTUNE_TW_KMAJOR_W8 ? 4 : 8; }
+int64_t tiles_of(int64_t M, int64_t N, const Geometry& g) {
+  return ((N + g.tn() - 1) / g.tn()) * ((M + g.tm() - 1) / g.tm());
+}
 
-// K splits: small-M tiles split until the grid holds about two workgroups
-// per CU (the weight stream is the cost; partials are M x N int32 per
-// split); large-M tiles only below one workgroup per CU, and only while the
-// partials stay small against the operands. Every split keeps >= 2 K-steps.
+// M <= 32: 16-row x 128-column tiles, every K-step of a workgroup loaded at
+// entry (small_ns). Larger M: 64 x 128 tiles (2 x 2 waves of 32 x 64),
+// K-steps in double-buffered batches.
+Geometry pick_geometry(int64_t M, int64_t N, int wl) {
+  (void)N;
+  if (M <= 32) return Geometry{1, 1, 2, small_ns(wl)};
+  return Geometry{2, 2, 4, 0};
+}
+
+// K splits. Small M: enough splits that each workgroup's range fits its
+// entry loads and the grid holds about two workgroups per CU. Large M: a
+// split only for grids below half a workgroup per CU, while the partials
+// (S x M x N int32) stay small against the operands.
 int pick_splits(int64_t M, int64_t N, int64_t K, int wl, const Geometry& g) {
-  const int64_t tiles = ((N + g.tn() - 1) / g.tn()) * ((M + g.tm() - 1) / g.tm());
-  const int64_t steps = (K + kps_of(wl) - 1) / kps_of(wl);
-  const int64_t target = g.wm == 1 ? 512 : 256;
+  const int64_t tiles = tiles_of(M, N, g), steps = steps_of(K, wl);
+  if (g.ns > 0) {
+    int64_t s = std::max((steps + g.ns - 1) / g.ns, (512 + tiles - 1) / tiles);
+    return (int)std::min(s, steps);
+  }
   int64_t s = 1;
-  while (tiles * s < target && s * 4 <= steps && s < 64 && (g.wm == 1 || 2 * s * M * N * 4 <= (int64_t)8 << 20))
-    s *= 2;
+  while (tiles * s < 128 && s * 8 <= steps && 2 * s * M * N * 4 <= ((int64_t)8 << 20)) s *= 2;
   return (int)s;
 }
 
-template <int WL, int AL, int EPI, int WM, int MT, int NT>
+template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, bool ONE>
 void launch_gemm_t(const TwArgs& a, hipStream_t st) {
   constexpr int TM = 16 * MT * WM, TN = 16 * NT * (4 / WM);
   const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM), (unsigned)a.splits);
-  tw_gemm<WL, AL, EPI, WM, MT, NT><<<grid, kThreads, 0, st>>>(a);
+  tw_gemm<WL, AL, EPI, WM, MT, NT, NB, ONE><<<grid, kThreads, 0, st>>>(a);
+  if (a.splits > 1) {
+    const long total = (long)a.M * a.N;
+    constexpr int SHIFT = WTraits<WL>::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0);
+    tw_reduce<EPI><<<(unsigned)((total + kThreads - 1) / kThreads), kThreads, 0, st>>>(a, SHIFT);
+  }
 }
 
 template <int WL, int AL, int EPI>
 void launch_gemm_g(const TwArgs& a, const Geometry& g, hipStream_t st) {
-  if (g.wm == 1) launch_gemm_t<WL, AL, EPI, 1, 1, 2>(a, st);
-  else launch_gemm_t<WL, AL, EPI, 2, 4, 4>(a, st);
+  // large-M batch: two halves of NBL steps stay within 64 KiB of LDS
+  constexpr int NBL = (WL == ACTUNE_TW_KMAJOR_W8 || WL == ACTUNE_TW_KMAJOR_W2) ? 2 : 3;
+  if (g.wm == 1) launch_gemm_t<WL, AL, EPI, 1, 1, 2, (WL == ACTUNE_TW_KMAJOR_W8 ? 4 : 8), true>(a, st);
+  else launch_gemm_t<WL, AL, EPI, 2, 2, 4, NBL, false>(a, st);
 }
 
 // the six (weight layout, activation layout) pairs of the reference family
@@ -492,8 +573,6 @@ void launch_gemm(int wl, int al, int epi, const TwArgs& a, const Geometry& g, hi
   TW_CASE(ACTUNE_TW_ROWS_S2, ACTUNE_TW_ACT_A4)
 #undef TW_CASE
 }
-
-int64_t round256(int64_t v) { return (v + 255) / 256 * 256; }
 
 int fail(const char* msg) {
   set_last_error(msg);
@@ -557,11 +636,9 @@ int actune_tokenwise_quantize(const void* x, int x_dtype, int64_t M, int64_t K, 
 
 int64_t actune_tokenwise_workspace_bytes(int64_t M, int64_t N, int64_t K, int w_layout, int a_layout) {
   if (check_tw_shape(M, N, K, w_layout, a_layout)) return -1;
-  const Geometry g = pick_geometry(M);
+  const Geometry g = pick_geometry(M, N, w_layout);
   const int S = pick_splits(M, N, K, w_layout, g);
-  if (S == 1) return 0;
-  const int64_t tiles = ((N + g.tn() - 1) / g.tn()) * ((M + g.tm() - 1) / g.tm());
-  return round256(tiles * 4) + (int64_t)S * M * N * 4;
+  return S == 1 ? 0 : (int64_t)S * M * N * 4;
 }
 
 int actune_tokenwise_linear(const void* a, int a_layout, const float* a_scales, const void* w, int w_layout,
@@ -579,7 +656,7 @@ int actune_tokenwise_linear(const void* a, int a_layout, const float* a_scales, 
   if (!a || !a_scales || !w || !w_scale || !out) return fail("null pointer");
   if (((uintptr_t)a % 16) || ((uintptr_t)w % 16) || ((uintptr_t)a_scales % 4) || ((uintptr_t)w_scale % 4))
     return fail("misaligned operand (packed data needs 16 B)");
-  const Geometry g = pick_geometry(M);
+  const Geometry g = pick_geometry(M, N, w_layout);
   const int S = pick_splits(M, N, K, w_layout, g);
   TwArgs args{};
   args.a = static_cast<const uint8_t*>(a);
@@ -594,14 +671,13 @@ int actune_tokenwise_linear(const void* a, int a_layout, const float* a_scales, 
   args.bias_dt = bias_dtype;
   args.out_dt = out_dtype;
   args.splits = S;
-  args.steps = (int)((K + kps_of(w_layout) - 1) / kps_of(w_layout));
+  args.steps = (int)steps_of(K, w_layout);
   if (S > 1) {
-    const int64_t need = actune_tokenwise_workspace_bytes(M, N, K, w_layout, a_layout);
-    if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 256))
+    const int64_t need = (int64_t)S * M * N * 4;
+    if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 16))
       return fail("workspace missing, misaligned or smaller than actune_tokenwise_workspace_bytes()");
-    const int64_t tiles = ((N + g.tn() - 1) / g.tn()) * ((M + g.tm() - 1) / g.tm());
-    args.counters = static_cast<uint32_t*>(workspace);
-    args.partial = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + round256(tiles * 4));
+    if (need >= ((int64_t)1 << 31)) return fail("split-K partials too large");
+    args.partial = static_cast<int32_t*>(workspace);
   }
   launch_gemm(w_layout, a_layout, epilogue, args, g, (hipStream_t)stream);
   hipError_t e = hipGetLastError();

@@ -48,14 +48,14 @@ from . import quantizers
 
 
 def _workspace(owner, m, n, k, w_layout, a_layout, device):
-    """The owner's split-K workspace (zeroed once; the kernel leaves its
-    counters zero), grown when a call needs more; None when unsplit."""
+    """The owner's split-K partial-sum workspace, grown when a call needs
+    more; None when the call runs unsplit."""
     need = _native.tokenwise_workspace_bytes(m, n, k, w_layout, a_layout)
     if need == 0:
         return None
     ws = getattr(owner, "_tw_workspace", None)
     if ws is None or ws.numel() < need or ws.device != device:
-        ws = torch.zeros(need, dtype=torch.uint8, device=device)
+        ws = torch.empty(need, dtype=torch.uint8, device=device)
         owner._tw_workspace = ws
     return ws
 
@@ -561,10 +561,10 @@ def _decode_check_residual(residual):
 def launch_decode(activation, packed, residual, activation_scale, weight_scale, bias, output, partial, *,
                   config=None):
     """Launch into caller-owned buffers (decode_w4a8_triton.py:113-149).
-    ``partial`` is the caller's workspace (any dtype, at least the bytes
-    actune_tokenwise_workspace_bytes() asks for); its counter region is
-    cleared here, so buffers from torch.empty work. ``config`` is accepted
-    for signature parity; the split is chosen per shape."""
+    ``partial`` is the caller's split-K workspace (any dtype, at least the
+    bytes actune_tokenwise_workspace_bytes() asks for; nothing in it needs
+    to start at any value). ``config`` is accepted for signature parity; the
+    split is chosen per shape."""
     _decode_check_residual(residual)
     n = packed.shape[1]
     k = packed.shape[0] * 2
@@ -575,7 +575,6 @@ def launch_decode(activation, packed, residual, activation_scale, weight_scale, 
         ws = partial.view(-1).view(torch.uint8)
         if ws.numel() < need:
             raise ValueError(f"partial workspace too small: {need} bytes needed")
-        ws[:need].zero_()  # per-tile counters must start at zero (the kernel leaves them zero again)
     return _native.tokenwise_linear(activation.reshape(m, k), _native.TW_ACT_A8, activation_scale.reshape(-1),
                                     packed, _native.TW_KMAJOR_W4, weight_scale, bias, n, k, _native.TW_EPI_A8,
                                     output.view(m, n), workspace=ws)
@@ -595,8 +594,6 @@ def launch_decode_group(activation, weights, residuals, activation_scale, scales
     if need and ws.numel() < need:
         raise ValueError(f"partial workspace too small: {need} bytes needed")
     for w, s, b, o in zip(weights, scales, biases, outputs):
-        if need:
-            ws[:need].zero_()
         _native.tokenwise_linear(activation.reshape(1, k), _native.TW_ACT_A8, activation_scale.reshape(-1), w,
                                  _native.TW_KMAJOR_W4, s, b, n, k, _native.TW_EPI_A8, o.view(1, n),
                                  workspace=ws if need else None)
@@ -643,7 +640,7 @@ class DecodeGraphPlan:
         self.output = torch.empty((self.groups, self.n), device=dev, dtype=value.dtype)
         self.outputs = tuple(self.output[i:i + 1] for i in range(self.groups))
         need = _native.tokenwise_workspace_bytes(1, self.n, self.k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8)
-        self.partial = torch.zeros(max(need, 256) * self.groups, device=dev, dtype=torch.uint8)
+        self.partial = torch.empty(max(need, 256) * self.groups, device=dev, dtype=torch.uint8)
         self._need = need
         self.graph = torch.cuda.CUDAGraph()
         stream = torch.cuda.Stream(device=dev)

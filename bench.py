@@ -65,6 +65,8 @@ def parse():
     p.add_argument("--only", choices=sorted(ONLY_SHAPES),
                    help="only launch one shape 24 times over distinct weights (for rocprofv3 counter runs)")
     p.add_argument("--config", type=int, default=-1, help="kernel config for --only (default: automatic)")
+    p.add_argument("--tokenwise-only", action="store_true",
+                   help="only run the tokenwise-family section and print it as one JSON line")
     return p.parse_args()
 
 
@@ -355,6 +357,65 @@ def bench_gemma(torch, _native, steps, warmup):
     return out
 
 
+TW_PAIRS = [("W4A8", 4, 8), ("W8A8", 8, 8), ("W2A8", 2, 8), ("W4A4", 4, 4), ("W2A4", 2, 4), ("W8A4", 8, 4)]
+
+
+def bench_tokenwise(torch, _native, steps, warmup):
+    """The tokenwise (per-row) family: per-row quantizer + int8-MFMA GEMM over
+    the reference's weight layouts (K-major nibble pairs / int8 / quarters,
+    row-major S4 / S2). M=1 and M=8 on the Llama-2-7B shapes for W4A8 (the
+    reference's decode use), rotating over >= 256 MB of distinct weights,
+    and M=512 for every pair (the MFMA-bound case: the int32 accumulator
+    needs no per-group rescale). Each launch pair = quantizer + GEMM."""
+    layouts = {"W4A8": _native.TW_KMAJOR_W4, "W8A8": _native.TW_KMAJOR_W8, "W2A8": _native.TW_KMAJOR_W2,
+               "W4A4": _native.TW_ROWS_S4, "W2A4": _native.TW_ROWS_S2, "W8A4": _native.TW_KMAJOR_W8}
+    g = torch.Generator(device="cuda").manual_seed(6)
+    out = {}
+
+    def run(name, W, A, m, n, k, copies):
+        wl = layouts[name]
+        al = _native.TW_ACT_A8 if A == 8 else _native.TW_ACT_A4
+        epi = _native.TW_EPI_A4 if name in ("W4A4", "W2A4") else _native.TW_EPI_A8
+        nbytes = n * k * W // 8
+        ws = [(torch.randint(0, 256, (nbytes,), generator=g, device="cuda", dtype=torch.uint8),
+               torch.rand(n, generator=g, device="cuda") * 0.01 + 0.005) for _ in range(copies)]
+        x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
+        act, sc = _native.tokenwise_quantize(x, A)
+        need = _native.tokenwise_workspace_bytes(m, n, k, wl, al)
+        work = torch.zeros(max(need, 256), dtype=torch.uint8, device="cuda")
+        y = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+
+        def gemm_only():
+            for w, s in ws:
+                _native.tokenwise_linear(act, al, sc, w, wl, s, None, n, k, epi, y, workspace=work if need else None)
+
+        def with_quant():
+            for w, s in ws:
+                _native.tokenwise_quantize(x, A, act, sc)
+                _native.tokenwise_linear(act, al, sc, w, wl, s, None, n, k, epi, y, workspace=work if need else None)
+
+        us = time_launches(torch, gemm_only, steps, warmup) / copies
+        us_q = time_launches(torch, with_quant, steps, warmup) / copies
+        del ws
+        tops = 2 * m * n * k / us / 1e6
+        return dict(us=round(us, 2), us_with_quantizer=round(us_q, 2), weight_GBps=round(nbytes / us / 1e3, 1),
+                    TOPS=round(tops, 1), frac_hbm=round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4),
+                    frac_int8=round(tops / INT8_PEAK_TOPS, 4))
+
+    for m in (1, 8):
+        row = {}
+        for _, n, k in (SHAPES[0], SHAPES[4], SHAPES[6]):
+            copies = max(12, (300 << 20) // (n * k // 2))
+            row[f"{n}x{k}"] = run("W4A8", 4, 8, m, n, k, copies)
+        out[f"W4A8_M={m}"] = row
+    for name, W, A in TW_PAIRS:
+        row = {}
+        for _, n, k in (SHAPES[0], SHAPES[4], SHAPES[6]):
+            row[f"{n}x{k}"] = run(name, W, A, 512, n, k, 4)
+        out[f"{name}_M=512"] = row
+    return out
+
+
 EXPERT = {"q": (1024, 1024), "k": (256, 1024), "v": (256, 1024), "o": (1024, 1024),
           "gate": (4096, 1024), "up": (4096, 1024), "down": (1024, 4096)}
 
@@ -450,6 +511,9 @@ def main():
     if args.only:
         run_only(torch, _native, args.only, args.W, args.A, args.config)
         return 0
+    if args.tokenwise_only:
+        print(json.dumps(dict(tokenwise=bench_tokenwise(torch, _native, args.steps, args.warmup))), flush=True)
+        return 0
 
     W, A = args.W, args.A
     results = {}
@@ -526,6 +590,7 @@ def main():
         line["detail"]["C3_prefill_M512"] = bench_prefill(torch, _native, 10, 3)
         line["detail"]["C4_gemma_W4A4"] = bench_gemma(torch, _native, 20, 5)
         line["detail"]["C5_expert_switching"] = bench_expert(torch, 20)
+        line["detail"]["tokenwise_family"] = bench_tokenwise(torch, _native, 10, 3)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, W, A)
     print(json.dumps(line), flush=True)

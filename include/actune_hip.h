@@ -194,8 +194,9 @@ int actune_tokenwise_quantize(const void* x, int x_dtype, int64_t M, int64_t K, 
 /*
  * Bytes of workspace actune_tokenwise_linear needs for this shape (0 when
  * it runs without a K split), or -1 for an invalid shape. The workspace
- * holds per-tile counters, which must be zero before its first use (the
- * kernel leaves them zero), and the int32 split-K partials.
+ * holds the int32 partial sums of the K splits (no state between calls);
+ * a split call is two launches, the split GEMM and an integer reduce that
+ * finishes the outputs.
  */
 int64_t actune_tokenwise_workspace_bytes(int64_t M, int64_t N, int64_t K, int w_layout, int a_layout);
 
@@ -206,9 +207,10 @@ int64_t actune_tokenwise_workspace_bytes(int64_t M, int64_t N, int64_t K, int w_
  * (w2a8_triton.py:24-112), the split-K decode pair _decode_partial_kernel +
  * _decode_reduce_kernel (decode_w4a8_triton.py:31-149) and the native
  * linear op (native_s4_extension_kernel.cu:483-573). a_scales: [M];
- * w_scale: [N]; bias: [N] or NULL; out: [M, N]. workspace: 256-byte aligned,
- * at least actune_tokenwise_workspace_bytes(); calls sharing one workspace
+ * w_scale: [N]; bias: [N] or NULL; out: [M, N]. workspace: at least
+ * actune_tokenwise_workspace_bytes() bytes; calls sharing one workspace
  * must not overlap in time. Results do not depend on the split.
+ * workspace alignment: 16 bytes.
  */
 int actune_tokenwise_linear(const void* a, int a_layout, const float* a_scales, const void* w, int w_layout,
                             const float* w_scale, const void* bias, int bias_dtype, void* out, int out_dtype,

@@ -144,9 +144,9 @@ def test_split_k_full_size_sampled(m, n, k):
         a_layout = _native.TW_ACT_A8 if A == 8 else _native.TW_ACT_A4
         act, s = _native.tokenwise_quantize(xd, A)
         need = _native.tokenwise_workspace_bytes(m, n, k, wl, a_layout)
-        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=DEV)
+        ws = torch.full((max(need, 1),), 0x5A, dtype=torch.uint8, device=DEV)
         out = torch.empty(m, n, device=DEV, dtype=torch.bfloat16)
-        for _ in range(2):  # the second call reuses the counters the first left at zero
+        for _ in range(2):  # the workspace holds no state between calls
             _native.tokenwise_linear(act, a_layout, s, torch.from_numpy(packed).to(DEV), wl,
                                      torch.from_numpy(scale).to(DEV), None, n, k, mode, out,
                                      workspace=ws if need else None)
@@ -154,8 +154,6 @@ def test_split_k_full_size_sampled(m, n, k):
         acc = O.tw_dots(a_codes, codes[cols])
         want = O.round_out(O.tw_epilogue(acc, a_scales, scale[cols], None, mode), "bf16")
         np.testing.assert_array_equal(bits(out)[:, cols], want, err_msg=f"W{W}A{A}")
-        if need:
-            assert not ws[:256].any()  # counters back at zero
 
 
 def test_w4a8_decode_graph_plan_and_counters():
@@ -194,8 +192,8 @@ def test_shared_a8_cache_reuses_one_quantization():
 
 
 def test_launch_decode_into_caller_buffers():
-    """launch_decode with a torch.empty partial buffer (its counters are
-    cleared by the call), as benchmarks use it (decode_w4a8_triton.py:113-149)."""
+    """launch_decode into caller-owned buffers holding arbitrary values, as
+    benchmarks use it (decode_w4a8_triton.py:113-149)."""
     torch.manual_seed(8)
     n, k = 4096, 4096
     mod = T.W4A8TritonLinear(torch.nn.Linear(k, n, bias=True, dtype=torch.bfloat16, device=DEV))
