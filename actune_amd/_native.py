@@ -55,6 +55,7 @@ def lib():
         so.actune_tokenwise_workspace_bytes.restype = _I64
         so.actune_tokenwise_linear.argtypes = [_P, _I, _P, _P, _I, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I, _P,
                                                _I64, _P]
+        so.actune_forward_fuses_quantizer.argtypes = [_I64, _I64, _I64, _I, _I, _I, _I]
         so.actune_config_valid.argtypes = [_I, _I64]
         so.actune_default_config.argtypes = [_I64, _I64, _I64, _I, _I]
         _LIB = so
@@ -147,6 +148,14 @@ def config_valid(config: int, m: int) -> bool:
 
 def default_config(m: int, n: int, k: int, w: int, a: int) -> int:
     return lib().actune_default_config(m, n, k, w, a)
+
+
+def forward_fuses_quantizer(m, n, k, w, a, dtype, config=CONFIG_AUTO) -> bool:
+    """Whether grouped_forward quantizes x inside its GEMM launch."""
+    rc = lib().actune_forward_fuses_quantizer(m, n, k, w, a, DTYPE_CODES[dtype], config)
+    if rc < 0:
+        raise ValueError(lib().actune_last_error().decode())
+    return bool(rc)
 
 
 def _require_cuda(*tensors):

@@ -105,6 +105,16 @@ bool decode_fused(int64_t M, int64_t n_total, int64_t K, int W, int nw, int x_dt
   return M <= kFusedMaxM && !decode_fits((int)K, (int)M, W, nw, true, x_dt);
 }
 
+// Whether a forward call on x with the (resolved) config quantizes x inside
+// the GEMM launch. The quantizer is fused into the GEMM for M <= 4 on the
+// small-M and streaming kernels (for larger M its per-workgroup cost is no
+// longer hidden under the weight loads; measured on MI355X). On the decode
+// configs decode_fused decides.
+bool forward_fuses(int config, int64_t M, int64_t n_total, int64_t K, int W, int x_dt) {
+  if (config >= kDecodeFirst) return decode_fused(M, n_total, K, W, kSmallMWaves[config - kDecodeFirst], x_dt);
+  return M <= kFusedMaxM && (config < kSmallMConfigs || (config >= kStreamFirst && config < kPrefillFirst));
+}
+
 // ACTUNE_CONFIG_AUTO: calls that hand over x (and may fuse the quantizer) use
 // actune_default_config; calls on packed activations use packed_default (the
 // same choice without the in-launch quantization).
@@ -290,6 +300,13 @@ int packed_default(int64_t M, int64_t N, int64_t K, int W, int A) {
 }
 }  // namespace
 
+int actune_forward_fuses_quantizer(int64_t M, int64_t N, int64_t K, int W, int A, int x_dtype, int config) {
+  g_err[0] = 0;
+  config = resolve(config, M, N, K, W, A, true);
+  if (check_shape(M, K, W, A, x_dtype, kF32, config) || N <= 0) return -1;
+  return forward_fuses(config, M, N, K, W, x_dtype) ? 1 : 0;
+}
+
 int actune_quantize_groups(const void* x, int x_dtype, const void* input_scale, int64_t M, int64_t K,
                            int A, uint8_t* packed, float* scales, void* stream) {
   g_err[0] = 0;
@@ -338,12 +355,7 @@ int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_s
   LinearArgs g = base_args(M, K, bias_dtype, x_dtype);
   for (int t = 0; t < ntargets; ++t)
     add_problem(g, targets[t].w, targets[t].w_scale, targets[t].bias, targets[t].out, targets[t].N);
-  // The quantizer is fused into the GEMM for M <= 4 on the small-M and
-  // streaming kernels (for larger M its per-workgroup cost is no longer
-  // hidden under the weight loads; measured on MI355X). On the decode
-  // configs decode_fused decides.
-  bool fused = M <= kFusedMaxM && (config < kSmallMConfigs || (config >= kStreamFirst && config < kPrefillFirst));
-  if (config >= kDecodeFirst) fused = decode_fused(M, n_total, K, W, kSmallMWaves[config - kDecodeFirst], x_dtype);
+  const bool fused = forward_fuses(config, M, n_total, K, W, x_dtype);
   if (fused) {
     g.x = x;
     g.xscale = input_scale;

@@ -50,8 +50,9 @@ class GraphReplay:
         """Serve small literal GPU constants built inside the function from a
         cache filled during warm-up (a fresh host->device copy cannot be
         captured); each use gets a clone because callers update in place.
-        Also bounds the tokenwise shared-activation cache to the call,
-        enabled when shared_a8 is set (graph.py:18-42)."""
+        Also bounds the shared activation caches to the call (the tokenwise
+        per-row codes, graph.py:18-42, and the group-64 codes), enabled when
+        shared_a8 is set."""
         make = torch.tensor
 
         def cached_tensor(data, *args, **kwargs):
@@ -66,8 +67,10 @@ class GraphReplay:
                 self.constants[key] = make(data, **kwargs)
             return self.constants[key].clone()
 
+        from .kernels.grouped import shared_activation_scope
         from .kernels.tokenwise import shared_a8_cache_scope
-        with shared_a8_cache_scope(enabled=self.shared_a8), patch.object(torch, "tensor", cached_tensor):
+        with shared_a8_cache_scope(enabled=self.shared_a8), shared_activation_scope(enabled=self.shared_a8), \
+                patch.object(torch, "tensor", cached_tensor):
             yield
 
     def _key(self, leaves, spec):

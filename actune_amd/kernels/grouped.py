@@ -13,6 +13,9 @@ passes one) and the packed GEMM, both launched on the current HIP stream.
 """
 from __future__ import annotations
 
+from contextlib import contextmanager
+from contextvars import ContextVar
+
 import torch
 
 from .. import _native
@@ -20,6 +23,53 @@ from ..precision import active_precision_profile
 from .quantizers import weight_codes
 
 CONFIG_AUTO = _native.CONFIG_AUTO
+
+
+class SharedActivationCache:
+    """Group-64 codes of the inputs seen in one scope, keyed by the source
+    tensor object, the activation width and the channel scale: linears that
+    read the same x at the same width (q/k/v, gate/up) then share one
+    quantizer launch, whatever their weight widths."""
+
+    __slots__ = ("enabled", "entries", "hits", "misses")
+
+    def __init__(self, *, enabled=True):
+        self.enabled = enabled
+        self.entries = []
+        self.hits = 0
+        self.misses = 0
+
+
+_SHARED_GROUP_STATE: ContextVar[SharedActivationCache | None] = ContextVar("actune_shared_group64_codes",
+                                                                           default=None)
+
+
+@contextmanager
+def shared_activation_scope(*, enabled=True):
+    """Bound the group-64 code cache to one forward (GraphReplay enters it
+    with its shared_a8 flag, the reference's switch for shared activation
+    quantization, graph.py:18-42). Outside a scope nothing is cached, so a
+    tensor reused in place never sees stale codes."""
+    state = SharedActivationCache(enabled=enabled)
+    token = _SHARED_GROUP_STATE.set(state)
+    try:
+        yield state
+    finally:
+        _SHARED_GROUP_STATE.reset(token)
+
+
+def _shared_codes(state, source, flat, a, input_scale):
+    """(packed, scales) of flat at width a from the scope's cache, quantizing
+    on a miss."""
+    for entry in state.entries:
+        src, shape, width, scale, packed, scales = entry
+        if src is source and shape == flat.shape and width == a and scale is input_scale:
+            state.hits += 1
+            return packed, scales
+    packed, scales = _native.quantize_groups(flat, a, input_scale)
+    state.misses += 1
+    state.entries.append((source, flat.shape, a, input_scale, packed, scales))
+    return packed, scales
 
 
 def extension():
@@ -64,15 +114,30 @@ class GroupedLinear(torch.nn.Module):
         # kernel configuration id (ACTUNE_CONFIG_AUTO or a tuned id); not a buffer
         self.config = CONFIG_AUTO
 
-    def forward(self, x, input_scale=None):
+    def forward(self, x, input_scale=None, source=None):
         """y = grouped linear of x (optionally x / input_scale, rounded to
-        x's dtype, fused into the quantizer)."""
+        x's dtype, fused into the quantizer). Inside an enabled
+        shared_activation_scope, calls whose GEMM takes the quantizer's codes
+        reuse the codes of an earlier call on the same source tensor (source
+        defaults to x) at the same width and channel scale."""
         if not x.is_cuda:
             raise ValueError("Grouped integer backend requires CUDA")
         flat = x.reshape(-1, self.in_features).contiguous()
         if input_scale is not None and input_scale.dtype != flat.dtype:
             flat = (flat / input_scale).contiguous()
             input_scale = None
+            source = flat
+        state = _SHARED_GROUP_STATE.get()
+        m = flat.shape[0]
+        if state is not None and state.enabled and m > 0:
+            config = self.config if self.config != CONFIG_AUTO else \
+                _native.default_config(m, self.out_features, self.in_features, self.w, self.a)
+            if not _native.forward_fuses_quantizer(m, self.out_features, self.in_features, self.w, self.a,
+                                                   flat.dtype, config):
+                packed, scales = _shared_codes(state, x if source is None else source, flat, self.a, input_scale)
+                out = _native.grouped_linear(packed, scales, self.packed_weight, self.weight_scale, self.bias,
+                                             flat, self.w, self.a, config)
+                return out.reshape(*x.shape[:-1], self.out_features)
         out = _native.grouped_forward(flat, self.packed_weight, self.weight_scale, self.bias,
                                       self.w, self.a, input_scale=input_scale, config=self.config)
         return out.reshape(*x.shape[:-1], self.out_features)
@@ -115,11 +180,17 @@ class GroupedPaddedLinear(torch.nn.Module):
     def _dispatch(self, x, input_scale):
         self.calls += 1
         self.input_elements += x.numel()
-        if self.padding:
-            x = torch.nn.functional.pad(x, (0, self.padding))
-            if input_scale is not None:
-                input_scale = torch.nn.functional.pad(input_scale, (0, self.padding), value=1.0)
-        return self.active_backend()(x, input_scale)
+        if not self.padding:
+            return self.active_backend()(x, input_scale)
+        source = x
+        x = torch.nn.functional.pad(x, (0, self.padding))
+        if input_scale is not None:
+            input_scale = torch.nn.functional.pad(input_scale, (0, self.padding), value=1.0)
+        backend = self.active_backend()
+        if getattr(backend.forward, "__func__", None) is GroupedLinear.forward:
+            # the padded copy is new on every call: key shared codes on the caller's tensor
+            return backend(x, input_scale, source=source)
+        return backend(x, input_scale)
 
 
 def _zero_padded(linear, padded):

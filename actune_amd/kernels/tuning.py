@@ -71,9 +71,10 @@ def select(key, launch, configurations, default):
     return chosen
 
 
-def grouped_forward(self, x, input_scale=None):
+def grouped_forward(self, x, input_scale=None, source=None):
     """GroupedLinear.forward with per-signature configuration selection
-    (installed by install_bank(tune=True))."""
+    (installed by install_bank(tune=True)); source is accepted for the
+    GroupedLinear.forward signature (the tuned path always quantizes)."""
     if not x.is_cuda:
         raise ValueError("Grouped integer backend requires CUDA")
     flat = x.reshape(-1, self.in_features).contiguous()

@@ -101,6 +101,16 @@ int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_s
                                  void* stream);
 
 /*
+ * 1 when actune_grouped_forward(_multi) with these arguments quantizes x
+ * inside the GEMM launch (nothing is written to a_buf / scale_buf), 0 when
+ * it launches the quantizer and runs the GEMM on its codes, -1 for invalid
+ * arguments. N is the total output width of the call. Lets callers reuse
+ * one quantization of x for several linears (no reference counterpart; the
+ * reference shares per-row A8 codes the same way, w4a8_triton.py:270-325).
+ */
+int actune_forward_fuses_quantizer(int64_t M, int64_t N, int64_t K, int W, int A, int x_dtype, int config);
+
+/*
  * actune_grouped_forward without caller-owned scratch: no counterpart in the
  * reference. For callers that cannot allocate device memory (code under
  * stream capture, tight serving loops, harnesses that forbid hipMalloc).

@@ -217,8 +217,8 @@ def _schedule(seed=1234, steps=10):
     return [CONFIGURATIONS[i] for i in g.integers(0, 4, steps)]
 
 
-@pytest.mark.parametrize("fused", [False, True])
-def test_graph_replay_precision_schedule_matches_eager(fused):
+@pytest.mark.parametrize("fused,shared", [(False, False), (True, False), (False, True)])
+def test_graph_replay_precision_schedule_matches_eager(fused, shared):
     """C5: 10 denoise steps over a 50-token chunk with q00/q01/q11/q10
     switching from a seeded schedule. Graph replays (one graph per active
     configuration) equal eager execution bit for bit, every replay, with eager
@@ -232,7 +232,7 @@ def test_graph_replay_precision_schedule_matches_eager(fused):
     x_eager, eager = _denoise(model, x0, profiles, model, fused)
     eager_counts = {n: (m.calls, m.input_elements) for n, m in runtime.modules.items()}
 
-    replay = GraphReplay(model, runtime.modules)
+    replay = GraphReplay(model, runtime.modules, shared_a8=shared)
     replay.enabled = True
     runtime.before()
     x_graph, graphed = _denoise(replay, x0, profiles, model, fused)
@@ -247,6 +247,23 @@ def test_graph_replay_precision_schedule_matches_eager(fused):
     for q in set(profiles):
         per_call = {n: 50 * EXPERT[n][1] for n in EXPERT}
         bank.check_request(q, per_call)
+
+
+def test_shared_activation_scope_quantizes_once_per_width():
+    """q/k/v/gate/up read the same x at M=50 (the GEMMs take the quantizer's
+    codes): inside shared_activation_scope the A4 linears share one
+    quantization (and an A2 sibling gets its own); outputs are bit-identical
+    to the unshared forward."""
+    from actune_amd.kernels.grouped import shared_activation_scope
+    model, _, runtime = _install()
+    x = torch.randn(50, 1024, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
+    for q, (want_miss, want_hit) in {"q00": (3, 4), "q01": (4, 3)}.items():
+        with precision_profile(q):
+            plain = model(x)
+            with shared_activation_scope() as state:
+                shared = model(x)
+        assert (state.misses, state.hits) == (want_miss, want_hit), (q, state.misses, state.hits)
+        assert all(torch.equal(a, b) for a, b in zip(plain, shared))
 
 
 def test_graph_replay_limit_falls_back_to_eager():
