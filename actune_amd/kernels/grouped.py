@@ -15,6 +15,7 @@ from __future__ import annotations
 
 from contextlib import contextmanager
 from contextvars import ContextVar
+from types import MethodType
 
 import torch
 
@@ -203,6 +204,36 @@ def _zero_padded(linear, padded):
         if fc.bias is not None:
             fc.bias.copy_(linear.bias)
     return fc
+
+
+def _inference_mlp(self, x):
+    """GemmaMLP forward that reuses the gate activation as the product's
+    buffer (grouped.py:18-25); gate/up run as sibling projections (one
+    launch when their active versions match, else shared codes inside a
+    shared_activation_scope), bit-identical to the separate calls."""
+    if torch.is_grad_enabled():
+        return self._group64_original_forward(x)
+    gate_proj, up_proj = self.gate_proj, self.up_proj
+    if isinstance(gate_proj, GroupedPaddedLinear) and isinstance(up_proj, GroupedPaddedLinear):
+        gate, up = grouped_sibling_forward(x, [gate_proj, up_proj])
+    else:
+        gate, up = gate_proj(x), up_proj(x)
+    gate = self.act_fn(gate)
+    gate.mul_(up)
+    return self.down_proj(gate)
+
+
+def reuse_mlp_temporary(model):
+    """Patch every transformers GemmaMLP of `model` (once) with
+    _inference_mlp; returns the number patched (grouped.py:28-36)."""
+    from transformers.models.gemma.modeling_gemma import GemmaMLP
+    count = 0
+    for module in model.modules():
+        if type(module) is GemmaMLP and not hasattr(module, "_group64_original_forward"):
+            module._group64_original_forward = module.forward
+            module.forward = MethodType(_inference_mlp, module)
+            count += 1
+    return count
 
 
 def grouped_sibling_forward(x, modules):

@@ -363,3 +363,38 @@ def test_sibling_forward_equals_separate_calls(m):
             counts = {n: (mod.calls, mod.input_elements) for n, mod in runtime.modules.items()}
         assert all(torch.equal(a, b) for a, b in zip(sep, kv + gu + qq)), q
         assert counts == sep_counts
+
+
+def test_reuse_mlp_temporary_with_grouped_projections():
+    """A GemmaMLP whose projections are GroupedPaddedLinear: the patched
+    forward (gate/up as siblings, gate buffer reused for the product) equals
+    the unpatched forward bit for bit, for matching and different gate/up
+    versions, and under graph replay with the shared activation cache."""
+    from transformers import GemmaConfig
+    from transformers.models.gemma.modeling_gemma import GemmaMLP
+    from actune_amd.kernels.grouped import reuse_mlp_temporary
+    cfg = GemmaConfig(hidden_size=1024, intermediate_size=4096, hidden_activation="gelu_pytorch_tanh")
+    mlp = GemmaMLP(cfg).to(device=DEV, dtype=torch.bfloat16)
+    same = {q: "w4a4" for q in CONFIGURATIONS}
+    mixed = {"q00": "w4a4", "q01": "w2a4", "q11": "w2a4", "q10": "w4a4"}
+    clips = {m: None for m in ("w4a4", "w2a4")}
+    mlp.gate_proj = GroupedPaddedLinear(mlp.gate_proj, mixed, "q11", clips)
+    mlp.up_proj = GroupedPaddedLinear(mlp.up_proj, same, "q11", clips)
+    mlp.down_proj = GroupedPaddedLinear(mlp.down_proj, same, "q11", clips)
+    x = torch.randn(50, 1024, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(DEV)
+    with torch.inference_mode():
+        want = {q: _run_profile(mlp, x, q) for q in CONFIGURATIONS}
+        assert reuse_mlp_temporary(mlp) == 1
+        for q in CONFIGURATIONS:
+            assert torch.equal(_run_profile(mlp, x, q), want[q]), q
+        replay = GraphReplay(mlp, {"gate": mlp.gate_proj, "up": mlp.up_proj, "down": mlp.down_proj},
+                             shared_a8=True)
+        replay.enabled = True
+        for q in CONFIGURATIONS + CONFIGURATIONS:
+            with precision_profile(q):
+                assert torch.equal(replay(x), want[q]), q
+
+
+def _run_profile(module, x, q):
+    with precision_profile(q):
+        return module(x).clone()
