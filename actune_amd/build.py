@@ -20,6 +20,9 @@ LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libactune_hip.so"
 SOURCES = ["api.hip", "quantize.hip", "gemm_smallm.hip", "gemm_tiled.hip", "gemm_stream.hip", "gemm_prefill.hip", "gemm_decode.hip",
            "noalloc.hip", "tokenwise.hip"]
+# diagnostic library of register-resident compute ceilings, timed by bench.py
+CEILING_SOURCE = "ceiling.hip"
+CEILING_LIB = LIB_DIR / "libactune_ceiling.so"
 ARCH = "gfx950"
 
 
@@ -68,14 +71,15 @@ def build(verbose: bool = False, incremental: bool = False) -> Path:
     link the library."""
     OBJ.mkdir(exist_ok=True)
     LIB_DIR.mkdir(exist_ok=True)
-    with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
-        objs = list(pool.map(lambda src: _compile(src, incremental), SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode:
-        raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES) + 1) as pool:
+        objs = list(pool.map(lambda src: _compile(src, incremental), SOURCES + [CEILING_SOURCE]))
+    for lib, parts in ((LIB, objs[:-1]), (CEILING_LIB, objs[-1:])):
+        tmp = lib.with_suffix(".so.tmp")
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, parts)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode:
+            raise RuntimeError(f"link failed:\n{res.stderr}")
+        os.replace(tmp, lib)
     if verbose:
         print(f"built {LIB}", file=sys.stderr)
     return LIB

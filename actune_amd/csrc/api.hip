@@ -210,6 +210,18 @@ int actune_config_valid(int config, int64_t M) {
   return 1;
 }
 
+namespace {
+// Waves of a decode workgroup that get work: the canonical chunks split K
+// into min(16, ceil(G/4)) nonempty quads, so a wave count above that leaves
+// waves with an empty K-range that still load and quantize nothing but cost
+// their launch and barrier time (measured on MI355X at K = 1024 / 2048:
+// 16 waves 0.9-1.7 us slower than 4 or 8).
+bool decode_waves_useful(int64_t K, int nw) {
+  const int64_t q = (K / kGroup + 3) / 4;
+  return nw <= 4 || nw <= q;
+}
+}  // namespace
+
 int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
   // Decode (M <= 64, measured on MI355X at Llama/Gemma shapes): the decode
   // kernel beats the small-M and streaming kernels wherever a wave's K-range
@@ -231,16 +243,26 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
     const int pref = tiles >= 1024 ? 1 : 2;
     if (fused_at(pref)) return kDecodeFirst + pref;
   } else if (M > kFusedMaxM && M <= kDecodeMax) {
-    // narrow N, 8-token tiles: 16 waves quantize x in the launch where light
-    if (fused_at(2)) return kDecodeFirst + 2;
-  } else if (M >= 1 && M <= kFusedMaxM) {
+    // narrow N, 8-token tiles: the most waves that get work quantize x in
+    // the launch where light
+    for (int c = 2; c >= 0; --c)
+      if (decode_waves_useful(K, kSmallMWaves[c]) && fused_at(c)) return kDecodeFirst + c;
+  } else if (M == 1) {
+    // narrow N, one token: the launch is latency-bound, and the fewest waves
+    // whose ring holds the K-range finish first (measured on MI355X at the
+    // Gemma-2B and Llama-2-7B shapes, W2/W4/W8: 4096x4096 4.4 us, 2048x2048
+    // 3.4 us, 256x2048 3.2 us)
+    for (int c = 0; c < 3; ++c)
+      if (fused_at(c)) return kDecodeFirst + c;
+  } else if (M >= 2 && M <= kFusedMaxM) {
     // narrow N, M <= 4: fewer waves per tile cost less per-workgroup work, so
     // take the smallest wave count that still gives every SIMD a wave (tiles
-    // x waves >= 1024) and fits K, with x quantized in the launch where that
-    // pays (decode_light)
+    // x waves >= 1024, or the most waves that get work) and fits K, with x
+    // quantized in the launch where that pays (decode_light)
     for (int c = 0; c < 3; ++c) {
-      if (!(tiles * kSmallMWaves[c] >= 1024 || c == 2)) continue;
-      if (fused_at(c)) return kDecodeFirst + c;
+      const bool last = c == 2 || !decode_waves_useful(K, kSmallMWaves[c + 1]);
+      if (!(tiles * kSmallMWaves[c] >= 1024 || last)) continue;
+      if (decode_waves_useful(K, kSmallMWaves[c]) && fused_at(c)) return kDecodeFirst + c;
     }
   }
   return packed_default(M, N, K, W, A);
@@ -266,9 +288,12 @@ int decode_packed_config(int64_t M, int64_t N, int64_t K, int W) {
     order[0] = 2; order[1] = 1; order[2] = 0;
   }
   for (int c : order) {
-    if (M <= kFusedMaxM && tiles <= 256 && !(tiles * kSmallMWaves[c] >= 1024 || c == 2)) continue;
-    if (packed_at(c)) return kDecodeFirst + c;
+    const bool last = c == 2 || !decode_waves_useful(K, kSmallMWaves[c + 1]);
+    if (M <= kFusedMaxM && tiles <= 256 && !(tiles * kSmallMWaves[c] >= 1024 || last)) continue;
+    if (decode_waves_useful(K, kSmallMWaves[c]) && packed_at(c)) return kDecodeFirst + c;
   }
+  for (int c : order)  // every useful count failed to fit: any that fits
+    if (packed_at(c)) return kDecodeFirst + c;
   return -1;
 }
 

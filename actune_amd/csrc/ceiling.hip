@@ -1,0 +1,142 @@
+// Register-resident compute ceilings of the prefill inner loop (a diagnostic
+// library, libactune_ceiling.so, timed by bench.py; not part of the
+// library's C ABI).
+//
+// Each kernel repeats, on operands held in registers, the per-group
+// instruction mix of one prefill design: no global or LDS traffic, no
+// barriers. Its throughput is therefore the most that design can reach on
+// MI355X, whatever the memory side does. Every wave runs the same number of
+// iterations and writes one value at the end.
+//
+//  kind 0: the library's prefill kernel (gemm_prefill): per 64-K group, one
+//          16-row weight tile unpacked from W4 (shifted int8 codes), four
+//          v_mfma_i32_16x16x64_i8 against four 16-token tiles, then the
+//          per-group rescale of the previous group: v_cvt_f32_i32 + fma per
+//          output; chunk partials added every 4 groups.
+//  kind 1: an fp8 alternative for W <= 4, A <= 4: per group, W4 codes moved
+//          to offset-binary e4m3 bytes (c + 8, exact; 3 VALU per packed
+//          dword), one v_mfma_scale_f32_32x32x64_f8f6f4 whose C operand
+//          carries the offset correction, then one fma per output (the MFMA
+//          result is already fp32).
+//  kind 2: as kind 1 for A8: the activation codes split into two planes
+//          (a = 16 hi + lo, both exact in e4m3), two chained MFMAs.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// keeps a value opaque to the compiler, so that loop-invariant operands are
+// not hoisted out of the loop
+#define ACT_OPAQUE(x) asm volatile("" : "+v"(x))
+
+constexpr int kWords = 48;  // input dwords per thread
+
+__global__ __launch_bounds__(256) void ceiling_int8(const uint32_t* in, float* out, int iters) {
+  const uint32_t* s = in + (size_t)(blockIdx.x * 256 + threadIdx.x) * kWords;
+  uint32_t wp0 = s[0], wp1 = s[1];
+  v4i b[4];
+  float sc[4];
+  for (int y = 0; y < 4; ++y) {
+    b[y] = v4i{(int)s[2 + 4 * y], (int)s[3 + 4 * y], (int)s[4 + 4 * y], (int)s[5 + 4 * y]};
+    sc[y] = __uint_as_float(s[20 + y] & 0x3fffffffu);
+  }
+  v4i D[2][4];
+  float p[4][4], acc[4][4];
+  for (int y = 0; y < 4; ++y)
+    for (int r = 0; r < 4; ++r) { p[y][r] = acc[y][r] = 0.f; D[0][y][r] = D[1][y][r] = 0; }
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      ACT_OPAQUE(wp0);
+      ACT_OPAQUE(wp1);
+      const v4i wd = v4i{(int)((wp0 << 4) & 0xF0F0F0F0u), (int)(wp0 & 0xF0F0F0F0u),
+                         (int)((wp1 << 4) & 0xF0F0F0F0u), (int)(wp1 & 0xF0F0F0F0u)};
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        ACT_OPAQUE(b[y]);
+        D[g & 1][y] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wd, b[y], v4i{0, 0, 0, 0}, 0, 0, 0);
+      }
+#pragma unroll
+      for (int y = 0; y < 4; ++y)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[y][r] = __builtin_fmaf((float)D[(g + 1) & 1][y][r], sc[y], p[y][r]);
+    }
+#pragma unroll
+    for (int y = 0; y < 4; ++y)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) { acc[y][r] += p[y][r]; p[y][r] = 0.f; }
+  }
+  float t = 0.f;
+  for (int y = 0; y < 4; ++y)
+    for (int r = 0; r < 4; ++r) t += acc[y][r];
+  out[blockIdx.x * 256 + threadIdx.x] = t;
+}
+
+template <bool HILO>
+__global__ __launch_bounds__(256) void ceiling_fp8(const uint32_t* in, float* out, int iters) {
+  const uint32_t* s = in + (size_t)(blockIdx.x * 256 + threadIdx.x) * kWords;
+  uint32_t wp[4];
+  for (int j = 0; j < 4; ++j) wp[j] = s[j] & 0x77777777u;
+  v8i alo, ahi;
+  for (int j = 0; j < 8; ++j) { alo[j] = (int)(s[8 + j] & 0x07070707u); ahi[j] = (int)(s[16 + j] & 0x07070707u); }
+  float sc[16];
+  v16f corr;
+  for (int r = 0; r < 16; ++r) { sc[r] = __uint_as_float(s[24 + r] & 0x3fffffffu); corr[r] = (float)(int)(s[24 + r] & 0xffu); }
+  v16f D[2];
+  float p[16], acc[16];
+  for (int r = 0; r < 16; ++r) { p[r] = acc[r] = 0.f; D[0][r] = D[1][r] = 0.f; }
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      ACT_OPAQUE(alo);
+      ACT_OPAQUE(ahi);
+      ACT_OPAQUE(corr);
+      v8i w;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ACT_OPAQUE(wp[j]);
+        w[2 * j] = (int)((wp[j] ^ 0x88888888u) & 0x0F0F0F0Fu);
+        w[2 * j + 1] = (int)(((wp[j] >> 4) ^ 0x08080808u) & 0x0F0F0F0Fu);
+      }
+      // scale operands: E8M0 exponents (127 = 2^0, 131 = 2^4 for the hi plane)
+      v16f d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(alo, w, corr, 0, 0, 0, 127, 0, 127);
+      if constexpr (HILO) d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ahi, w, d, 0, 0, 0, 131, 0, 127);
+      D[g & 1] = d;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) p[r] = __builtin_fmaf(D[(g + 1) & 1][r], sc[r], p[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { acc[r] += p[r]; p[r] = 0.f; }
+  }
+  float t = 0.f;
+  for (int r = 0; r < 16; ++r) t += acc[r];
+  out[blockIdx.x * 256 + threadIdx.x] = t;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Input dwords per thread the kernels read (the caller passes blocks * 256 *
+// this many) and int8-equivalent multiply-accumulates per wave iteration
+// (4 groups of 64 K against a 64-output-wide tile for kind 0, a 32x32 tile
+// for kinds 1 and 2: 4 * 65536 either way).
+int actune_ceiling_words(void) { return kWords; }
+long actune_ceiling_macs_per_iter(void) { return 4L * 65536L; }
+
+// Runs kind 0, 1 or 2 on `blocks` workgroups of 4 waves; 0 on success.
+int actune_ceiling_run(int kind, const uint32_t* in, float* out, int blocks, int iters, void* stream) {
+  if (!in || !out || blocks <= 0 || iters <= 0) return -1;
+  const hipStream_t st = (hipStream_t)stream;
+  if (kind == 0) ceiling_int8<<<blocks, 256, 0, st>>>(in, out, iters);
+  else if (kind == 1) ceiling_fp8<false><<<blocks, 256, 0, st>>>(in, out, iters);
+  else if (kind == 2) ceiling_fp8<true><<<blocks, 256, 0, st>>>(in, out, iters);
+  else return -1;
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+}  // extern "C"

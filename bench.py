@@ -357,6 +357,62 @@ def bench_gemma(torch, _native, steps, warmup):
     return out
 
 
+def bench_ceilings(torch):
+    """Limits measured on this GPU that bound the two hot kernels:
+    - graph_launch_floor_us: per-launch time of a hipGraph of tiny fill
+      kernels (torch zero_ on one element): the least any launch of a
+      replayed step costs, whatever it computes;
+    - prefill_register_ceiling: int8-equivalent TOPS of register-resident
+      loops with the prefill inner loop's instruction mix
+      (libactune_ceiling.so; no global/LDS traffic, no barriers) at 2 and 4
+      waves per SIMD: kind 0 = the library's int8 16x16x64 MFMA + per-group
+      cvt/fma rescale, kind 1 = fp8 32x32x64 MFMA for W, A <= 4 (one fma per
+      output), kind 2 = the same for A8 as two hi/lo planes."""
+    import ctypes
+    from actune_amd import build as _build
+    lib = ctypes.CDLL(str(_build.CEILING_LIB))
+    lib.actune_ceiling_run.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_void_p]
+    lib.actune_ceiling_macs_per_iter.restype = ctypes.c_long
+    words, macs = lib.actune_ceiling_words(), lib.actune_ceiling_macs_per_iter()
+    out = {}
+    x = torch.zeros(1, device="cuda")
+
+    def fills():
+        for _ in range(200):
+            x.zero_()
+
+    gph = capture(torch, fills)
+    out["graph_launch_floor_us"] = round(time_graph(torch, gph, 20, 3) * 1e3 / 200, 3)
+    del gph
+    kinds = {0: "int8 16x16x64 + cvt/fma rescale (gemm_prefill's loop)", 1: "fp8 32x32x64, W,A <= 4 (fma only)",
+             2: "fp8 32x32x64, A8 as hi/lo planes"}
+    iters, st = 400, torch.cuda.current_stream()
+    ceil = {}
+    for waves_per_simd in (2, 4):
+        blocks = 256 * waves_per_simd  # 4 waves per workgroup, one per SIMD
+        buf = torch.randint(0, 2 ** 31 - 1, (blocks * 256 * words,), dtype=torch.int32, device="cuda")
+        res = torch.zeros(blocks * 256, device="cuda")
+        for kind, label in kinds.items():
+            def run(it, kind=kind):
+                rc = lib.actune_ceiling_run(kind, buf.data_ptr(), res.data_ptr(), blocks, it, st.cuda_stream)
+                if rc:
+                    raise RuntimeError(f"ceiling kernel {kind} failed ({rc})")
+            run(10)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            run(iters)
+            e1.record()
+            torch.cuda.synchronize()
+            tops = 2 * macs * blocks * 4 * iters / (e0.elapsed_time(e1) * 1e-3) / 1e12
+            ceil.setdefault(label, {})[f"{waves_per_simd}_waves_per_simd"] = dict(
+                TOPS=round(tops, 1), frac=round(tops / INT8_PEAK_TOPS, 4))
+        del buf, res
+    out["prefill_register_ceiling"] = ceil
+    return out
+
+
 TW_PAIRS = [("W4A8", 4, 8), ("W8A8", 8, 8), ("W2A8", 2, 8), ("W4A4", 4, 4), ("W2A4", 2, 4), ("W8A4", 8, 4)]
 
 
@@ -540,6 +596,11 @@ def main():
         r = {}
         r["ms_sib"], r["launches_sib"] = run_schedule(torch, _native, stack, W, A, True, args.steps, args.warmup)
         r["ms_lin"], r["launches_lin"] = run_schedule(torch, _native, stack, W, A, False, args.steps, args.warmup)
+        # every layer replays the first layer's weights (about 101 MB, held by
+        # the 256 MB memory-side cache): the same launches with warm caches
+        warm = stack[:len(SHAPES)] * args.layers
+        r["ms_warm"], _ = run_schedule(torch, _native, warm, W, A, True, args.steps, args.warmup)
+        del warm
         per_shape = {}
         for name, n, k in (SHAPES[0], SHAPES[4], SHAPES[6]):
             subset = [e for e in stack if e["name"] == name]
@@ -603,12 +664,15 @@ def main():
                            "us_per_linear": round(r["ms_lin"] * 1e3 / r["linears"], 3),
                            "weight_GBps": round(r["wbytes"] / (r["ms_lin"] * 1e-3) / 1e9, 1)},
             "per_shape": r["per_shape"],
+            "siblings_warm_cache": {"ms_per_step": round(r["ms_warm"], 4),
+                                    "note": "every layer reads the first layer's weights (cache-resident)"},
         }
     if not args.no_extra:
         line["detail"]["C3_prefill_M512"] = bench_prefill(torch, _native, 10, 3)
         line["detail"]["C4_gemma_W4A4"] = bench_gemma(torch, _native, 20, 5)
         line["detail"]["C5_expert_switching"] = bench_expert(torch, 20)
         line["detail"]["tokenwise_family"] = bench_tokenwise(torch, _native, 10, 3)
+        line["detail"]["ceilings"] = bench_ceilings(torch)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, W, A)
     print(json.dumps(line), flush=True)

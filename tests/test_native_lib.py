@@ -29,6 +29,21 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
 
 
+def test_ceiling_library_loads_and_rejects_bad_arguments():
+    """The diagnostic ceiling library (timed by bench.py) is built beside the
+    main one; it checks its arguments before launching anything."""
+    from actune_amd import build
+    lib = ctypes.CDLL(str(build.CEILING_LIB))
+    lib.actune_ceiling_macs_per_iter.restype = ctypes.c_long
+    assert lib.actune_ceiling_words() == 48 and lib.actune_ceiling_macs_per_iter() == 4 * 65536
+    lib.actune_ceiling_run.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_void_p]
+    assert lib.actune_ceiling_run(0, None, None, 1, 1, None) == -1
+    buf = ctypes.create_string_buffer(16)
+    assert lib.actune_ceiling_run(3, buf, buf, 1, 1, None) == -1     # unknown kind
+    assert lib.actune_ceiling_run(0, buf, buf, 0, 1, None) == -1     # no workgroups
+
+
 def test_version_and_layout_selftest():
     assert "gfx950" in _native.version()
     assert _native.lib().actune_layout_selftest() == 0
@@ -51,7 +66,13 @@ def test_config_table():
     assert _native.default_config(4, 4096, 4096, 4, 8) == 15   # 4 tokens x 16 groups exceed the x passes
     assert _native.default_config(1, 4096, 11008, 4, 8) == 16
     assert _native.default_config(1, 4096, 4096, 8, 8) == 15   # W8: 8 groups per ring
-    assert _native.default_config(1, 1024, 4096, 4, 8) == 16   # 64 tiles: 16 waves each
+    assert _native.default_config(1, 1024, 4096, 4, 8) == 14   # narrow N, one token: fewest waves that fit
+    # waves past the nonempty canonical chunks (ceil(K/256) quads) get no work
+    assert _native.default_config(1, 256, 2048, 4, 4) == 14
+    assert _native.default_config(2, 256, 2048, 4, 4) == 15    # 8 quads: at most 8 waves
+    assert _native.default_config(8, 256, 2048, 4, 4) == 15
+    assert _native.default_config(8, 256, 1024, 4, 4) == 14    # 4 quads: 4 waves
+    assert _native.default_config(8, 2048, 2048, 4, 4) == 15
     assert _native.default_config(1, 4096, 65536, 4, 8) == 2   # no decode config fits
     # M = 8: 16 waves quantize x in the launch, up to four row tiles sharing a
     # workgroup; for K = 11008 no wave count both fits its ring and quantizes
