@@ -20,7 +20,6 @@ _LIB = None
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 CONFIG_AUTO = -1
-CONFIG_PREFILL_F8 = 17  # fp8 prefill kernel (W, A <= 4), forward calls with a workspace only
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -50,12 +49,6 @@ def lib():
                                               _I, _I, _I, _P]
         so.actune_grouped_forward_multi.argtypes = [_P, _I, _P, _P, _P, ctypes.POINTER(_Target), _I, _I,
                                                     _I64, _I64, _I, _I, _I, _P]
-        so.actune_grouped_forward_ws.argtypes = [_P, _I, _P, _P, _P, _P, _I64, _P, _P, _P, _I, _P, _I64, _I64,
-                                                 _I64, _I, _I, _I, _P]
-        so.actune_grouped_forward_multi_ws.argtypes = [_P, _I, _P, _P, _P, _P, _I64, ctypes.POINTER(_Target), _I,
-                                                       _I, _I64, _I64, _I, _I, _I, _P]
-        so.actune_forward_workspace_bytes.argtypes = [_I64, _I64, _I64, _I, _I, _I]
-        so.actune_forward_workspace_bytes.restype = _I64
         so.actune_grouped_dots_i32.argtypes = [_P, _P, _I64, _I64, _I64, _I, _I, _I, _P, _P]
         so.actune_tokenwise_quantize.argtypes = [_P, _I, _I64, _I64, _I, _P, _P, _P]
         so.actune_tokenwise_workspace_bytes.argtypes = [_I64, _I64, _I64, _I, _I]
@@ -191,30 +184,6 @@ def _act_buffers(packed, scales, m, k, a, device):
     return packed, scales
 
 
-def forward_workspace_bytes(m, n, k, w, a, config=CONFIG_AUTO) -> int:
-    """Workspace bytes a forward call with these arguments needs (the fp8
-    prefill path's operand codes, M*K bytes; 0 for the other kernels); n is
-    the total output width."""
-    need = lib().actune_forward_workspace_bytes(m, n, k, w, a, config)
-    if need < 0:
-        raise ValueError("invalid forward arguments")
-    return need
-
-
-def _forward_workspace(workspace, need, device):
-    """The caller's workspace (u8, at least `need` bytes) or a new one; None
-    when the call needs none."""
-    if need == 0:
-        return None
-    if workspace is None:
-        return torch.empty(need, device=device, dtype=torch.uint8)
-    if workspace.device != device or workspace.dtype != torch.uint8 or not workspace.is_contiguous():
-        raise RuntimeError("workspace must be a contiguous uint8 tensor on the input's device")
-    if workspace.numel() < need:
-        raise RuntimeError(f"workspace too small ({workspace.numel()} < {need} bytes)")
-    return workspace
-
-
 def quantize_groups(x: torch.Tensor, a: int, input_scale: torch.Tensor | None = None,
                     packed: torch.Tensor | None = None, scales: torch.Tensor | None = None):
     """Group-64 quantize a contiguous [M, K] tensor; returns (packed, scales)."""
@@ -279,12 +248,11 @@ def grouped_linear(a, as_, w, ws, bias, source_or_shape, W, A, config=CONFIG_AUT
 
 
 def grouped_forward(flat, w, ws, bias, W, A, input_scale=None, config=CONFIG_AUTO, out=None,
-                    packed=None, scales=None, workspace=None):
+                    packed=None, scales=None):
     """Quantize + GEMM for a contiguous [M, K] input (GroupedLinear.forward's
     device work, grouped.py:127-143); returns [M, N] in flat.dtype.
-    packed [M, K*A/8] / scales [M, K/64] / out may be preallocated, and the
-    workspace (u8, forward_workspace_bytes) of the fp8 prefill path."""
-    _require_cuda(flat, w, ws, bias, input_scale, out, packed, scales, workspace)
+    packed [M, K*A/8] / scales [M, K/64] / out may be preallocated."""
+    _require_cuda(flat, w, ws, bias, input_scale, out, packed, scales)
     _check_widths(W, A)
     _check_flat(flat)
     m, k = flat.shape
@@ -295,22 +263,20 @@ def grouped_forward(flat, w, ws, bias, W, A, input_scale=None, config=CONFIG_AUT
         out = torch.empty((m, n), device=flat.device, dtype=flat.dtype)
     _check_buffer(out, "out", (m, n), flat.dtype, flat.device)
     bias_dt = _bias_code(bias)
-    workspace = _forward_workspace(workspace, forward_workspace_bytes(m, n, k, W, A, config), flat.device)
-    _check(lib().actune_grouped_forward_ws(
-        _ptr(flat), _dtype_code(flat), _ptr(input_scale), _ptr(packed), _ptr(scales), _ptr(workspace),
-        0 if workspace is None else workspace.numel(), _ptr(w), _ptr(ws),
+    _check(lib().actune_grouped_forward(
+        _ptr(flat), _dtype_code(flat), _ptr(input_scale), _ptr(packed), _ptr(scales), _ptr(w), _ptr(ws),
         _ptr(bias), bias_dt, _ptr(out), m, n, k, W, A, config, _stream(flat.device)))
     return out
 
 
 def grouped_forward_multi(flat, targets, W, A, input_scale=None, config=CONFIG_AUTO, packed=None,
-                          scales=None, workspace=None):
+                          scales=None):
     """Quantize + GEMM of one [M, K] input against up to 4 linears in one
     launch. targets: sequence of (w, ws, bias, out) with out [M, N_t] (None
     to allocate). Returns the list of outputs."""
     if not 1 <= len(targets) <= MAX_TARGETS:
         raise ValueError("between 1 and 4 targets required")
-    _require_cuda(flat, input_scale, packed, scales, workspace, *[t for tgt in targets for t in tgt])
+    _require_cuda(flat, input_scale, packed, scales, *[t for tgt in targets for t in tgt])
     _check_widths(W, A)
     _check_flat(flat)
     m, k = flat.shape
@@ -329,12 +295,9 @@ def grouped_forward_multi(flat, targets, W, A, input_scale=None, config=CONFIG_A
         outs.append(out)
         arr[j] = _Target(w.data_ptr(), ws.data_ptr(), None if bias is None else bias.data_ptr(), out.data_ptr(), n)
     packed, scales = _act_buffers(packed, scales, m, k, A, flat.device)
-    n_total = sum(int(arr[j].N) for j in range(len(targets)))
-    workspace = _forward_workspace(workspace, forward_workspace_bytes(m, n_total, k, W, A, config), flat.device)
-    _check(lib().actune_grouped_forward_multi_ws(_ptr(flat), _dtype_code(flat), _ptr(input_scale), _ptr(packed),
-                                                 _ptr(scales), _ptr(workspace),
-                                                 0 if workspace is None else workspace.numel(), arr, len(targets),
-                                                 bias_dt, m, k, W, A, config, _stream(flat.device)))
+    _check(lib().actune_grouped_forward_multi(_ptr(flat), _dtype_code(flat), _ptr(input_scale), _ptr(packed),
+                                              _ptr(scales), arr, len(targets), bias_dt, m, k, W, A, config,
+                                              _stream(flat.device)))
     return outs
 
 

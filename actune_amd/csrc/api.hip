@@ -26,10 +26,6 @@ constexpr int kPrefillConfigs = 4;
 constexpr int kDecodeFirst = kPrefillFirst + kPrefillConfigs;  // ids 14..16: decode kernel, M <= 64
 constexpr int kDecodeMax = 64;
 constexpr int kFusedMaxM = 4;      // small-M and streaming calls up to this M quantize inside the GEMM
-// id 17 (ACTUNE_CONFIG_PREFILL_F8): the fp8 prefill kernel, W, A <= 4, forward
-// calls with a workspace only (outside actune_num_configs())
-constexpr int kConfigF8 = ACTUNE_CONFIG_PREFILL_F8;
-static_assert(kConfigF8 == kNumConfigs, "the fp8 config follows the packed-call configs");
 constexpr int kSmallMWaves[kSmallMConfigs] = {4, 8, 16};
 thread_local char g_err[512];
 // Kernels address every operand through 32-bit buffer offsets and use
@@ -70,8 +66,6 @@ int check_shape(int64_t M, int64_t K, int W, int A, int out_dt, int bias_dt, int
   if (M > INT_MAX || K > INT_MAX / 8) return fail(ACTUNE_ERR_INVALID, "dimensions too large");
   if (M * K * 4 >= kMaxBufferBytes) return fail(ACTUNE_ERR_INVALID, "operand too large (each buffer must stay below 2 GiB)");
   if (!dtype_ok(out_dt) || !dtype_ok(bias_dt)) return fail(ACTUNE_ERR_INVALID, "unsupported output/bias dtype");
-  if (config == kConfigF8)
-    return fail(ACTUNE_ERR_INVALID, "configuration 17 (fp8 prefill) runs only through actune_grouped_forward_ws");
   if (config < 0 || config >= kNumConfigs) return fail(ACTUNE_ERR_INVALID, "invalid configuration");
   if (config < kSmallMConfigs && M > kSmallMMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
   if (config >= kStreamFirst && config < kPrefillFirst && M > kStreamMax)
@@ -127,17 +121,6 @@ bool forward_fuses(int config, int64_t M, int64_t n_total, int64_t K, int W, int
 int resolve(int config, int64_t M, int64_t N, int64_t K, int W, int A, bool has_x) {
   if (config != ACTUNE_CONFIG_AUTO) return config;
   return has_x ? actune_default_config(M, N, K, W, A) : packed_default(M, N, K, W, A);
-}
-
-// The config a forward call with a workspace runs: ACTUNE_CONFIG_AUTO takes
-// the fp8 prefill kernel for W, A <= 4 wherever the int8 choice is a
-// large-M kernel (prefill or tiled), otherwise the int8 choice.
-int resolve_ws(int config, int64_t M, int64_t N, int64_t K, int W, int A) {
-  if (config == kConfigF8) return config;
-  const int c = resolve(config, M, N, K, W, A, true);
-  const bool large = (c >= kSmallMConfigs && c < kStreamFirst) || (c >= kPrefillFirst && c < kDecodeFirst);
-  (void)large;  // measured slower than the int8 kernels on every C3/C4 shape: never chosen by AUTO
-  return c;
 }
 
 // Fill the problem table of a launch; returns the number of 16-row tiles.
@@ -419,59 +402,6 @@ int actune_grouped_forward(const void* x, int x_dtype, const void* input_scale, 
   const actune_linear_target t{w, w_scale, bias, out, N};
   return actune_grouped_forward_multi(x, x_dtype, input_scale, a_buf, scale_buf, &t, 1, bias_dtype, M, K,
                                       W, A, config, stream);
-}
-
-int64_t actune_forward_workspace_bytes(int64_t M, int64_t N, int64_t K, int W, int A, int config) {
-  if (M < 0 || N <= 0 || K <= 0 || K % 64 || !width_ok(W) || !width_ok(A)) return -1;
-  return resolve_ws(config, M, N, K, W, A) == kConfigF8 ? M * K : 0;
-}
-
-int actune_grouped_forward_multi_ws(const void* x, int x_dtype, const void* input_scale, uint8_t* a_buf,
-                                    float* scale_buf, void* workspace, int64_t workspace_bytes,
-                                    const actune_linear_target* targets, int ntargets, int bias_dtype, int64_t M,
-                                    int64_t K, int W, int A, int config, void* stream) {
-  g_err[0] = 0;
-  if (ntargets < 1 || ntargets > ACTUNE_MAX_TARGETS || !targets)
-    return fail(ACTUNE_ERR_INVALID, "between 1 and 4 targets required");
-  if (!width_ok(W) || !width_ok(A)) return fail(ACTUNE_ERR_INVALID, "Unsupported integer width");
-  int64_t n_total = 0;
-  for (int t = 0; t < ntargets; ++t) n_total += targets[t].N;
-  if (M < 0 || K <= 0 || K % 64) return fail(ACTUNE_ERR_INVALID, "Grouped backend requires K divisible by 64");
-  const int c = n_total > 0 ? resolve_ws(config, M, n_total, K, W, A) : config;
-  if (c != kConfigF8)
-    return actune_grouped_forward_multi(x, x_dtype, input_scale, a_buf, scale_buf, targets, ntargets, bias_dtype,
-                                        M, K, W, A, c, stream);
-  // fp8 prefill: the quantizer writes fp8 operand codes [M, K] to the
-  // workspace and the group scales to scale_buf; a_buf is not used
-  if (W > 4 || A > 4) return fail(ACTUNE_ERR_INVALID, "configuration 17 (fp8 prefill) needs W, A <= 4");
-  if (!dtype_ok(bias_dtype) || !dtype_ok(x_dtype)) return fail(ACTUNE_ERR_INVALID, "unsupported dtype");
-  int rc = check_quantize(x, x_dtype, input_scale, M, K, A, reinterpret_cast<const uint8_t*>(workspace), scale_buf);
-  for (int t = 0; t < ntargets && !rc; ++t)
-    rc = check_target(targets[t].w, targets[t].w_scale, targets[t].out, targets[t].N, M, K, W);
-  if (!rc && M * K >= kMaxBufferBytes) rc = fail(ACTUNE_ERR_INVALID, "operand too large (each buffer must stay below 2 GiB)");
-  if (rc || M == 0) return rc;
-  if (workspace_bytes < M * K) return fail(ACTUNE_ERR_INVALID, "workspace too small (M*K bytes required)");
-  if (!aligned(workspace, 16)) return fail(ACTUNE_ERR_INVALID, "misaligned workspace (16 B required)");
-  hipStream_t st = (hipStream_t)stream;
-  launch_quantize_f8(x, x_dtype, input_scale, M, K, A, W, static_cast<uint8_t*>(workspace), scale_buf, st);
-  LinearArgs g = base_args(M, K, bias_dtype, x_dtype);
-  g.a = static_cast<const uint8_t*>(workspace);
-  g.as = scale_buf;
-  for (int t = 0; t < ntargets; ++t) {
-    LinearArgs one = g;
-    add_problem(one, targets[t].w, targets[t].w_scale, targets[t].bias, targets[t].out, targets[t].N);
-    launch_prefill_f8(W, A, one, st);
-  }
-  return check_launch();
-}
-
-int actune_grouped_forward_ws(const void* x, int x_dtype, const void* input_scale, uint8_t* a_buf,
-                              float* scale_buf, void* workspace, int64_t workspace_bytes, const uint8_t* w,
-                              const float* w_scale, const void* bias, int bias_dtype, void* out, int64_t M,
-                              int64_t N, int64_t K, int W, int A, int config, void* stream) {
-  const actune_linear_target t{w, w_scale, bias, out, N};
-  return actune_grouped_forward_multi_ws(x, x_dtype, input_scale, a_buf, scale_buf, workspace, workspace_bytes,
-                                         &t, 1, bias_dtype, M, K, W, A, config, stream);
 }
 
 int actune_grouped_dots_i32(const uint8_t* a, const uint8_t* w, int64_t M, int64_t N, int64_t K,

@@ -93,12 +93,6 @@ void set_last_error(const char* msg);
 
 void launch_quantize(const void* x, int dt, const void* sc, long M, long K, int A, uint8_t* packed,
                      float* scales, hipStream_t stream);
-// fp8 operand codes [M, K] bytes + scales [M, K/64] for the fp8 prefill
-// kernel (A in {2, 4}, element order of weight width W in {2, 4})
-void launch_quantize_f8(const void* x, int dt, const void* sc, long M, long K, int A, int W, uint8_t* codes8,
-                        float* scales, hipStream_t stream);
-// fp8 MFMA prefill (W, A <= 4): g.a holds the fp8 operand codes
-void launch_prefill_f8(int W, int A, const LinearArgs& g, hipStream_t st);
 void launch_smallm(int W, int A, int nw, int mode, const LinearArgs& g, hipStream_t st);
 void launch_tiled(int W, int A, int shape, bool dots, const LinearArgs& g, hipStream_t st);
 void launch_stream(int W, int A, int nw, int mode, const LinearArgs& g, hipStream_t st);

@@ -62,69 +62,6 @@ __global__ __launch_bounds__(256) void quantize_groups_kernel(const void* __rest
   if (seg == 0) scales[gi] = s;
 }
 
-// fp8 operand mode (the fp8 prefill kernel's activations): the same codes
-// and scales, written as one e4m3 byte per code, sign-magnitude in the
-// linear low range (byte (c < 0 ? 0x80 : 0) | |c| holds c * 2^-9; |c| <= 8
-// for A <= 4), in the element order the weight width W unpacks to (so that
-// one MFMA K order serves both operands). Per group the 64 bytes are
-// [K-half 0: 32 bytes][K-half 1: 32 bytes]; inside a half, 4-bit weights
-// order code 8d + 2t + (r % 2) at byte t of dword r (d = r / 2), 2-bit
-// weights code 16d + 4t + (r % 4) (d = r / 4). The lane owning codes
-// 8 seg .. 8 seg + 7 writes bytes 8 seg .. 8 seg + 7 of its group.
-__device__ __forceinline__ uint32_t sm_byte(int c) {
-  return (c < 0 ? 0x80u : 0u) | (uint32_t)(c < 0 ? -c : c);
-}
-
-template <int A, int DT, bool SCALE, int W>
-__global__ __launch_bounds__(256) void quantize_f8_kernel(const void* __restrict__ x,
-                                                          const void* __restrict__ input_scale,
-                                                          long groups, int G,
-                                                          uint8_t* __restrict__ codes8,
-                                                          float* __restrict__ scales) {
-  static_assert(A == 2 || A == 4, "fp8 operands hold A <= 4 codes");
-  static_assert(W == 2 || W == 4, "weight widths with an fp8 path");
-  const long gi = (long)blockIdx.x * 32 + (threadIdx.x >> 3);
-  const int seg = threadIdx.x & 7;
-  const bool live = gi < groups;
-  const long gsafe = live ? gi : groups - 1;
-  const long e0 = gsafe * kGroup + seg * 8;
-  const int k0 = (int)(gsafe % G) * kGroup + seg * 8;
-
-  float v[8];
-  load8<DT>(x, e0, v);
-  if constexpr (SCALE) {
-    float d[8];
-    load8<DT>(input_scale, k0, d);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = round_to_dtype<DT>(v[e] / d[e]);
-  }
-  int c[8];
-  const float s = group_codes<A, DT>(v, c);
-  uint32_t out0, out1;
-  if constexpr (W == 4) {
-    out0 = sm_byte(c[0]) | sm_byte(c[2]) << 8 | sm_byte(c[4]) << 16 | sm_byte(c[6]) << 24;
-    out1 = sm_byte(c[1]) | sm_byte(c[3]) << 8 | sm_byte(c[5]) << 16 | sm_byte(c[7]) << 24;
-  } else {
-    // a 16-code block spans lanes seg (even) and seg + 1: half-dword j of a
-    // lane holds its codes j and j + 4; dword j of the block joins the even
-    // lane's half-dword j (low) with the odd lane's (high); the even lane
-    // writes dwords 0, 1, the odd lane dwords 2, 3
-    uint32_t hw[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) hw[j] = sm_byte(c[j]) | sm_byte(c[j + 4]) << 8;
-    const bool odd = seg & 1;
-    const uint32_t send0 = odd ? hw[0] : hw[2], send1 = odd ? hw[1] : hw[3];
-    // quad_perm [1, 0, 3, 2]: swap with the neighbouring lane
-    const uint32_t r0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)send0, 0xB1, 0xF, 0xF, false);
-    const uint32_t r1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)send1, 0xB1, 0xF, 0xF, false);
-    out0 = odd ? (r0 | hw[2] << 16) : (hw[0] | r0 << 16);
-    out1 = odd ? (r1 | hw[3] << 16) : (hw[1] | r1 << 16);
-  }
-  if (!live) return;
-  *reinterpret_cast<v2u*>(codes8 + gi * kGroup + seg * 8) = v2u{out0, out1};
-  if (seg == 0) scales[gi] = s;
-}
-
 template <int A, int DT>
 static void launch_quantize_dt(const void* x, const void* sc, long M, long K, uint8_t* packed,
                                float* scales, hipStream_t stream) {
@@ -149,39 +86,6 @@ void launch_quantize(const void* x, int dt, const void* sc, long M, long K, int 
   if (A == 8) launch_quantize_a<8>(x, dt, sc, M, K, packed, scales, stream);
   else if (A == 4) launch_quantize_a<4>(x, dt, sc, M, K, packed, scales, stream);
   else launch_quantize_a<2>(x, dt, sc, M, K, packed, scales, stream);
-}
-
-}  // namespace actune
-
-namespace actune {
-
-template <int A, int DT, int W>
-static void launch_quantize_f8_w(const void* x, const void* sc, long M, long K, uint8_t* codes8, float* scales,
-                                 hipStream_t stream) {
-  const long groups = M * (K / kGroup);
-  const dim3 grid((unsigned)((groups + 31) / 32));
-  if (sc)
-    quantize_f8_kernel<A, DT, true, W><<<grid, 256, 0, stream>>>(x, sc, groups, (int)(K / kGroup), codes8, scales);
-  else
-    quantize_f8_kernel<A, DT, false, W><<<grid, 256, 0, stream>>>(x, sc, groups, (int)(K / kGroup), codes8, scales);
-}
-
-template <int A, int DT>
-static void launch_quantize_f8_dt(const void* x, const void* sc, long M, long K, int W, uint8_t* codes8,
-                                  float* scales, hipStream_t stream) {
-  if (W == 4) launch_quantize_f8_w<A, DT, 4>(x, sc, M, K, codes8, scales, stream);
-  else launch_quantize_f8_w<A, DT, 2>(x, sc, M, K, codes8, scales, stream);
-}
-
-void launch_quantize_f8(const void* x, int dt, const void* sc, long M, long K, int A, int W, uint8_t* codes8,
-                        float* scales, hipStream_t stream) {
-#define QF8(AB)                                                                             \
-  if (dt == kBF16) launch_quantize_f8_dt<AB, kBF16>(x, sc, M, K, W, codes8, scales, stream); \
-  else if (dt == kF16) launch_quantize_f8_dt<AB, kF16>(x, sc, M, K, W, codes8, scales, stream); \
-  else launch_quantize_f8_dt<AB, kF32>(x, sc, M, K, W, codes8, scales, stream)
-  if (A == 4) { QF8(4); }
-  else { QF8(2); }
-#undef QF8
 }
 
 }  // namespace actune

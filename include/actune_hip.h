@@ -37,8 +37,6 @@ typedef struct actune_linear_target {
 } actune_linear_target;
 enum { ACTUNE_DTYPE_BF16 = 0, ACTUNE_DTYPE_F16 = 1, ACTUNE_DTYPE_F32 = 2 };
 #define ACTUNE_CONFIG_AUTO (-1)
-/* fp8 prefill kernel (W, A <= 4), runnable through actune_grouped_forward_ws only */
-#define ACTUNE_CONFIG_PREFILL_F8 17
 
 /* Library version string. */
 const char* actune_version(void);
@@ -160,32 +158,6 @@ int actune_grouped_dots_i32(const uint8_t* a, const uint8_t* w, int64_t M, int64
 int actune_num_configs(void);
 int actune_config_valid(int config, int64_t M);
 int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A);
-
-/*
- * actune_grouped_forward(_multi) with a caller-owned workspace, which lets
- * the call run ACTUNE_CONFIG_PREFILL_F8: for W, A <= 4 the quantizer writes
- * the codes as fp8 operand bytes [M, K] into the workspace (a_buf is then not
- * used, scale_buf receives the group scales) and the prefill kernel contracts
- * them on fp8 MFMAs that return the exact group dots in fp32 (one fma per
- * output and group instead of convert + fma). Results equal
- * actune_grouped_forward's bit for bit. ACTUNE_CONFIG_AUTO resolves to it for
- * W, A <= 4 wherever actune_default_config picks a large-M kernel (the
- * prefill or tiled configs), otherwise to actune_default_config's choice.
- * actune_forward_workspace_bytes: the workspace bytes a call with these
- * arguments needs (M * K for the fp8 config, else 0; -1 for invalid
- * arguments); N is the total output width. Same device work as
- * GroupedLinear.forward (actune/kernels/grouped.py:127-143); the workspace
- * has no counterpart in the reference.
- */
-int64_t actune_forward_workspace_bytes(int64_t M, int64_t N, int64_t K, int W, int A, int config);
-int actune_grouped_forward_ws(const void* x, int x_dtype, const void* input_scale, uint8_t* a_buf,
-                              float* scale_buf, void* workspace, int64_t workspace_bytes, const uint8_t* w,
-                              const float* w_scale, const void* bias, int bias_dtype, void* out, int64_t M,
-                              int64_t N, int64_t K, int W, int A, int config, void* stream);
-int actune_grouped_forward_multi_ws(const void* x, int x_dtype, const void* input_scale, uint8_t* a_buf,
-                                    float* scale_buf, void* workspace, int64_t workspace_bytes,
-                                    const actune_linear_target* targets, int ntargets, int bias_dtype, int64_t M,
-                                    int64_t K, int W, int A, int config, void* stream);
 
 /* ------------------------------------------------------------------------
  * Tokenwise family: per-row dynamic activation scales, full-K int32
