@@ -13,13 +13,18 @@
 //          v_mfma_i32_16x16x64_i8 against four 16-token tiles, then the
 //          per-group rescale of the previous group: v_cvt_f32_i32 + fma per
 //          output; chunk partials added every 4 groups.
-//  kind 1: an fp8 alternative for W <= 4, A <= 4: per group, W4 codes moved
-//          to offset-binary e4m3 bytes (c + 8, exact; 3 VALU per packed
-//          dword), one v_mfma_scale_f32_32x32x64_f8f6f4 whose C operand
-//          carries the offset correction, then one fma per output (the MFMA
+//  kind 1: an exact fp8 alternative for W <= 4, A <= 4: per group, W4 codes
+//          moved to offset-binary e4m3 bytes (c + 8, exact; 3 VALU per packed
+//          dword), a v_mfma_scale_f32_32x32x64_f8f6f4 of the constant -8
+//          against the activations (the offset correction -8 sum a) feeding
+//          the C operand of the main MFMA, then one fma per output (the MFMA
 //          result is already fp32).
 //  kind 2: as kind 1 for A8: the activation codes split into two planes
-//          (a = 16 hi + lo, both exact in e4m3), two chained MFMAs.
+//          (a = 16 hi + lo, both exact in e4m3): two correction and two
+//          main MFMAs, chained.
+//  kind 3: kind 1 without the correction MFMA (its C operand taken from
+//          registers): the bound of an fp8 design whose correction costs
+//          nothing.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -76,7 +81,7 @@ __global__ __launch_bounds__(256) void ceiling_int8(const uint32_t* in, float* o
   out[blockIdx.x * 256 + threadIdx.x] = t;
 }
 
-template <bool HILO>
+template <bool HILO, bool CORR>
 __global__ __launch_bounds__(256) void ceiling_fp8(const uint32_t* in, float* out, int iters) {
   const uint32_t* s = in + (size_t)(blockIdx.x * 256 + threadIdx.x) * kWords;
   uint32_t wp[4];
@@ -89,6 +94,9 @@ __global__ __launch_bounds__(256) void ceiling_fp8(const uint32_t* in, float* ou
   v16f D[2];
   float p[16], acc[16];
   for (int r = 0; r < 16; ++r) { p[r] = acc[r] = 0.f; D[0][r] = D[1][r] = 0.f; }
+  v8i neg8;  // -8 (byte 0x88) everywhere
+  for (int j = 0; j < 8; ++j) neg8[j] = (int)0x88888888u;
+  const v16f zero16 = {};
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -103,7 +111,12 @@ __global__ __launch_bounds__(256) void ceiling_fp8(const uint32_t* in, float* ou
         w[2 * j + 1] = (int)(((wp[j] >> 4) ^ 0x08080808u) & 0x0F0F0F0Fu);
       }
       // scale operands: E8M0 exponents (127 = 2^0, 131 = 2^4 for the hi plane)
-      v16f d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(alo, w, corr, 0, 0, 0, 127, 0, 127);
+      v16f c = corr;
+      if constexpr (CORR) {
+        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(alo, neg8, zero16, 0, 0, 0, 127, 0, 127);
+        if constexpr (HILO) c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ahi, neg8, c, 0, 0, 0, 131, 0, 127);
+      }
+      v16f d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(alo, w, c, 0, 0, 0, 127, 0, 127);
       if constexpr (HILO) d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ahi, w, d, 0, 0, 0, 131, 0, 127);
       D[g & 1] = d;
 #pragma unroll
@@ -124,17 +137,18 @@ extern "C" {
 // Input dwords per thread the kernels read (the caller passes blocks * 256 *
 // this many) and int8-equivalent multiply-accumulates per wave iteration
 // (4 groups of 64 K against a 64-output-wide tile for kind 0, a 32x32 tile
-// for kinds 1 and 2: 4 * 65536 either way).
+// for kinds 1-3: 4 * 65536 either way).
 int actune_ceiling_words(void) { return kWords; }
 long actune_ceiling_macs_per_iter(void) { return 4L * 65536L; }
 
-// Runs kind 0, 1 or 2 on `blocks` workgroups of 4 waves; 0 on success.
+// Runs kind 0, 1, 2 or 3 on `blocks` workgroups of 4 waves; 0 on success.
 int actune_ceiling_run(int kind, const uint32_t* in, float* out, int blocks, int iters, void* stream) {
   if (!in || !out || blocks <= 0 || iters <= 0) return -1;
   const hipStream_t st = (hipStream_t)stream;
   if (kind == 0) ceiling_int8<<<blocks, 256, 0, st>>>(in, out, iters);
-  else if (kind == 1) ceiling_fp8<false><<<blocks, 256, 0, st>>>(in, out, iters);
-  else if (kind == 2) ceiling_fp8<true><<<blocks, 256, 0, st>>>(in, out, iters);
+  else if (kind == 1) ceiling_fp8<false, true><<<blocks, 256, 0, st>>>(in, out, iters);
+  else if (kind == 2) ceiling_fp8<true, true><<<blocks, 256, 0, st>>>(in, out, iters);
+  else if (kind == 3) ceiling_fp8<false, false><<<blocks, 256, 0, st>>>(in, out, iters);
   else return -1;
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }

@@ -366,8 +366,9 @@ def bench_ceilings(torch):
       loops with the prefill inner loop's instruction mix
       (libactune_ceiling.so; no global/LDS traffic, no barriers) at 2 and 4
       waves per SIMD: kind 0 = the library's int8 16x16x64 MFMA + per-group
-      cvt/fma rescale, kind 1 = fp8 32x32x64 MFMA for W, A <= 4 (one fma per
-      output), kind 2 = the same for A8 as two hi/lo planes."""
+      cvt/fma rescale, kind 1 = exact fp8 32x32x64 MFMA for W, A <= 4 (one fma per
+      output after an offset-correction MFMA), kind 2 = the same for A8 as two
+      hi/lo planes, kind 3 = kind 1 with the correction taken for free."""
     import ctypes
     from actune_amd import build as _build
     lib = ctypes.CDLL(str(_build.CEILING_LIB))
@@ -385,8 +386,10 @@ def bench_ceilings(torch):
     gph = capture(torch, fills)
     out["graph_launch_floor_us"] = round(time_graph(torch, gph, 20, 3) * 1e3 / 200, 3)
     del gph
-    kinds = {0: "int8 16x16x64 + cvt/fma rescale (gemm_prefill's loop)", 1: "fp8 32x32x64, W,A <= 4 (fma only)",
-             2: "fp8 32x32x64, A8 as hi/lo planes"}
+    kinds = {0: "int8 16x16x64 + cvt/fma rescale (gemm_prefill's loop)",
+             1: "fp8 32x32x64, W,A <= 4, exact (offset-correction MFMA + fma)",
+             2: "fp8 32x32x64, A8 as hi/lo planes, exact",
+             3: "fp8 32x32x64, W,A <= 4, correction for free (unreachable bound)"}
     iters, st = 400, torch.cuda.current_stream()
     ceil = {}
     for waves_per_simd in (2, 4):

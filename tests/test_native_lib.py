@@ -40,7 +40,7 @@ def test_ceiling_library_loads_and_rejects_bad_arguments():
                                        ctypes.c_void_p]
     assert lib.actune_ceiling_run(0, None, None, 1, 1, None) == -1
     buf = ctypes.create_string_buffer(16)
-    assert lib.actune_ceiling_run(3, buf, buf, 1, 1, None) == -1     # unknown kind
+    assert lib.actune_ceiling_run(4, buf, buf, 1, 1, None) == -1     # unknown kind
     assert lib.actune_ceiling_run(0, buf, buf, 0, 1, None) == -1     # no workgroups
 
 
