@@ -316,7 +316,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   // waves have the same loads in flight: behind a branch, the compiler's
   // waits for the activation passes would count from the shorter path and
   // make wave 0 wait for weight slots before quantizing.
-  const ChannelConst cc = fetch_channel(pr.ws, pr.bias, bias_dt, N, n0 + 16 * wave + e_row, wave < TR);
+  const ChannelConst cc = fetch_channel(pr.ws, pr.bias, bias_dt, N, n0 + 16 * (wave % TR) + e_row, wave / TR < MT / 4);
 
   // ---------------------------------------------------------------- activation slab
   // the zero region: one dword per thread of the first four waves
@@ -509,14 +509,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   __syncthreads();
 
   // ---------------------------------------------------------------- epilogue
-  // wave t < TR finishes tile t
-  if (wave < TR) {
-    const int n = n0 + 16 * wave + e_row;
-#pragma unroll
-    for (int jt = 0; jt < MT / 4; ++jt) {
+  // wave w finishes tile w % TR, tokens 4j .. 4j + 3 for j = w / TR, w / TR +
+  // NW / TR, ... (the 4-token groups of an 8- or 16-token tile are finished
+  // by different waves at once)
+  if (MT == 4 ? wave < TR : true) {
+    const int et = wave % TR, n = n0 + 16 * et + e_row;
+    for (int jt = wave / TR; jt < MT / 4; jt += NW / TR) {
       const int m = e_m + 4 * jt;
       if (m < M && n < N) {
-        const float* rr = red + (size_t)(16 * wave + e_row) * MT + m;
+        const float* rr = red + (size_t)(16 * et + e_row) * MT + m;
         float acc = rr[0];
 #pragma unroll
         for (int q = 1; q < kChunks; ++q) acc = acc + rr[(size_t)q * RS];
