@@ -131,6 +131,42 @@ __device__ __forceinline__ void store_result(const TwArgs& a, int m, int n, int3
   else store_out<kF32>(a.out, o, y);
 }
 
+// Writes a wave's MT x NT accumulator tiles (lane: rows row_base + 16 mt +
+// 0..3, column col_base + 16 nt): with K splits, split z's raw int32 partial
+// sums (tw_reduce adds the splits, in any order, and finishes); otherwise
+// the finished outputs.
+template <int WL, int AL, int EPI, int MT, int NT>
+__device__ __forceinline__ void finish_tile(const TwArgs& args, const v4i (&acc)[MT][NT], int row_base,
+                                            int col_base, int z) {
+  constexpr int SHIFT = WTraits<WL>::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0);
+  const int M = args.M, N = args.N;
+  if (args.splits > 1) {
+    int32_t* part = args.partial + (size_t)z * M * N;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = row_base + mt * 16 + i, n = col_base + nt * 16;
+          if (m < M && n < N) part[(size_t)m * N + n] = acc[mt][nt][i];
+        }
+    return;
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int n = col_base + nt * 16;
+    if (n >= N) continue;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = row_base + mt * 16 + i;
+        if (m < M) store_result<EPI>(args, m, n, acc[mt][nt][i] >> SHIFT);
+      }
+  }
+}
+
 __device__ __forceinline__ v2u tr8(const uint8_t* p) {
   typedef int v2i_t __attribute__((ext_vector_type(2)));
   auto lp = (__attribute__((address_space(3))) v2i_t*)((__attribute__((address_space(3))) uint8_t*)p);
@@ -154,16 +190,14 @@ __device__ __forceinline__ void lds_store16(uint8_t* p, const v4u& v) {
 
 constexpr int align_of_stride(int s) { return s % 16 == 0 ? 16 : (s % 8 == 0 ? 8 : 4); }
 
-// WM waves along M (1 or 2), the rest along N; each wave owns MT x NT
-// 16x16 output tiles. Workgroup tile: TM = 16 MT WM rows, TN = 16 NT (4/WM)
-// columns. Grid: x = column tiles, y = row tiles, z = K splits (each split
-// writes its int32 partial sums; tw_reduce adds them and finishes).
-// K-steps move in batches of NB: a batch's loads are all issued together
-// (registers), staged into NB LDS buffers and computed after one barrier.
-// ONE (small M): a workgroup's K-range is a single batch (the host keeps it
-// at most NB steps), so every load is in flight at once. Otherwise two LDS
-// halves alternate: batch b + 1 loads while batch b computes.
-template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, bool ONE>
+// Small-M tokenwise GEMM. WM waves along M (1 or 2), the rest along N; each
+// wave owns MT x NT 16x16 output tiles. Workgroup tile: TM = 16 MT WM rows,
+// TN = 16 NT (4/WM) columns. Grid: x = column tiles, y = row tiles, z = K
+// splits (each split writes its int32 partial sums; tw_reduce adds them and
+// finishes). A workgroup's whole K-range (at most NB K-steps: the host splits
+// K until it is) is loaded at entry, every load in flight at once, staged into
+// NB LDS buffers and computed after one barrier.
+template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB>
 __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   using T = WTraits<WL>;
   constexpr int WN = 4 / WM;
@@ -174,8 +208,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   constexpr int WBUF = WROWS * WSTR, ABUF = TM * ASTR;
   constexpr int WCH = WROWS * WRB / 16, ACH = TM * ARB / 16;       // 16-byte chunks per step
   constexpr int NWC = (WCH + kThreads - 1) / kThreads, NAC = (ACH + kThreads - 1) / kThreads;
-  constexpr int SHIFT = T::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0);
-  constexpr int NBUF = ONE ? NB : 2 * NB;
+  constexpr int NBUF = NB;
   static_assert(NBUF * (WBUF + ABUF) <= 64 * 1024, "LDS tile buffers exceed 64 KiB");
   __shared__ __align__(16) uint8_t smem[NBUF * (WBUF + ABUF)];
 
@@ -327,73 +360,336 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
     }
   };
 
-  // (steps past g1 load zeros and add nothing, so batches are straight-line
-  // code with no bounds tests)
-  auto issue_batch = [&](int g, v4u (&wreg)[NB][NWC], v4u (&areg)[NB][NAC]) {
+  // every step of the K-range at once (steps past g1 load zeros and add
+  // nothing, so the batch is straight-line code with no bounds tests)
+  v4u wreg[NB][NWC], areg[NB][NAC];
 #pragma unroll
-    for (int i = 0; i < NB; ++i) issue(g + i, wreg[i], areg[i]);
-  };
-  auto stage_batch = [&](int half, const v4u (&wreg)[NB][NWC], const v4u (&areg)[NB][NAC]) {
+  for (int i = 0; i < NB; ++i) issue(g0 + i, wreg[i], areg[i]);
 #pragma unroll
-    for (int i = 0; i < NB; ++i) stage(half * NB + i, wreg[i], areg[i]);
-  };
-  auto compute_batch = [&](int half) {
+  for (int i = 0; i < NB; ++i) stage(i, wreg[i], areg[i]);
+  __syncthreads();
 #pragma unroll
-    for (int i = 0; i < NB; ++i) compute(half * NB + i);
-  };
-  if constexpr (ONE) {
-    v4u wreg[NB][NWC], areg[NB][NAC];
-    issue_batch(g0, wreg, areg);
-    stage_batch(0, wreg, areg);
-    __syncthreads();
-    compute_batch(0);
-  } else if (g0 < g1) {
-    v4u w0[NB][NWC], a0[NB][NAC], w1[NB][NWC], a1[NB][NAC];
-    issue_batch(g0, w0, a0);
-    stage_batch(0, w0, a0);
-    __syncthreads();
-    for (int g = g0; g < g1; g += 2 * NB) {
-      const bool more1 = g + NB < g1, more2 = g + 2 * NB < g1;
-      if (more1) issue_batch(g + NB, w1, a1);
-      compute_batch(0);
-      if (more1) stage_batch(1, w1, a1);
-      __syncthreads();
-      if (!more1) break;
-      if (more2) issue_batch(g + 2 * NB, w0, a0);
-      compute_batch(1);
-      if (more2) stage_batch(0, w0, a0);
-      __syncthreads();
-    }
-  }
+  for (int i = 0; i < NB; ++i) compute(i);
 
-  const int row_base = m0 + wm * 16 * MT + 4 * kb, col_base = n0 + wn * 16 * NT + r16;
-  if (S > 1) {
-    // raw partial sums of this split; tw_reduce adds the splits (integer
-    // addition: any order gives the same sum) and finishes
-    int32_t* part = args.partial + (size_t)z * M * N;
+  finish_tile<WL, AL, EPI, MT, NT>(args, acc, m0 + wm * 16 * MT + 4 * kb, n0 + wn * 16 * NT + r16, z);
+}
+
+// ------------------------------------------------------------ LDS-DMA ring
+// buffer_load_dwordx4 ... lds writes lane l's 16 bytes at M0 + 16 l, and a
+// lane whose offset is out of range writes zeros (both checked on MI355X).
+// It is issued from inline asm so that the compiler's wait-count tracking
+// does not see it: the compiler treats every LDS read as possibly aliasing
+// any DMA in flight and would wait for all of them (vmcnt(0)) before each
+// read, which serialises the ring; the kernel instead waits for exactly the
+// loads of the step it is about to read. The s_nop is the one wait state an
+// SALU write of M0 needs before an LDS DMA.
+__device__ __forceinline__ void dma16(Rsrc r, uint32_t m0, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(m0), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+
+// waits until at most N of this wave's vector memory operations are in flight
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N <= 63, "vmcnt holds 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+// Staged rows of RB bytes are not padded (a DMA block is 1 KiB of
+// consecutive chunks); chunk c of row r sits at chunk c ^ swz(r), with
+// swz(r) = (r / rows per 256 bytes) % chunks per row, so that the rows one
+// 16-lane group reads (8 or 16 consecutive rows, 8- or 16-byte pieces) fall
+// on distinct banks.
+template <int RB>
+__device__ __forceinline__ constexpr int swz(int r) {
+  return (r / (RB >= 256 ? 1 : 256 / RB)) % (RB / 16);
+}
+template <int RB>
+__device__ __forceinline__ constexpr int lds_pos(int r, int b) {
+  return r * RB + 16 * ((b >> 4) ^ swz<RB>(r)) + (b & 15);
+}
+
+// Large-M tokenwise GEMM: the tile geometry of tw_gemm, with the K-steps
+// staged through a ring of D LDS slots filled by DMA loads. Every K-step of
+// a workgroup is NI 1-KiB blocks (weights, then activations); wave w issues
+// blocks w, w + 4, ... (IPW per wave, the surplus aimed at a per-wave junk
+// KiB with offsets out of range). Step t + D - 1 is issued right after the
+// barrier that opens step t, into the slot step t - 1 used, so D - 1 steps
+// are in flight while one is computed, with no registers held for them.
+// A lane's global offsets are fixed; the step advance is the scalar offset
+// (out of range for steps past the workgroup's K-range).
+template <int WL, int AL, int EPI, int WM, int MT, int NT, int KS, int D>
+__global__ __launch_bounds__(kThreads) void tw_gemm_ring(const TwArgs args) {
+  using T = WTraits<WL>;
+  constexpr int WN = 4 / WM;
+  constexpr int TM = 16 * MT * WM, TN = 16 * NT * WN;
+  constexpr int U = T::U;
+  constexpr int WROWS = T::rows(TN), WRB = T::row_bytes(TN), ARB = a_row_bytes(WL, AL);
+  constexpr int WB = WROWS * WRB, AB = TM * ARB, SUB = WB + AB, SLOT = KS * SUB;
+  static_assert(WB % 1024 == 0 && AB % 1024 == 0, "tiles are whole 1-KiB DMA blocks");
+  constexpr int NWI = WB / 1024, NI = NWI + AB / 1024, IPW = (NI + 3) / 4;
+  static_assert(D >= 3 && (D - 2) * KS * IPW <= 63, "ring depth");
+  extern __shared__ __align__(16) uint8_t tw_ring[];
+
+  const int M = args.M, N = args.N, K = args.K;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int n0 = (int)blockIdx.x * TN, m0 = (int)blockIdx.y * TM;
+  const int z = (int)blockIdx.z;
+  const int g0 = (int)((long)z * args.steps / args.splits), g1 = (int)((long)(z + 1) * args.steps / args.splits);
+
+  uint32_t wbytes;
+  if constexpr (WL == ACTUNE_TW_KMAJOR_W8) wbytes = (uint32_t)K * N;
+  else if constexpr (WL == ACTUNE_TW_KMAJOR_W4) wbytes = (uint32_t)(K / 2) * N;
+  else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) wbytes = (uint32_t)(K / 4) * N;
+  else if constexpr (WL == ACTUNE_TW_ROWS_S4) wbytes = (uint32_t)N * (K / 2);
+  else wbytes = (uint32_t)N * (K / 4);
+  const uint32_t arow = AL == ACTUNE_TW_ACT_A4 ? (uint32_t)K / 2 : (uint32_t)K;
+  const Rsrc wr = make_rsrc(args.w, wbytes);
+  const Rsrc ar = make_rsrc(args.a, (uint32_t)M * arow);
+  const uint32_t wstep = T::KM ? (uint32_t)WROWS * (uint32_t)N : (uint32_t)WRB;
+  constexpr uint32_t astep = (AL == ACTUNE_TW_ACT_A4 || WL == ACTUNE_TW_KMAJOR_W4 || WL == ACTUNE_TW_KMAJOR_W2) ? 32 : 64;
+
+  // block j of this wave: lane offset (step 0), scalar step stride, LDS
+  // offset inside a slot (or of the junk KiB), weight or activation buffer
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)tw_ring;
+  uint32_t voff[IPW], sstep[IPW], lofs[IPW];
+  bool isw[IPW], junk[IPW];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = row_base + mt * 16 + i, n = col_base + nt * 16;
-          if (m < M && n < N) part[(size_t)m * N + n] = acc[mt][nt][i];
-        }
-    return;
+  for (int j = 0; j < IPW; ++j) {
+    const int b = 4 * j + wave;
+    isw[j] = b < NWI;
+    junk[j] = b >= NI;
+    if (b < NWI) {
+      constexpr int SW = WRB / 16;
+      const int p = 64 * b + lane, r = p / SW, c = (p % SW) ^ swz<WRB>(r);
+      bool live;
+      uint32_t off;
+      if constexpr (T::KM) {
+        live = n0 + 16 * c < N;
+        off = (uint32_t)r * (uint32_t)N + (uint32_t)(n0 + 16 * c);
+      } else {
+        live = n0 + r < N;
+        off = (uint32_t)(n0 + r) * (uint32_t)(WL == ACTUNE_TW_ROWS_S4 ? K / 2 : K / 4) + (uint32_t)(16 * c);
+      }
+      voff[j] = live ? off : kOff;
+      sstep[j] = wstep;
+      lofs[j] = (uint32_t)(1024 * b);
+    } else if (b < NI) {
+      constexpr int SA = ARB / 16;
+      const int p = 64 * (b - NWI) + lane, r = p / SA, c = (p % SA) ^ swz<ARB>(r);
+      uint32_t k;
+      if constexpr (AL == ACTUNE_TW_ACT_A4) k = 16 * c;
+      else if constexpr (WL == ACTUNE_TW_KMAJOR_W4) k = (uint32_t)(c >> 1) * (K / 2) + 16 * (c & 1);
+      else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) k = (uint32_t)(c >> 1) * (K / 4) + 16 * (c & 1);
+      else k = 16 * c;
+      voff[j] = m0 + r < M ? (uint32_t)(m0 + r) * arow + k : kOff;
+      sstep[j] = astep;
+      lofs[j] = (uint32_t)(WB + 1024 * (b - NWI));
+    } else {
+      voff[j] = kOff;
+      sstep[j] = 0;
+      lofs[j] = (uint32_t)(D * SLOT + 1024 * wave);
+    }
+    // uniform per wave; readfirstlane keeps it in a scalar register
+    lofs[j] = __builtin_amdgcn_readfirstlane(lds0 + lofs[j]);
   }
+  // ring step t: K-steps g0 + KS t + q (q < KS) into sub-slot q of `slot`
+  auto issue = [&](int t, int slot) {
+#pragma unroll
+    for (int q = 0; q < KS; ++q) {
+      const int g = g0 + KS * t + q;
+#pragma unroll
+      for (int j = 0; j < IPW; ++j) {
+        const uint32_t m0v = lofs[j] + (junk[j] ? 0u : (uint32_t)(slot * SLOT + q * SUB));
+        const uint32_t soff = g < g1 && !junk[j] ? (uint32_t)g * sstep[j] : kOff;
+        dma16(isw[j] ? wr : ar, __builtin_amdgcn_readfirstlane(m0v), voff[j], __builtin_amdgcn_readfirstlane(soff));
+      }
+    }
+  };
+
+  // per-lane LDS read offsets inside a slot (step-invariant)
+  const int r16 = lane & 15, kb = lane >> 4;
+  const int tr_row = (lane & 15) >> 1, tr_half = lane & 1;
+  int wofs[NT][2], aofs[MT][U][2];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int n = col_base + nt * 16;
-    if (n >= N) continue;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = row_base + mt * 16 + i;
-        if (m < M) store_result<EPI>(args, m, n, acc[mt][nt][i] >> SHIFT);
-      }
+    const int cn = wn * 16 * NT + nt * 16;
+    if constexpr (WL == ACTUNE_TW_KMAJOR_W8) {
+      wofs[nt][0] = lds_pos<WRB>(16 * kb + tr_row, cn + 8 * tr_half);
+      wofs[nt][1] = lds_pos<WRB>(16 * kb + 8 + tr_row, cn + 8 * tr_half);
+    } else if constexpr (T::KM) {
+      wofs[nt][0] = wofs[nt][1] = lds_pos<WRB>(8 * kb + tr_row, cn + 8 * tr_half);
+    } else if constexpr (WL == ACTUNE_TW_ROWS_S4) {
+      wofs[nt][0] = wofs[nt][1] = lds_pos<WRB>(cn + r16, 8 * kb);
+    } else {
+      wofs[nt][0] = wofs[nt][1] = lds_pos<WRB>(cn + r16, 4 * kb);
+    }
   }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = wm * 16 * MT + mt * 16 + r16;
+      if constexpr (AL == ACTUNE_TW_ACT_A4) {
+        aofs[mt][u][0] = aofs[mt][u][1] = WB + lds_pos<ARB>(row, 8 * kb);
+      } else if constexpr (WL == ACTUNE_TW_KMAJOR_W4 || WL == ACTUNE_TW_KMAJOR_W2) {
+        // k = j.. and the paired range: bytes 64 u + 8 kb and 64 u + 32 + 8 kb
+        aofs[mt][u][0] = WB + lds_pos<ARB>(row, 64 * u + 8 * kb);
+        aofs[mt][u][1] = WB + lds_pos<ARB>(row, 64 * u + 32 + 8 * kb);
+      } else {
+        aofs[mt][u][0] = aofs[mt][u][1] = WB + lds_pos<ARB>(row, 16 * kb);
+      }
+    }
+
+  v4i acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  // one step's operand fragments as read from LDS (weights still packed)
+  struct Frag {
+    v2u w[KS][U][NT][2];
+    v2u a[KS][U][MT][2];
+  };
+  auto read = [&](int slot, Frag& f) {
+#pragma unroll
+    for (int q = 0; q < KS; ++q) {
+      const uint8_t* base = tw_ring + slot * SLOT + q * SUB;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          if constexpr (WL == ACTUNE_TW_KMAJOR_W8) {
+            f.w[q][u][nt][0] = tr8(base + wofs[nt][0]);
+            f.w[q][u][nt][1] = tr8(base + wofs[nt][1]);
+          } else if constexpr (T::KM) {
+            if (u == 0) f.w[q][u][nt][0] = tr8(base + wofs[nt][0]);
+          } else if constexpr (WL == ACTUNE_TW_ROWS_S4) {
+            f.w[q][u][nt][0] = *reinterpret_cast<const v2u*>(base + wofs[nt][0]);
+          } else {
+            f.w[q][u][nt][0] = v2u{*reinterpret_cast<const uint32_t*>(base + wofs[nt][0]), 0u};
+          }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          if constexpr (AL == ACTUNE_TW_ACT_A4) {
+            f.a[q][u][mt][0] = *reinterpret_cast<const v2u*>(base + aofs[mt][u][0]);
+          } else if constexpr (WL == ACTUNE_TW_KMAJOR_W4 || WL == ACTUNE_TW_KMAJOR_W2) {
+            f.a[q][u][mt][0] = *reinterpret_cast<const v2u*>(base + aofs[mt][u][0]);
+            f.a[q][u][mt][1] = *reinterpret_cast<const v2u*>(base + aofs[mt][u][1]);
+          } else {
+            const v4u v = *reinterpret_cast<const v4u*>(base + aofs[mt][u][0]);
+            f.a[q][u][mt][0] = v2u{v[0], v[1]};
+            f.a[q][u][mt][1] = v2u{v[2], v[3]};
+          }
+        }
+      }
+    }
+  };
+  // MFMAs in column-tile order: the unpack of tile nt + 1 can issue while
+  // the MFMAs of tile nt run
+  auto mma = [&](const Frag& f) {
+#pragma unroll
+    for (int q = 0; q < KS; ++q) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        uint32_t af[MT][4];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          if constexpr (AL == ACTUNE_TW_ACT_A4) {
+            const uint32_t pp[2] = {f.a[q][u][mt][0][0], f.a[q][u][mt][0][1]};
+            unpack_slot<4>(pp, af[mt]);
+            if constexpr (WL == ACTUNE_TW_ROWS_S2) reorder_slot<4, 2>(af[mt]);
+            else if constexpr (T::KM) reorder_slot<4, 8>(af[mt]);
+          } else {
+            af[mt][0] = f.a[q][u][mt][0][0]; af[mt][1] = f.a[q][u][mt][0][1];
+            af[mt][2] = f.a[q][u][mt][1][0]; af[mt][3] = f.a[q][u][mt][1][1];
+          }
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          uint32_t bf[4];
+          if constexpr (WL == ACTUNE_TW_KMAJOR_W8) {
+            bf[0] = f.w[q][u][nt][0][0]; bf[1] = f.w[q][u][nt][0][1];
+            bf[2] = f.w[q][u][nt][1][0]; bf[3] = f.w[q][u][nt][1][1];
+          } else if constexpr (WL == ACTUNE_TW_KMAJOR_W4) {
+            const v2u b = f.w[q][u][nt][0];
+            bf[0] = (b[0] << 4) & 0xF0F0F0F0u; bf[1] = (b[1] << 4) & 0xF0F0F0F0u;
+            bf[2] = b[0] & 0xF0F0F0F0u;        bf[3] = b[1] & 0xF0F0F0F0u;
+          } else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) {
+            // fields 2u (k = j + 2u K/4) and 2u + 1 of the bytes read at u = 0
+            const v2u b = f.w[q][0][nt][0];
+            const int s0 = 6 - 4 * u, s1 = 4 - 4 * u;
+            bf[0] = (b[0] << s0) & 0xC0C0C0C0u;
+            bf[1] = (b[1] << s0) & 0xC0C0C0C0u;
+            bf[2] = (b[0] << s1) & 0xC0C0C0C0u;
+            bf[3] = (b[1] << s1) & 0xC0C0C0C0u;
+          } else if constexpr (WL == ACTUNE_TW_ROWS_S4) {
+            const uint32_t pp[2] = {f.w[q][u][nt][0][0], f.w[q][u][nt][0][1]};
+            unpack_slot<4>(pp, bf);
+          } else {
+            const uint32_t pw = f.w[q][u][nt][0][0];
+            unpack_slot<2>(&pw, bf);
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma16x16x64(af[mt], bf, acc[mt][nt]);
+        }
+      }
+    }
+  };
+  // Step t's fragments are read from LDS one iteration ahead, so their LDS
+  // latency hides behind step t - 1's MFMAs. The barrier that opens the
+  // read of step t + 1 also tells every wave that step t - 1's slot (read
+  // two iterations ago) is free for the DMA of step t + D - 1.
+  const int nsteps = (g1 - g0 + KS - 1) / KS;
+#pragma unroll
+  for (int i = 0; i < D - 1; ++i) issue(i, i);
+  Frag f0, f1;
+  int rs = 1, ls = D - 1;  // slot read next, slot loaded next
+  auto advance = [&]() {
+    rs = rs == D - 1 ? 0 : rs + 1;
+    ls = ls == D - 1 ? 0 : ls + 1;
+  };
+  if (nsteps > 0) {
+    wait_vmem<(D - 2) * KS * IPW>();
+    __syncthreads();
+    read(0, f0);
+  }
+  // Two steps per trip, each with a next step to read. The trip has no
+  // branch between a read and the MFMAs after it, so the compiler's
+  // wait-count merge at a join cannot make step t's MFMAs wait for the
+  // reads of step t + 1.
+  int t = 0;
+  for (; t + 2 < nsteps; t += 2) {
+    wait_vmem<(D - 3) * KS * IPW>();
+    __syncthreads();
+    issue(t + D - 1, ls);
+    read(rs, f1);
+    advance();
+    mma(f0);
+    wait_vmem<(D - 3) * KS * IPW>();
+    __syncthreads();
+    issue(t + D, ls);
+    read(rs, f0);
+    advance();
+    mma(f1);
+  }
+  // the last one or two steps (every later step was issued as out of range)
+  if (t + 1 < nsteps) {
+    wait_vmem<(D - 3) * KS * IPW>();
+    __syncthreads();
+    read(rs, f1);
+    mma(f0);
+    mma(f1);
+  } else if (t < nsteps) {
+    mma(f0);
+  }
+  // no DMA may still be writing this workgroup's LDS when it ends
+  wait_vmem<0>();
+  finish_tile<WL, AL, EPI, MT, NT>(args, acc, m0 + wm * 16 * MT + 4 * kb, n0 + wn * 16 * NT + r16, z);
 }
 
 // Adds the K splits' partial sums of one output each and finishes it.
@@ -493,7 +789,8 @@ __global__ __launch_bounds__(kThreads) void tw_quantize_kernel(const void* __res
 
 // ---------------------------------------------------------------- host side
 struct Geometry {
-  int wm, mt, nt, ns;
+  int wm, mt, nt, ns;   // small M: ns K-steps loaded at entry
+  int ks, d;            // large M: K-steps per ring slot, ring slots
   int tm() const { return 16 * mt * wm; }
   int tn() const { return 16 * nt * (4 / wm); }
 };
@@ -508,17 +805,20 @@ int64_t tiles_of(int64_t M, int64_t N, const Geometry& g) {
 }
 
 // M <= 32: 16-row x 128-column tiles, every K-step of a workgroup loaded at
-// entry (small_ns). Larger M: 64 x 128 tiles (2 x 2 waves of 32 x 64),
-// K-steps in double-buffered batches; 64 x 64 tiles (waves of 32 x 32) where
-// the 64 x 128 grid would give a CU fewer than two workgroups, i.e. one wave
-// per SIMD (measured on MI355X at M=512, N=4096: 11-19% faster for the int8,
-// nibble-pair, S4 and S2 layouts; the quarter layout keeps 64 x 128, whose
-// 4096x11008 launch went from 49 to 59 us).
+// entry (small_ns; tw_gemm). Larger M: the LDS-DMA ring (tw_gemm_ring),
+// chosen from measurements on MI355X at M = 512 over the Llama-2-7B shapes
+// (six layout pairs): where the 64 x 128 grid holds at least 512 tiles (two or
+// more workgroups per CU), 64 x 128 tiles with 3 slots of one K-step (two for
+// the row-major S4 / S2 layouts), small enough in LDS for three workgroups
+// per CU (W4A8 11008x4096: 60.8 -> 45.9 us); with fewer tiles, 4 slots of two
+// K-steps, on 64 x 128 tiles for the K-major layouts and 64 x 64 tiles for S4
+// / S2 (W4A8 4096x11008: 57.7 -> 51.2 us, W4A4 4096x4096: 30.4 -> 20.3 us).
 Geometry pick_geometry(int64_t M, int64_t N, int wl) {
-  if (M <= 32) return Geometry{1, 1, 2, small_ns(wl)};
-  const Geometry big{2, 2, 4, 0};
-  if (wl != ACTUNE_TW_KMAJOR_W2 && tiles_of(M, N, big) < 512) return Geometry{2, 2, 2, 0};
-  return big;
+  if (M <= 32) return Geometry{1, 1, 2, small_ns(wl), 0, 0};
+  const bool km = wl <= ACTUNE_TW_KMAJOR_W2;
+  const Geometry big{2, 2, 4, 0, km ? 1 : 2, 3};
+  if (tiles_of(M, N, big) >= 512) return big;
+  return km ? Geometry{2, 2, 4, 0, 2, 4} : Geometry{2, 2, 2, 0, 2, 4};
 }
 
 // K splits. Small M: enough splits that each workgroup's range fits its
@@ -536,11 +836,35 @@ int pick_splits(int64_t M, int64_t N, int64_t K, int wl, const Geometry& g) {
   return (int)s;
 }
 
-template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, bool ONE>
+template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB>
 void launch_gemm_t(const TwArgs& a, hipStream_t st) {
   constexpr int TM = 16 * MT * WM, TN = 16 * NT * (4 / WM);
   const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM), (unsigned)a.splits);
-  tw_gemm<WL, AL, EPI, WM, MT, NT, NB, ONE><<<grid, kThreads, 0, st>>>(a);
+  tw_gemm<WL, AL, EPI, WM, MT, NT, NB><<<grid, kThreads, 0, st>>>(a);
+  if (a.splits > 1) {
+    const long total = (long)a.M * a.N;
+    constexpr int SHIFT = WTraits<WL>::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0);
+    tw_reduce<EPI><<<(unsigned)((total + kThreads - 1) / kThreads), kThreads, 0, st>>>(a, SHIFT);
+  }
+}
+
+// LDS bytes of a tw_gemm_ring launch: D slots, and the junk KiB per wave when
+// a step's blocks do not divide evenly over the four waves
+template <int WL, int AL, int WM, int MT, int NT, int KS, int D>
+constexpr size_t ring_lds_bytes() {
+  constexpr int TM = 16 * MT * WM, TN = 16 * NT * (4 / WM);
+  constexpr int SUB = WTraits<WL>::rows(TN) * WTraits<WL>::row_bytes(TN) + TM * a_row_bytes(WL, AL);
+  return (size_t)D * KS * SUB + ((SUB / 1024) % 4 ? 4096 : 0);
+}
+
+template <int WL, int AL, int EPI, int WM, int MT, int NT, int KS, int D>
+void launch_ring_t(const TwArgs& a, hipStream_t st) {
+  constexpr int TM = 16 * MT * WM, TN = 16 * NT * (4 / WM);
+  constexpr size_t lds = ring_lds_bytes<WL, AL, WM, MT, NT, KS, D>();
+  static_assert(lds <= kStreamLdsMax, "ring exceeds the LDS budget");
+  if constexpr (lds > 64 * 1024) allow_dynamic_lds<tw_gemm_ring<WL, AL, EPI, WM, MT, NT, KS, D>>();
+  const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM), (unsigned)a.splits);
+  tw_gemm_ring<WL, AL, EPI, WM, MT, NT, KS, D><<<grid, kThreads, lds, st>>>(a);
   if (a.splits > 1) {
     const long total = (long)a.M * a.N;
     constexpr int SHIFT = WTraits<WL>::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0);
@@ -550,11 +874,11 @@ void launch_gemm_t(const TwArgs& a, hipStream_t st) {
 
 template <int WL, int AL, int EPI>
 void launch_gemm_g(const TwArgs& a, const Geometry& g, hipStream_t st) {
-  // large-M batch: two halves of NBL steps stay within 64 KiB of LDS
-  constexpr int NBL = (WL == ACTUNE_TW_KMAJOR_W8 || WL == ACTUNE_TW_KMAJOR_W2) ? 2 : 3;
-  if (g.wm == 1) launch_gemm_t<WL, AL, EPI, 1, 1, 2, (WL == ACTUNE_TW_KMAJOR_W8 ? 4 : 8), true>(a, st);
-  else if (g.nt == 2) launch_gemm_t<WL, AL, EPI, 2, 2, 2, NBL, false>(a, st);
-  else launch_gemm_t<WL, AL, EPI, 2, 2, 4, NBL, false>(a, st);
+  constexpr bool KM = WTraits<WL>::KM;
+  if (g.wm == 1) launch_gemm_t<WL, AL, EPI, 1, 1, 2, (WL == ACTUNE_TW_KMAJOR_W8 ? 4 : 8)>(a, st);
+  else if (g.d == 3) launch_ring_t<WL, AL, EPI, 2, 2, 4, KM ? 1 : 2, 3>(a, st);
+  else if constexpr (KM) launch_ring_t<WL, AL, EPI, 2, 2, 4, 2, 4>(a, st);
+  else launch_ring_t<WL, AL, EPI, 2, 2, 2, 2, 4>(a, st);
 }
 
 // the six (weight layout, activation layout) pairs of the reference family

@@ -368,14 +368,17 @@ def bench_ceilings(torch):
       waves per SIMD: kind 0 = the library's int8 16x16x64 MFMA + per-group
       cvt/fma rescale, kind 1 = exact fp8 32x32x64 MFMA for W, A <= 4 (one fma per
       output after an offset-correction MFMA), kind 2 = the same for A8 as two
-      hi/lo planes, kind 3 = kind 1 with the correction taken for free."""
+      hi/lo planes, kind 3 = kind 1 with the correction taken for free, kind 4 =
+      kind 0 on int8 32x32x32 MFMAs (the 16x16x64 form issues at half the int8
+      rate on gfx950), kinds 5 / 6 = 16x16x64 / 32x32x32 int8 MFMAs alone."""
     import ctypes
     from actune_amd import build as _build
     lib = ctypes.CDLL(str(_build.CEILING_LIB))
     lib.actune_ceiling_run.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                        ctypes.c_void_p]
     lib.actune_ceiling_macs_per_iter.restype = ctypes.c_long
-    words, macs = lib.actune_ceiling_words(), lib.actune_ceiling_macs_per_iter()
+    lib.actune_ceiling_macs_per_iter.argtypes = [ctypes.c_int]
+    words = lib.actune_ceiling_words()
     out = {}
     x = torch.zeros(1, device="cuda")
 
@@ -389,8 +392,11 @@ def bench_ceilings(torch):
     kinds = {0: "int8 16x16x64 + cvt/fma rescale (gemm_prefill's loop)",
              1: "fp8 32x32x64, W,A <= 4, exact (offset-correction MFMA + fma)",
              2: "fp8 32x32x64, A8 as hi/lo planes, exact",
-             3: "fp8 32x32x64, W,A <= 4, correction for free (unreachable bound)"}
-    iters, st = 400, torch.cuda.current_stream()
+             3: "fp8 32x32x64, W,A <= 4, correction for free (unreachable bound)",
+             4: "int8 32x32x32 + cvt/fma rescale",
+             5: "int8 16x16x64 MFMAs alone",
+             6: "int8 32x32x32 MFMAs alone"}
+    iters, st = 4000, torch.cuda.current_stream()
     ceil = {}
     for waves_per_simd in (2, 4):
         blocks = 256 * waves_per_simd  # 4 waves per workgroup, one per SIMD
@@ -408,6 +414,7 @@ def bench_ceilings(torch):
             run(iters)
             e1.record()
             torch.cuda.synchronize()
+            macs = lib.actune_ceiling_macs_per_iter(kind)
             tops = 2 * macs * blocks * 4 * iters / (e0.elapsed_time(e1) * 1e-3) / 1e12
             ceil.setdefault(label, {})[f"{waves_per_simd}_waves_per_simd"] = dict(
                 TOPS=round(tops, 1), frac=round(tops / INT8_PEAK_TOPS, 4))
