@@ -193,16 +193,18 @@ __global__ __launch_bounds__(256) void ceiling_mfma(const uint32_t* in, float* o
   v4i a = v4i{(int)s[0], (int)s[1], (int)s[2], (int)s[3]}, b = v4i{(int)s[4], (int)s[5], (int)s[6], (int)s[7]};
   int t = 0;
   if constexpr (M32) {
-    v16i c[8];
-    for (int j = 0; j < 8; ++j)
+    // four accumulators of 16 registers (eight would hold 128 VGPRs and cap
+    // the occupancy), two MFMAs each per iteration
+    v16i c[4];
+    for (int j = 0; j < 4; ++j)
       for (int r = 0; r < 16; ++r) c[j][r] = 0;
     for (int it = 0; it < iters; ++it) {
       ACT_OPAQUE(a);
       ACT_OPAQUE(b);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c[j], 0, 0, 0);
+      for (int j = 0; j < 8; ++j) c[j & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c[j & 3], 0, 0, 0);
     }
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < 4; ++j)
       for (int r = 0; r < 16; ++r) t += c[j][r];
   } else {
     v4i c[16];
