@@ -55,6 +55,8 @@ def lib():
         so.actune_tokenwise_workspace_bytes.restype = _I64
         so.actune_tokenwise_linear.argtypes = [_P, _I, _P, _P, _I, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I, _P,
                                                _I64, _P]
+        so.actune_tokenwise_linear_x.argtypes = [_P, _I, _P, _P, _I, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I,
+                                                 _P, _I64, _P]
         so.actune_forward_fuses_quantizer.argtypes = [_I64, _I64, _I64, _I, _I, _I, _I]
         so.actune_config_valid.argtypes = [_I, _I64]
         so.actune_default_config.argtypes = [_I64, _I64, _I64, _I, _I]
@@ -357,6 +359,37 @@ def tokenwise_workspace_bytes(m, n, k, w_layout, a_layout):
     if need < 0:
         raise ValueError(lib().actune_last_error().decode())
     return need
+
+
+def tokenwise_linear_x(x, as_out, w, w_layout, ws, bias, n, k, epilogue, out, workspace=None):
+    """One row of x ([1, K] bf16 / f16 / f32) quantized to A8 inside the GEMM
+    launch (actune_tokenwise_linear_x): the result of tokenwise_quantize(x, 8)
+    followed by tokenwise_linear on its codes, bit for bit. as_out: float32
+    [1], receives the row's activation scale; w: a K-major layout; workspace
+    as for tokenwise_linear with A8 activations."""
+    _require_cuda(x, as_out, w, ws, bias, out, workspace)
+    if x.dim() != 2 or x.shape[0] != 1 or x.shape[1] != k:
+        raise RuntimeError("fused quantization takes x of shape [1, K]")
+    if not (x.is_contiguous() and w.is_contiguous() and ws.is_contiguous()
+            and (bias is None or bias.is_contiguous())):
+        raise RuntimeError("contiguous operands required")
+    if as_out.dtype != torch.float32 or ws.dtype != torch.float32:
+        raise RuntimeError("float scales/bias required")
+    if as_out.numel() != 1 or not as_out.is_contiguous() or ws.numel() != n or (bias is not None and bias.numel() != n):
+        raise RuntimeError("scale shape mismatch")
+    wbytes = {TW_KMAJOR_W8: k * n, TW_KMAJOR_W4: k // 2 * n, TW_KMAJOR_W2: k // 4 * n}.get(w_layout)
+    if wbytes is None:
+        raise RuntimeError("fused quantization takes the K-major (A8) weight layouts")
+    if w.numel() != wbytes or w.element_size() != 1:
+        raise RuntimeError("packed weight shape mismatch")
+    _check_buffer(out, "out", (1, n), out.dtype, x.device)
+    need = tokenwise_workspace_bytes(1, n, k, w_layout, TW_ACT_A8)
+    if need and (workspace is None or workspace.numel() < need or workspace.dtype != torch.uint8):
+        raise RuntimeError(f"workspace of at least {need} bytes required")
+    _check(lib().actune_tokenwise_linear_x(
+        _ptr(x), _dtype_code(x), _ptr(as_out), _ptr(w), w_layout, _ptr(ws), _ptr(bias), _bias_code(bias), _ptr(out),
+        _dtype_code(out), 1, n, k, epilogue, _ptr(workspace) if need else None, need, _stream(x.device)))
+    return out
 
 
 def tokenwise_linear(a, a_layout, as_, w, w_layout, ws, bias, n, k, epilogue, out, workspace=None):

@@ -54,6 +54,8 @@ namespace actune {
 namespace {
 
 constexpr int kThreads = 256;
+// longest row the fused-quantization launch takes (8 passes of 8 elements per thread)
+constexpr int kTwFusedMaxK = 16384;
 
 template <int WL> struct WTraits;
 // U: MFMAs per K-step (64 k each); TW: shift of the weight codes;
@@ -102,7 +104,8 @@ constexpr int a_stride(int wl, int al) { return al == ACTUNE_TW_ACT_A4 ? 40 : a_
 
 struct TwArgs {
   const uint8_t* a;     // int8 codes [M, K] or packed A4 [M, K/2]
-  const float* as;      // [M]
+  const void* x;        // activation rows [M, K] (fused quantization; a unused)
+  const float* as;      // [M] (fused quantization: written by the launch)
   const uint8_t* w;     // weight buffer (layout WL)
   const float* ws;      // [N]
   const void* bias;     // [N] or nullptr
@@ -197,7 +200,16 @@ constexpr int align_of_stride(int s) { return s % 16 == 0 ? 16 : (s % 8 == 0 ? 8
 // finishes). A workgroup's whole K-range (at most NB K-steps: the host splits
 // K until it is) is loaded at entry, every load in flight at once, staged into
 // NB LDS buffers and computed after one barrier.
-template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB>
+//
+// XDT >= 0 (fused quantization, one row of A8): the launch reads the row x of
+// dtype XDT instead of codes. Every workgroup loads the whole row for its
+// amax (first, so that the in-order memory counter lets the amax finish
+// before the weights land), then its K-range of x, then its weights; it
+// computes the row scale s = fl(max(amax, 1e-8) * fl(1/127)) and the codes
+// rint(v / s) clamped to [-128, 127] exactly as tw_quantize_kernel does, and
+// stages the codes as the activation tile. The first workgroup writes s to
+// args.as (the integer reduce reads it).
+template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, int XDT = -1>
 __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   using T = WTraits<WL>;
   constexpr int WN = 4 / WM;
@@ -211,6 +223,11 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   constexpr int NBUF = NB;
   static_assert(NBUF * (WBUF + ABUF) <= 64 * 1024, "LDS tile buffers exceed 64 KiB");
   __shared__ __align__(16) uint8_t smem[NBUF * (WBUF + ABUF)];
+
+  constexpr bool FX = XDT >= 0;
+  static_assert(!FX || (AL == ACTUNE_TW_ACT_A8 && TM == 16 && T::KM), "fused quantization: A8, 16-row tiles");
+  constexpr int XSZ = XDT == kF32 ? 4 : 2;  // bytes per x element
+  constexpr int XRC = kTwFusedMaxK / (kThreads * 8);  // amax passes of 8 elements per thread
 
   const int M = args.M, N = args.N, K = args.K;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -228,7 +245,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   else wbytes = (uint32_t)N * (K / 4);
   const uint32_t arow = AL == ACTUNE_TW_ACT_A4 ? (uint32_t)K / 2 : (uint32_t)K;
   const Rsrc wr = make_rsrc(args.w, wbytes);
-  const Rsrc ar = make_rsrc(args.a, (uint32_t)M * arow);
+  const Rsrc ar = FX ? make_rsrc(args.x, (uint32_t)K * XSZ) : make_rsrc(args.a, (uint32_t)M * arow);
 
   // Per-thread base offsets of its weight / activation chunks (step 0) and
   // the per-step byte strides, all 32-bit: a step's loads are then one add
@@ -258,7 +275,9 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
     else if constexpr (WL == ACTUNE_TW_KMAJOR_W4) k = (uint32_t)(cb >> 1) * (K / 2) + 16 * (cb & 1);
     else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) k = (uint32_t)(cb >> 1) * (K / 4) + 16 * (cb & 1);
     else k = 16 * cb;
-    abase[i] = live ? (uint32_t)(m0 + row) * arow + k : kOff;
+    // fused: byte offset of element k of the row (row 0 only)
+    if constexpr (FX) abase[i] = live && row == 0 ? k * XSZ : kOff;
+    else abase[i] = live ? (uint32_t)(m0 + row) * arow + k : kOff;
   }
   constexpr uint32_t astep = (AL == ACTUNE_TW_ACT_A4 || WL == ACTUNE_TW_KMAJOR_W4 || WL == ACTUNE_TW_KMAJOR_W2) ? 32 : 64;
 
@@ -273,15 +292,18 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
     for (int i = 0; i < NAC; ++i)
       areg[i] = __builtin_amdgcn_raw_buffer_load_b128(ar, abase[i] == kOff ? kOff : abase[i] + (uint32_t)g * astep, soff, 0);
   };
-  auto stage = [&](int buf, const v4u (&wreg)[NWC], const v4u (&areg)[NAC]) {
+  auto stage_w = [&](int buf, const v4u (&wreg)[NWC]) {
     uint8_t* wt = smem + buf * (WBUF + ABUF);
-    uint8_t* at = wt + WBUF;
 #pragma unroll
     for (int i = 0; i < NWC; ++i) {
       const int c = tid + i * kThreads;
       if (WCH % kThreads == 0 || c < WCH)
         lds_store16<align_of_stride(WSTR)>(wt + (c / (WRB / 16)) * WSTR + 16 * (c % (WRB / 16)), wreg[i]);
     }
+  };
+  auto stage = [&](int buf, const v4u (&wreg)[NWC], const v4u (&areg)[NAC]) {
+    uint8_t* at = smem + buf * (WBUF + ABUF) + WBUF;
+    stage_w(buf, wreg);
 #pragma unroll
     for (int i = 0; i < NAC; ++i) {
       const int c = tid + i * kThreads;
@@ -363,15 +385,107 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   // every step of the K-range at once (steps past g1 load zeros and add
   // nothing, so the batch is straight-line code with no bounds tests)
   v4u wreg[NB][NWC], areg[NB][NAC];
+  TwArgs fin = args;
+  if constexpr (FX) {
+    __shared__ float xs[kThreads / 64 + 1];
+    // 1. the row for its amax, 2. this workgroup's K-range of x (EPT
+    // consecutive elements per thread), 3. the weights
+    float xm[XRC][8];
 #pragma unroll
-  for (int i = 0; i < NB; ++i) issue(g0 + i, wreg[i], areg[i]);
+    for (int p = 0; p < XRC; ++p) {
+      const int e = p * kThreads * 8 + tid * 8;
+      buffer_load8<XDT>(ar, e < K ? (uint32_t)e * XSZ : kOff, xm[p]);
+    }
+    // thread tid: bytes b .. b + EPT - 1 of staged row 0 of step i (inside
+    // one 16-byte chunk, so at consecutive k)
+    constexpr int EPT = NB * ARB / kThreads;
+    static_assert(EPT == 1 || EPT == 2 || EPT == 4, "fused slice: 1, 2 or 4 elements per thread");
+    const int fi = tid * EPT / ARB, fb = tid * EPT % ARB, fc = fb / 16;
+    uint32_t kx;
+    if constexpr (WL == ACTUNE_TW_KMAJOR_W4) kx = (uint32_t)(fc >> 1) * (K / 2) + 16 * (fc & 1);
+    else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) kx = (uint32_t)(fc >> 1) * (K / 4) + 16 * (fc & 1);
+    else kx = 16 * fc;
+    kx += (uint32_t)(fb % 16) + (uint32_t)(g0 + fi) * astep;
+    const uint32_t xoff = g0 + fi < g1 ? kx * XSZ : kOff;
+    float xv[EPT];
+    if constexpr (EPT * XSZ == 16) {
+      const v4u q = __builtin_amdgcn_raw_buffer_load_b128(ar, xoff, 0, 0);
+      if constexpr (XSZ == 4) {
 #pragma unroll
-  for (int i = 0; i < NB; ++i) stage(i, wreg[i], areg[i]);
+        for (int e = 0; e < 4; ++e) xv[e] = __uint_as_float(q[e]);
+      } else {
+        float v8[8];
+        unpack8<XDT>(q, q, v8);
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) xv[e] = v8[e];
+      }
+    } else {
+      uint32_t q[2] = {0u, 0u};
+      if constexpr (EPT * XSZ == 8) {
+        const v2u t = __builtin_amdgcn_raw_buffer_load_b64(ar, xoff, 0, 0);
+        q[0] = t[0]; q[1] = t[1];
+      } else if constexpr (EPT * XSZ == 4) {
+        q[0] = __builtin_amdgcn_raw_buffer_load_b32(ar, xoff, 0, 0);
+      } else {
+        q[0] = __builtin_amdgcn_raw_buffer_load_b16(ar, xoff, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        if constexpr (XSZ == 4) xv[e] = __uint_as_float(q[e]);
+        else {
+          const uint16_t h = (uint16_t)(q[e / 2] >> (16 * (e % 2)));
+          xv[e] = XDT == kBF16 ? bf16_to_f32(h) : f16_to_f32(h);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const uint32_t soff = g0 + i < g1 ? 0u : kOff;
+#pragma unroll
+      for (int c = 0; c < NWC; ++c)
+        wreg[i][c] = __builtin_amdgcn_raw_buffer_load_b128(
+            wr, wbase[c] == kOff ? kOff : wbase[c] + (uint32_t)(g0 + i) * wstep, soff, 0);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int p = 0; p < XRC; ++p)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(xm[p][e]));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if (lane == 0) xs[wave] = amax;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) amax = fmaxf(amax, xs[w]);
+    const float sc = fmaxf(amax, 1e-8f) * (1.0f / 127.0f);
+    if (tid == 0) {
+      xs[kThreads / 64] = sc;
+      if (blockIdx.x == 0 && z == 0) const_cast<float*>(args.as)[0] = sc;
+    }
+    // this thread's codes into row 0 of step fi's activation tile (out of
+    // range steps hold x = 0: code 0; rows 1-15 are never stored)
+    uint32_t cw = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+      cw |= ((uint32_t)(int)fminf(fmaxf(rintf(xv[e] / sc), -128.0f), 127.0f) & 0xffu) << (8 * e);
+    uint8_t* dst = smem + fi * (WBUF + ABUF) + WBUF + fb;
+    if constexpr (EPT == 4) *reinterpret_cast<uint32_t*>(dst) = cw;
+    else if constexpr (EPT == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)cw;
+    else *dst = (uint8_t)cw;
+    fin.as = &xs[kThreads / 64];  // the epilogue of an unsplit launch reads s from LDS
+#pragma unroll
+    for (int i = 0; i < NB; ++i) stage_w(i, wreg[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) issue(g0 + i, wreg[i], areg[i]);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) stage(i, wreg[i], areg[i]);
+  }
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < NB; ++i) compute(i);
 
-  finish_tile<WL, AL, EPI, MT, NT>(args, acc, m0 + wm * 16 * MT + 4 * kb, n0 + wn * 16 * NT + r16, z);
+  finish_tile<WL, AL, EPI, MT, NT>(fin, acc, m0 + wm * 16 * MT + 4 * kb, n0 + wn * 16 * NT + r16, z);
 }
 
 // ------------------------------------------------------------ LDS-DMA ring
@@ -836,11 +950,11 @@ int pick_splits(int64_t M, int64_t N, int64_t K, int wl, const Geometry& g) {
   return (int)s;
 }
 
-template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB>
+template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, int XDT = -1>
 void launch_gemm_t(const TwArgs& a, hipStream_t st) {
   constexpr int TM = 16 * MT * WM, TN = 16 * NT * (4 / WM);
   const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM), (unsigned)a.splits);
-  tw_gemm<WL, AL, EPI, WM, MT, NT, NB><<<grid, kThreads, 0, st>>>(a);
+  tw_gemm<WL, AL, EPI, WM, MT, NT, NB, XDT><<<grid, kThreads, 0, st>>>(a);
   if (a.splits > 1) {
     const long total = (long)a.M * a.N;
     constexpr int SHIFT = WTraits<WL>::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0);
@@ -879,6 +993,26 @@ void launch_gemm_g(const TwArgs& a, const Geometry& g, hipStream_t st) {
   else if (g.d == 3) launch_ring_t<WL, AL, EPI, 2, 2, 4, KM ? 1 : 2, 3>(a, st);
   else if constexpr (KM) launch_ring_t<WL, AL, EPI, 2, 2, 4, 2, 4>(a, st);
   else launch_ring_t<WL, AL, EPI, 2, 2, 2, 2, 4>(a, st);
+}
+
+// one A8 row quantized inside the GEMM launch (small-M geometry, 16 x 128 tiles)
+template <int WL, int EPI, int XDT>
+void launch_fused_t(const TwArgs& a, hipStream_t st) {
+  launch_gemm_t<WL, ACTUNE_TW_ACT_A8, EPI, 1, 1, 2, (WL == ACTUNE_TW_KMAJOR_W8 ? 4 : 8), XDT>(a, st);
+}
+
+void launch_fused(int wl, int epi, int xdt, const TwArgs& a, hipStream_t st) {
+#define TWF(W_, E_)                                                      \
+  if (wl == W_ && epi == E_) {                                           \
+    if (xdt == kBF16) launch_fused_t<W_, E_, kBF16>(a, st);              \
+    else if (xdt == kF16) launch_fused_t<W_, E_, kF16>(a, st);           \
+    else launch_fused_t<W_, E_, kF32>(a, st);                            \
+    return;                                                              \
+  }
+  TWF(ACTUNE_TW_KMAJOR_W8, ACTUNE_TW_EPI_A8) TWF(ACTUNE_TW_KMAJOR_W8, ACTUNE_TW_EPI_A4)
+  TWF(ACTUNE_TW_KMAJOR_W4, ACTUNE_TW_EPI_A8) TWF(ACTUNE_TW_KMAJOR_W4, ACTUNE_TW_EPI_A4)
+  TWF(ACTUNE_TW_KMAJOR_W2, ACTUNE_TW_EPI_A8) TWF(ACTUNE_TW_KMAJOR_W2, ACTUNE_TW_EPI_A4)
+#undef TWF
 }
 
 // the six (weight layout, activation layout) pairs of the reference family
@@ -971,11 +1105,16 @@ int64_t actune_tokenwise_workspace_bytes(int64_t M, int64_t N, int64_t K, int w_
   return S == 1 ? 0 : (int64_t)S * M * N * 4;
 }
 
-int actune_tokenwise_linear(const void* a, int a_layout, const float* a_scales, const void* w, int w_layout,
-                            const float* w_scale, const void* bias, int bias_dtype, void* out, int out_dtype,
-                            int64_t M, int64_t N, int64_t K, int epilogue, void* workspace,
-                            int64_t workspace_bytes, void* stream) {
-  set_last_error("");
+}  // extern "C"
+
+namespace actune {
+namespace {
+
+// Checks shared by the two linear entry points and the launch arguments;
+// act is the codes (a) or the row (x) pointer, checked for 16-byte alignment.
+int prepare_linear(TwArgs& args, const void* act, int a_layout, const float* a_scales, const void* w, int w_layout,
+                   const float* w_scale, const void* bias, int bias_dtype, void* out, int out_dtype, int64_t M,
+                   int64_t N, int64_t K, int epilogue, void* workspace, int64_t workspace_bytes) {
   int rc = check_tw_shape(M, N, K, w_layout, a_layout);
   if (rc) return rc;
   if (epilogue != ACTUNE_TW_EPI_A8 && epilogue != ACTUNE_TW_EPI_A4) return fail("unknown epilogue");
@@ -983,13 +1122,12 @@ int actune_tokenwise_linear(const void* a, int a_layout, const float* a_scales, 
       (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32))
     return fail("unsupported output/bias dtype");
   if (M == 0) return ACTUNE_OK;
-  if (!a || !a_scales || !w || !w_scale || !out) return fail("null pointer");
-  if (((uintptr_t)a % 16) || ((uintptr_t)w % 16) || ((uintptr_t)a_scales % 4) || ((uintptr_t)w_scale % 4))
+  if (!act || !a_scales || !w || !w_scale || !out) return fail("null pointer");
+  if (((uintptr_t)act % 16) || ((uintptr_t)w % 16) || ((uintptr_t)a_scales % 4) || ((uintptr_t)w_scale % 4))
     return fail("misaligned operand (packed data needs 16 B)");
   const Geometry g = pick_geometry(M, N, w_layout);
   const int S = pick_splits(M, N, K, w_layout, g);
-  TwArgs args{};
-  args.a = static_cast<const uint8_t*>(a);
+  args = TwArgs{};
   args.as = a_scales;
   args.w = static_cast<const uint8_t*>(w);
   args.ws = w_scale;
@@ -1009,13 +1147,53 @@ int actune_tokenwise_linear(const void* a, int a_layout, const float* a_scales, 
     if (need >= ((int64_t)1 << 31)) return fail("split-K partials too large");
     args.partial = static_cast<int32_t*>(workspace);
   }
-  launch_gemm(w_layout, a_layout, epilogue, args, g, (hipStream_t)stream);
+  return ACTUNE_OK;
+}
+
+int launch_status() {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_last_error(hipGetErrorString(e));
     return ACTUNE_ERR_DEVICE;
   }
   return ACTUNE_OK;
+}
+
+}  // namespace
+}  // namespace actune
+
+extern "C" {
+
+int actune_tokenwise_linear(const void* a, int a_layout, const float* a_scales, const void* w, int w_layout,
+                            const float* w_scale, const void* bias, int bias_dtype, void* out, int out_dtype,
+                            int64_t M, int64_t N, int64_t K, int epilogue, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  set_last_error("");
+  TwArgs args;
+  const int rc = prepare_linear(args, a, a_layout, a_scales, w, w_layout, w_scale, bias, bias_dtype, out, out_dtype,
+                                M, N, K, epilogue, workspace, workspace_bytes);
+  if (rc || M == 0) return rc;
+  args.a = static_cast<const uint8_t*>(a);
+  launch_gemm(w_layout, a_layout, epilogue, args, pick_geometry(M, N, w_layout), (hipStream_t)stream);
+  return launch_status();
+}
+
+int actune_tokenwise_linear_x(const void* x, int x_dtype, float* a_scales, const void* w, int w_layout,
+                              const float* w_scale, const void* bias, int bias_dtype, void* out, int out_dtype,
+                              int64_t M, int64_t N, int64_t K, int epilogue, void* workspace,
+                              int64_t workspace_bytes, void* stream) {
+  set_last_error("");
+  if (x_dtype != kBF16 && x_dtype != kF16 && x_dtype != kF32) return fail("unsupported activation dtype");
+  if (w_layout > ACTUNE_TW_KMAJOR_W2) return fail("fused quantization takes the K-major (A8) weight layouts");
+  if (M != 1) return fail("fused quantization takes one row (M = 1)");
+  if (K > kTwFusedMaxK) return fail("fused quantization takes in_features <= 16384");
+  TwArgs args;
+  const int rc = prepare_linear(args, x, ACTUNE_TW_ACT_A8, a_scales, w, w_layout, w_scale, bias, bias_dtype, out,
+                                out_dtype, M, N, K, epilogue, workspace, workspace_bytes);
+  if (rc) return rc;
+  args.x = x;
+  launch_fused(w_layout, epilogue, x_dtype, args, (hipStream_t)stream);
+  return launch_status();
 }
 
 }  // extern "C"

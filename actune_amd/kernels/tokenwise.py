@@ -546,6 +546,10 @@ class W8A4NativeLinear(torch.nn.Module):
 
 
 # ---------------------------------------------------------------- exact split-K decode
+# longest row the GEMM launch quantizes itself (actune_tokenwise_linear_x)
+_FUSED_MAX_K = 16384
+
+
 class _WorkspaceOwner:
     pass
 
@@ -620,7 +624,10 @@ class DecodeGraphPlan:
     """Replay the fixed decode launch sequence (per-row quantizer, then one
     split-K GEMM per projection) from a hipGraph with private staging
     buffers; inputs are copied in and outputs cloned on every call
-    (decode_w4a8_triton.py:326-425)."""
+    (decode_w4a8_triton.py:326-425). Where the row fits it
+    (in_features <= 16384), each projection's split GEMM quantizes the row
+    itself (actune_tokenwise_linear_x): two launches per projection and no
+    quantizer launch, with the same codes and outputs."""
 
     def __init__(self, value, weights, residuals, scales, biases):
         for r in residuals:
@@ -634,8 +641,9 @@ class DecodeGraphPlan:
         self.n = weights[0].shape[1]
         self.groups = len(weights)
         dev = value.device
+        self.fused = self.k <= _FUSED_MAX_K and value.dtype in (torch.bfloat16, torch.float16, torch.float32)
         self.input = torch.empty((1, self.k), device=dev, dtype=value.dtype)
-        self.activation = torch.empty_like(self.input, dtype=torch.int8)
+        self.activation = None if self.fused else torch.empty_like(self.input, dtype=torch.int8)
         self.scale = torch.empty(1, device=dev, dtype=torch.float32)
         self.output = torch.empty((self.groups, self.n), device=dev, dtype=value.dtype)
         self.outputs = tuple(self.output[i:i + 1] for i in range(self.groups))
@@ -656,18 +664,24 @@ class DecodeGraphPlan:
         current.wait_stream(stream)
 
     def _launch(self):
-        _native.tokenwise_quantize(self.input, 8, self.activation, self.scale)
+        if not self.fused:
+            _native.tokenwise_quantize(self.input, 8, self.activation, self.scale)
         step = max(self._need, 256)
         for i in range(self.groups):
             ws = self.partial[i * step:(i + 1) * step] if self._need else None
-            _native.tokenwise_linear(self.activation, _native.TW_ACT_A8, self.scale, self.weights[i],
-                                     _native.TW_KMAJOR_W4, self.scales[i], self.biases[i], self.n, self.k,
-                                     _native.TW_EPI_A8, self.outputs[i], workspace=ws)
+            if self.fused:
+                _native.tokenwise_linear_x(self.input, self.scale, self.weights[i], _native.TW_KMAJOR_W4,
+                                           self.scales[i], self.biases[i], self.n, self.k, _native.TW_EPI_A8,
+                                           self.outputs[i], workspace=ws)
+            else:
+                _native.tokenwise_linear(self.activation, _native.TW_ACT_A8, self.scale, self.weights[i],
+                                         _native.TW_KMAJOR_W4, self.scales[i], self.biases[i], self.n, self.k,
+                                         _native.TW_EPI_A8, self.outputs[i], workspace=ws)
 
     @property
     def workspace_bytes(self):
         return sum(t.numel() * t.element_size()
-                   for t in (self.input, self.activation, self.scale, self.output, self.partial))
+                   for t in (self.input, self.activation, self.scale, self.output, self.partial) if t is not None)
 
     def run(self, value):
         with self.lock:

@@ -432,7 +432,8 @@ def bench_tokenwise(torch, _native, steps, warmup):
     row-major S4 / S2). M=1 and M=8 on the Llama-2-7B shapes for W4A8 (the
     reference's decode use), rotating over >= 256 MB of distinct weights,
     and M=512 for every pair (the MFMA-bound case: the int32 accumulator
-    needs no per-group rescale). Each launch pair = quantizer + GEMM."""
+    needs no per-group rescale). Each launch pair = quantizer + GEMM; at M=1
+    also the GEMM that quantizes the row itself (us_quantizer_fused)."""
     layouts = {"W4A8": _native.TW_KMAJOR_W4, "W8A8": _native.TW_KMAJOR_W8, "W2A8": _native.TW_KMAJOR_W2,
                "W4A4": _native.TW_ROWS_S4, "W2A4": _native.TW_ROWS_S2, "W8A4": _native.TW_KMAJOR_W8}
     g = torch.Generator(device="cuda").manual_seed(6)
@@ -460,13 +461,21 @@ def bench_tokenwise(torch, _native, steps, warmup):
                 _native.tokenwise_quantize(x, A, act, sc)
                 _native.tokenwise_linear(act, al, sc, w, wl, s, None, n, k, epi, y, workspace=work if need else None)
 
+        def fused():  # one row quantized inside the split GEMM (A8 layouts)
+            for w, s in ws:
+                _native.tokenwise_linear_x(x, sc, w, wl, s, None, n, k, epi, y, workspace=work if need else None)
+
         us = time_launches(torch, gemm_only, steps, warmup) / copies
         us_q = time_launches(torch, with_quant, steps, warmup) / copies
+        us_f = time_launches(torch, fused, steps, warmup) / copies if m == 1 and A == 8 else None
         del ws
         tops = 2 * m * n * k / us / 1e6
-        return dict(us=round(us, 2), us_with_quantizer=round(us_q, 2), weight_GBps=round(nbytes / us / 1e3, 1),
-                    TOPS=round(tops, 1), frac_hbm=round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4),
-                    frac_int8=round(tops / INT8_PEAK_TOPS, 4))
+        row = dict(us=round(us, 2), us_with_quantizer=round(us_q, 2), weight_GBps=round(nbytes / us / 1e3, 1),
+                   TOPS=round(tops, 1), frac_hbm=round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4),
+                   frac_int8=round(tops / INT8_PEAK_TOPS, 4))
+        if us_f is not None:
+            row["us_quantizer_fused"] = round(us_f, 2)
+        return row
 
     for m in (1, 8):
         row = {}

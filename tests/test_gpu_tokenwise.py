@@ -209,3 +209,81 @@ def test_launch_decode_into_caller_buffers():
     with T.decode_optimization_scope(enabled=False):
         want = mod(x)
     assert torch.equal(out, want)
+
+
+# ---------------------------------------------------------------- fused one-row quantization
+def _kmajor_weights(n, k, W, seed):
+    w = torch.from_numpy(np.random.default_rng(seed).standard_normal((n, k)).astype(np.float32))
+    codes, scale = O.weight_codes(w.numpy(), W, 8, gpu_division=True)
+    return torch.from_numpy(O.pack_kmajor(codes, W)).to(DEV), torch.from_numpy(scale).to(DEV)
+
+
+@pytest.mark.parametrize("W,wl", [(4, _native.TW_KMAJOR_W4), (8, _native.TW_KMAJOR_W8), (2, _native.TW_KMAJOR_W2)])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (11008, 4096), (4096, 11008), (256, 2048), (48, 256), (32, 96),
+                                 (128, 16384)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_fused_row_quantization_equals_two_step(W, wl, n, k, dtype):
+    """actune_tokenwise_linear_x (the row quantized inside the split GEMM)
+    gives the quantizer + linear result bit for bit, scale included."""
+    if k % {4: 32, 8: 64, 2: 128}[W]:
+        pytest.skip("in_features not allowed for this layout")
+    w, ws = _kmajor_weights(n, k, W, seed=n + k + W)
+    bias = torch.randn(n, device=DEV).to(dtype) if n % 3 == 0 else None
+    x = (torch.randn(1, k, device=DEV) * 3).to(dtype)
+    act, s = _native.tokenwise_quantize(x, 8)
+    need = _native.tokenwise_workspace_bytes(1, n, k, wl, _native.TW_ACT_A8)
+    ws_buf = torch.full((max(need, 1),), 0x5A, dtype=torch.uint8, device=DEV)
+    want = torch.empty(1, n, device=DEV, dtype=dtype)
+    _native.tokenwise_linear(act, _native.TW_ACT_A8, s, w, wl, ws, bias, n, k, _native.TW_EPI_A8, want,
+                             workspace=ws_buf if need else None)
+    got = torch.full((1, n), 3.0, device=DEV, dtype=dtype)
+    s_out = torch.full((1,), -1.0, device=DEV)
+    for _ in range(2):  # repeated calls on the same buffers
+        _native.tokenwise_linear_x(x, s_out, w, wl, ws, bias, n, k, _native.TW_EPI_A8, got,
+                                   workspace=ws_buf if need else None)
+    torch.cuda.synchronize()
+    assert torch.equal(s_out, s)
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("scale", [0.0, 1e-30, 1e-4, 1e3])
+def test_fused_row_quantization_magnitudes_against_oracle(scale):
+    """Zero, subnormal-scale, small and large rows through the fused launch,
+    against the CPU oracle (per-row codes, exact dots, epilogue)."""
+    n, k = 256, 4096
+    rng = np.random.default_rng(11)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    codes, wscale = O.weight_codes(w, 4, 8, gpu_division=True)
+    x = torch.from_numpy((rng.standard_normal((1, k)) * scale).astype(np.float32)).to(torch.bfloat16)
+    out = torch.empty(1, n, device=DEV, dtype=torch.bfloat16)
+    s_out = torch.empty(1, device=DEV)
+    need = _native.tokenwise_workspace_bytes(1, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8)
+    ws_buf = torch.empty(max(need, 1), dtype=torch.uint8, device=DEV)
+    _native.tokenwise_linear_x(x.to(DEV), s_out, torch.from_numpy(O.pack_kmajor(codes, 4)).to(DEV),
+                               _native.TW_KMAJOR_W4, torch.from_numpy(wscale).to(DEV), None, n, k,
+                               _native.TW_EPI_A8, out, workspace=ws_buf if need else None)
+    a_codes, a_scales = O.tw_quantize_rows(bits(x), 8)
+    want = O.round_out(O.tw_epilogue(O.tw_dots(a_codes, codes), a_scales, wscale, None, 0), "bf16")
+    np.testing.assert_array_equal(bits(out), want)
+    np.testing.assert_array_equal(s_out.cpu().numpy(), a_scales)
+
+
+def test_fused_row_quantization_rejects_what_it_does_not_take():
+    x = torch.randn(2, 256, device=DEV).to(torch.bfloat16)
+    w = torch.zeros(256 // 2 * 64, dtype=torch.uint8, device=DEV)
+    ws = torch.ones(64, device=DEV)
+    out = torch.empty(2, 64, device=DEV, dtype=torch.bfloat16)
+    s_out = torch.empty(1, device=DEV)
+    with pytest.raises(RuntimeError, match=r"\[1, K\]"):
+        _native.tokenwise_linear_x(x, s_out, w, _native.TW_KMAJOR_W4, ws, None, 64, 256, _native.TW_EPI_A8, out)
+    lib = _native.lib()
+    # the C ABI checks the row count, K and the layout itself
+    rc = lib.actune_tokenwise_linear_x(x.data_ptr(), 0, s_out.data_ptr(), w.data_ptr(), _native.TW_KMAJOR_W4,
+                                       ws.data_ptr(), None, 0, out.data_ptr(), 0, 2, 64, 256, 0, None, 0, None)
+    assert rc != 0 and b"one row" in lib.actune_last_error()
+    rc = lib.actune_tokenwise_linear_x(x.data_ptr(), 0, s_out.data_ptr(), w.data_ptr(), _native.TW_KMAJOR_W4,
+                                       ws.data_ptr(), None, 0, out.data_ptr(), 0, 1, 64, 32768, 0, None, 0, None)
+    assert rc != 0 and b"16384" in lib.actune_last_error()
+    rc = lib.actune_tokenwise_linear_x(x.data_ptr(), 0, s_out.data_ptr(), w.data_ptr(), _native.TW_ROWS_S4,
+                                       ws.data_ptr(), None, 0, out.data_ptr(), 0, 1, 64, 256, 0, None, 0, None)
+    assert rc != 0 and b"K-major" in lib.actune_last_error()
