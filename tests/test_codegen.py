@@ -127,3 +127,25 @@ def test_mfma_results_wait_on_every_path(device_asm):
     assert any(any(op.startswith("v_mfma") for _a, op, _x, _t in ins) for ins in fns.values())
     bad = {name: h[:3] for name, ins in fns.items() if (h := _mfma_hazards(ins))}
     assert not bad, f"VALU access to an MFMA result before {MFMA_WAIT} wait states: {bad}"
+
+
+# ---------------------------------------------------------------- M0 and LDS DMA
+def test_m0_is_only_set_for_lds_dma(device_asm):
+    """The tokenwise ring kernel issues its LDS-DMA loads from inline asm
+    that sets M0 (the LDS base of the load) itself. The compiler reserves M0
+    and does not expect the asm to change it, so the shipped code must use
+    M0 nowhere else: every reference to m0 is that s_mov, followed by the
+    one wait state and the load, and every LDS-DMA load has its own M0 set
+    right before it."""
+    fns = _functions(device_asm)
+    loads = 0
+    for name, ins in fns.items():
+        for k, (_a, op, args, _t) in enumerate(ins):
+            if re.search(r"\bm0\b", args):
+                assert op == "s_mov_b32" and args.startswith("m0,"), (name, op, args)
+                assert k + 2 < len(ins) and ins[k + 1][1] == "s_nop" and ins[k + 2][1] == "buffer_load_dwordx4" \
+                    and ins[k + 2][2].endswith(" lds"), (name, ins[k:k + 3])
+            if op.startswith("buffer_load") and args.endswith(" lds"):
+                loads += 1
+                assert k >= 2 and ins[k - 2][1] == "s_mov_b32" and ins[k - 2][2].startswith("m0,"), (name, op, args)
+    assert loads > 0, "no LDS-DMA loads in the library"
