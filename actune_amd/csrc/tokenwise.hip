@@ -524,14 +524,15 @@ __device__ __forceinline__ constexpr int lds_pos(int r, int b) {
 }
 
 // Large-M tokenwise GEMM: the tile geometry of tw_gemm, with the K-steps
-// staged through a ring of D LDS slots filled by DMA loads. Every K-step of
-// a workgroup is NI 1-KiB blocks (weights, then activations); wave w issues
-// blocks w, w + 4, ... (IPW per wave, the surplus aimed at a per-wave junk
-// KiB with offsets out of range). Step t + D - 1 is issued right after the
-// barrier that opens step t, into the slot step t - 1 used, so D - 1 steps
-// are in flight while one is computed, with no registers held for them.
-// A lane's global offsets are fixed; the step advance is the scalar offset
-// (out of range for steps past the workgroup's K-range).
+// staged through a ring of D LDS slots filled by DMA loads; a slot holds KS
+// consecutive K-steps (one ring step). Every K-step of a workgroup is NI
+// 1-KiB blocks (weights, then activations); wave w issues blocks w, w + 4,
+// ... (IPW per wave, the surplus aimed at a per-wave junk KiB with offsets
+// out of range). Ring step t + D - 1 is issued right after the barrier that
+// opens the read of ring step t + 1, into the slot ring step t - 1 used, so
+// up to D - 2 ring steps are in flight beyond the one being read, with no
+// registers held for them. A lane's global offsets are fixed; the K-step
+// advance is the scalar offset (out of range past the workgroup's K-range).
 template <int WL, int AL, int EPI, int WM, int MT, int NT, int KS, int D>
 __global__ __launch_bounds__(kThreads) void tw_gemm_ring(const TwArgs args) {
   using T = WTraits<WL>;
