@@ -75,15 +75,32 @@ ONLY_SHAPES = {
     "q": (1, [(4096, 4096)], -1), "gate": (1, [(11008, 4096)], -1), "down": (1, [(4096, 11008)], -1),
     "qkv": (1, [(4096, 4096)] * 3, -1), "gateup": (1, [(11008, 4096)] * 2, -1),
     "prefill512": (512, [(4096, 4096)], -1),
+    # the tokenwise W4A8 GEMM (K-major nibble pairs) on its per-row A8 codes
+    "tw512": (512, [(4096, 4096)], "tokenwise"),
 }
 
 
 def run_only(torch, _native, name, W, A, config):
     m, spec, cfg = ONLY_SHAPES[name]
-    cfg = config if config >= 0 else cfg
     k = spec[0][1]
     g = torch.Generator(device="cuda").manual_seed(0)
     x = torch.randn(m, k, device="cuda").to(torch.bfloat16)
+    if cfg == "tokenwise":
+        n = spec[0][0]
+        act, sc = _native.tokenwise_quantize(x, 8)
+        need = _native.tokenwise_workspace_bytes(m, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8)
+        work = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+        sets = [(torch.randint(0, 256, (k // 2 * n,), generator=g, device="cuda", dtype=torch.uint8),
+                 torch.rand(n, device="cuda") * 0.01) for _ in range(24)]
+        out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        for w, ws in sets:
+            _native.tokenwise_linear(act, _native.TW_ACT_A8, sc, w, _native.TW_KMAJOR_W4, ws, None, n, k,
+                                     _native.TW_EPI_A8, out, workspace=work if need else None)
+        torch.cuda.synchronize()
+        print(json.dumps(dict(only=name, M=m, targets=spec, launches=len(sets), path="tokenwise W4A8")))
+        return
+    cfg = config if config >= 0 else cfg
     sets = [[(torch.randint(0, 256, (n, k * W // 8), generator=g, device="cuda", dtype=torch.uint8),
               torch.rand(n, device="cuda") * 0.01, None, torch.empty(m, n, device="cuda", dtype=torch.bfloat16))
              for n, _ in spec] for _ in range(24)]
