@@ -220,11 +220,13 @@ def _kmajor_weights(n, k, W, seed):
 
 @pytest.mark.parametrize("W,wl", [(4, _native.TW_KMAJOR_W4), (8, _native.TW_KMAJOR_W8), (2, _native.TW_KMAJOR_W2)])
 @pytest.mark.parametrize("n,k", [(4096, 4096), (11008, 4096), (4096, 11008), (256, 2048), (48, 256), (32, 96),
-                                 (128, 16384)])
+                                 (128, 16384), (64, 64), (48, 64)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_fused_row_quantization_equals_two_step(W, wl, n, k, dtype):
     """actune_tokenwise_linear_x (the row quantized inside the split GEMM)
-    gives the quantizer + linear result bit for bit, scale included."""
+    gives the quantizer + linear result bit for bit, scale included; K = 64
+    is one K-step, so the launch is unsplit and its epilogue reads the row
+    scale the launch computed."""
     if k % {4: 32, 8: 64, 2: 128}[W]:
         pytest.skip("in_features not allowed for this layout")
     w, ws = _kmajor_weights(n, k, W, seed=n + k + W)
@@ -232,6 +234,8 @@ def test_fused_row_quantization_equals_two_step(W, wl, n, k, dtype):
     x = (torch.randn(1, k, device=DEV) * 3).to(dtype)
     act, s = _native.tokenwise_quantize(x, 8)
     need = _native.tokenwise_workspace_bytes(1, n, k, wl, _native.TW_ACT_A8)
+    if k == 64:
+        assert need == 0  # one K-step: no split
     ws_buf = torch.full((max(need, 1),), 0x5A, dtype=torch.uint8, device=DEV)
     want = torch.empty(1, n, device=DEV, dtype=dtype)
     _native.tokenwise_linear(act, _native.TW_ACT_A8, s, w, wl, ws, bias, n, k, _native.TW_EPI_A8, want,
