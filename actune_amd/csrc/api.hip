@@ -243,10 +243,15 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
     const int pref = tiles >= 1024 ? 1 : 2;
     if (fused_at(pref)) return kDecodeFirst + pref;
   } else if (M > kFusedMaxM && M <= kDecodeMax) {
-    // narrow N, 8-token tiles: the most waves that get work quantize x in
-    // the launch where light
-    for (int c = 2; c >= 0; --c)
+    // narrow N, 8- and 16-token tiles: the most waves that get work quantize
+    // x in the launch where light. Above 12 tokens 16 waves do not: at 1024
+    // rows and K = 4096 the 8-wave launch on the quantizer's codes is faster
+    // (measured W4A4/W8A4/W2A8, M = 14-24: 7.9-8.4 against 8.2-9.0 us;
+    // M = 9-12: 16 waves in-launch 6.3-7.9 against 7.2-8.1 us)
+    for (int c = 2; c >= 0; --c) {
+      if (kSmallMWaves[c] == 16 && M > 12) continue;
       if (decode_waves_useful(K, kSmallMWaves[c]) && fused_at(c)) return kDecodeFirst + c;
+    }
   } else if (M == 1) {
     // narrow N, one token: the launch is latency-bound, and the fewest waves
     // whose ring holds the K-range finish first (measured on MI355X at the
@@ -273,7 +278,9 @@ namespace {
 // fits (measured on MI355X, W2/W4/W8 x A4/A8, M = 1..64): M <= 4 and narrow
 // N, the fewest waves that still give every SIMD a wave; wide N (more than
 // 256 row tiles), 4 waves (16 above 8 tokens, whose tiles then share
-// workgroups four at a time) below 1024 row tiles and 8 waves from there on;
+// workgroups four at a time, but 8 for two 16-token blocks: W4A8 11008x4096
+// at M = 24 / 32, 21.3 / 22.5 against 22.7 / 23.6 us) below 1024 row tiles
+// and 8 waves from there on;
 // narrow N above 4 tokens, the fewest waves that fit, except 16 waves for
 // 256 row tiles with K >= 4096 at W8 or above 32 tokens.
 int decode_packed_config(int64_t M, int64_t N, int64_t K, int W) {
@@ -283,6 +290,7 @@ int decode_packed_config(int64_t M, int64_t N, int64_t K, int W) {
   int order[3] = {0, 1, 2};
   if (tiles > 256 && M >= 2) {
     if (tiles >= 1024) { order[0] = 1; order[1] = M > 8 ? 2 : 0; order[2] = M > 8 ? 0 : 2; }
+    else if (M > 16 && M <= 32) { order[0] = 1; order[1] = 2; order[2] = 0; }  // two 16-token blocks
     else if (M > 8) { order[0] = 2; order[1] = 1; order[2] = 0; }
   } else if (M > 8 && tiles >= 256 && K >= 4096 && (W == 8 || M > 32)) {
     order[0] = 2; order[1] = 1; order[2] = 0;

@@ -47,9 +47,9 @@ __host__ __device__ constexpr int decode_ring(int W) { return W == 2 ? 4 : 8; }
 // token tile: tokens 4j..4j+3 land in lanes 16j..16j+15
 static int decode_token_tile(int M) { return M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 // activation passes a wave issues up front: fused passes quantize 8
-// group-rows (M <= 8 only), packed passes unpack 16
+// group-rows, packed passes unpack 16
 __host__ __device__ constexpr int decode_passes(int MT, bool packed) {
-  return packed ? (MT < 8 ? MT : 8) : (MT == 8 ? 8 : 4);
+  return packed ? (MT < 8 ? MT : 8) : (MT == 4 ? 4 : 8);
 }
 
 // Largest groups per wave of a K split over nw waves.
@@ -102,7 +102,7 @@ int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob) {
 }
 
 bool decode_fits(int K, int M, int W, int nw, bool packed, int x_dt) {
-  if (!packed && (x_dt != kBF16 || M > 8)) return false;  // fused mode: bf16 x, M <= 8
+  if (!packed && x_dt != kBF16) return false;  // fused mode: bf16 x
   if (M < 1 || M > kDecodeMaxM || (nw != 4 && nw != 8 && nw != 16)) return false;
   const int gw = decode_groups_per_wave(K, nw), gps = 8 / W;
   if ((gw + gps - 1) / gps > decode_ring(W)) return false;
@@ -122,7 +122,7 @@ __device__ __forceinline__ int chunk_begin_u(int c, int G) {
   return b < (uint32_t)G ? (int)b : G;
 }
 
-// MT: token tile (4 or 8). PACKED: activations come as packed codes +
+// MT: token tile (4, 8 or 16). PACKED: activations come as packed codes +
 // scales (args.a, args.as); otherwise bf16 x (and the bf16 channel scale
 // when SCALE) is quantized here. ONE: M == 1 (only register 0 of a lane's
 // MFMA result can be nonzero); its launches read token operands at constant
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
   constexpr bool FAST = ONE;
   constexpr int PR = PACKED ? 16 : 8;      // group-rows per activation pass
   constexpr int NPX = FULL && ONE && !PACKED ? (RING * GS + 7) / 8 : decode_passes(MT, PACKED);
-  static_assert(MT == 4 || MT == 8 || (MT == 16 && PACKED), "token tiles of 4, 8 or (codes only) 16");
+  static_assert(MT == 4 || MT == 8 || MT == 16, "token tiles of 4, 8 or 16");
   static_assert(!ONE || MT == 4, "M == 1 uses the 4-token tile");
   static_assert(!ONE || TR == 1, "M == 1 launches own one row tile per workgroup");
   static_assert(TR <= NW, "waves 0..TR-1 finish one tile each");
@@ -163,13 +163,18 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, in
                     "+s"(pr.w), "+s"(pr.ws), "+s"(pr.bias), "+s"(pr.out), "+s"(pr.N));
   const int N = pr.N, G = K / kGroup;
   if constexpr (MT == 16) {
-    // 16-token block blockIdx.z: its tokens, codes, scales and output rows
+    // 16-token block blockIdx.z: its tokens, x rows or codes and scales, and
+    // output rows (the channel scale of the fused mode is per column)
     const int m0 = 16 * (int)blockIdx.z;
     const bool last = m0 + 16 >= M;
     m_inv = last ? args.m_div_tail : 4096u;
     M = last ? M - m0 : 16;
-    xsrc = static_cast<const uint8_t*>(xsrc) + (size_t)m0 * (K / 8) * A;
-    xaux = static_cast<const float*>(xaux) + (size_t)m0 * G;
+    if constexpr (PACKED) {
+      xsrc = static_cast<const uint8_t*>(xsrc) + (size_t)m0 * (K / 8) * A;
+      xaux = static_cast<const float*>(xaux) + (size_t)m0 * G;
+    } else {
+      xsrc = static_cast<const uint8_t*>(xsrc) + (size_t)m0 * K * ESZ;
+    }
     pr.out = static_cast<uint8_t*>(pr.out) + (size_t)m0 * N * (out_dt == kF32 ? 4 : 2);
   }
   const int n0 = (int)blockIdx.x * 16 * TR;
@@ -582,9 +587,12 @@ static void launch_decode_nw(bool packed, const LinearArgs& g, hipStream_t st) {
   } else if (g.M <= 4) {
     if (scale) launch_decode_tr<W, A, NW, 4, false, true>(g, st);
     else launch_decode_tr<W, A, NW, 4, false, false>(g, st);
-  } else {
+  } else if (g.M <= 8) {
     if (scale) launch_decode_tr<W, A, NW, 8, false, true>(g, st);
     else launch_decode_tr<W, A, NW, 8, false, false>(g, st);
+  } else {
+    if (scale) launch_decode_tr<W, A, NW, 16, false, true>(g, st);
+    else launch_decode_tr<W, A, NW, 16, false, false>(g, st);
   }
 #undef DEC_FULL
 }

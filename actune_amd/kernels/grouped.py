@@ -41,6 +41,10 @@ class SharedActivationCache:
         self.misses = 0
 
 
+# largest M at which a call inside an enabled shared scope still quantizes
+# inside its GEMM when its forward would
+_SHARED_FUSED_MAX_M = 8
+
 _SHARED_GROUP_STATE: ContextVar[SharedActivationCache | None] = ContextVar("actune_shared_group64_codes",
                                                                            default=None)
 
@@ -131,13 +135,17 @@ class GroupedLinear(torch.nn.Module):
         state = _SHARED_GROUP_STATE.get()
         m = flat.shape[0]
         if state is not None and state.enabled and m > 0:
-            config = self.config if self.config != CONFIG_AUTO else \
-                _native.default_config(m, self.out_features, self.in_features, self.w, self.a)
-            if not _native.forward_fuses_quantizer(m, self.out_features, self.in_features, self.w, self.a,
-                                                   flat.dtype, config):
+            # Past _SHARED_FUSED_MAX_M tokens the codes are shared even where
+            # the forward would quantize inside its GEMM: the in-launch
+            # quantization then costs more than a GEMM on shared codes
+            # (measured on MI355X at M = 50, 1024x1024: about 1.5 us per
+            # linear), and the linears of a scope usually read the same x.
+            if m > _SHARED_FUSED_MAX_M or not _native.forward_fuses_quantizer(
+                    m, self.out_features, self.in_features, self.w, self.a, flat.dtype, self.config):
                 packed, scales = _shared_codes(state, x if source is None else source, flat, self.a, input_scale)
+                # an automatic config resolves to the choice for packed codes
                 out = _native.grouped_linear(packed, scales, self.packed_weight, self.weight_scale, self.bias,
-                                             flat, self.w, self.a, config)
+                                             flat, self.w, self.a, self.config)
                 return out.reshape(*x.shape[:-1], self.out_features)
         out = _native.grouped_forward(flat, self.packed_weight, self.weight_scale, self.bias,
                                       self.w, self.a, input_scale=input_scale, config=self.config)

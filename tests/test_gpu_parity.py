@@ -384,8 +384,11 @@ def test_decode_shared_row_tiles(W, A, m, n):
 @pytest.mark.parametrize("k", [1024, 4096])
 def test_decode_token_blocks(W, A, m, k):
     """M = 17..64 runs the decode kernel in 16-token blocks (the last one
-    ragged): the GEMM on the quantizer's codes with 4, 8 and 16 waves and the
-    default forward equal the oracle bit for bit (N ragged)."""
+    ragged): the GEMM on the quantizer's codes with 4, 8 and 16 waves, the
+    forward on bf16 x with each of them (x quantized per block inside the
+    launch where a wave's K-range is at most 4 groups, with and without the
+    channel scale) and the default forward equal the oracle bit for bit (N
+    ragged)."""
     n = 700
     x, w, b = seeded_inputs(m, k, n, seed=m * 7 + k + W * A, bias=True)
     wc, wsc, w_dev, ws_dev = _packed_weight(w, W, A)
@@ -397,3 +400,15 @@ def test_decode_token_blocks(W, A, m, k):
         out = _native.grouped_linear(p, s, w_dev, ws_dev, bd, xd, W, A, config)
         np.testing.assert_array_equal(bits(out), want, err_msg=f"config {config}")
     np.testing.assert_array_equal(bits(_native.grouped_forward(xd, w_dev, ws_dev, bd, W, A)), want)
+    scale = torch.linspace(0.5, 2.0, k).to(torch.bfloat16)
+    _, sa_scales, sa_codes = oracle_activation(x, A, scale)
+    want_s = O.round_out(O.linear(sa_codes, sa_scales, wc, wsc, b.float().numpy(), bounds=canonical_bounds(k // 64)), "bf16")
+    fused_any = False
+    for config in (14, 15, 16):
+        fused_any |= _native.forward_fuses_quantizer(m, n, k, W, A, torch.bfloat16, config)
+        out = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, config=config)
+        np.testing.assert_array_equal(bits(out), want, err_msg=f"forward config {config}")
+        out = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, input_scale=scale.to(DEV), config=config)
+        np.testing.assert_array_equal(bits(out), want_s, err_msg=f"forward config {config}, channel scale")
+    # at K = 1024 the in-launch quantization is light at every M here
+    assert fused_any or k != 1024
