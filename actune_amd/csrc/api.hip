@@ -23,8 +23,9 @@ constexpr int kStreamMax = 16;
 constexpr int kStreamConfigs = 3;
 constexpr int kPrefillFirst = kStreamFirst + kStreamConfigs;  // ids 10..13: prefill kernel, any M
 constexpr int kPrefillConfigs = 4;
-constexpr int kDecodeFirst = kPrefillFirst + kPrefillConfigs;  // ids 14..16: decode kernel, M <= 64
-constexpr int kDecodeMax = 64;
+constexpr int kDecodeFirst = kPrefillFirst + kPrefillConfigs;  // ids 14..16: decode kernel, M <= 1024
+constexpr int kDecodeMax = 1024;      // decode configs: 16-token blocks on grid z
+constexpr int kDecodeAutoMax = 64;   // decode_packed_config and the small-M defaults up to this M
 constexpr int kFusedMaxM = 4;      // small-M and streaming calls up to this M quantize inside the GEMM
 constexpr int kSmallMWaves[kSmallMConfigs] = {4, 8, 16};
 thread_local char g_err[512];
@@ -70,7 +71,7 @@ int check_shape(int64_t M, int64_t K, int W, int A, int out_dt, int bias_dt, int
   if (config < kSmallMConfigs && M > kSmallMMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
   if (config >= kStreamFirst && config < kPrefillFirst && M > kStreamMax)
     return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 16");
-  if (config >= kDecodeFirst && M > kDecodeMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 64");
+  if (config >= kDecodeFirst && M > kDecodeMax) return fail(ACTUNE_ERR_INVALID, "configuration needs M <= 1024");
   return ACTUNE_OK;
 }
 
@@ -233,7 +234,7 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
     const int nw = kSmallMWaves[c];
     return decode_fits((int)K, (int)M, W, nw, false, kBF16) && decode_light(M, N, K, W, nw);
   };
-  if (M >= 2 && M <= kDecodeMax && tiles > 256) {
+  if (M >= 2 && M <= kDecodeAutoMax && tiles > 256) {
     // Wide N: several row tiles share a workgroup and its quantized x
     // (decode_row_tiles); 16 waves, whose short K-ranges allow four tiles,
     // below 1024 row tiles, 8 waves from there on. Two tokens below 1024 row
@@ -242,7 +243,7 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
     if (M == 2 && tiles < 1024 && fused_at(0)) return kDecodeFirst;
     const int pref = tiles >= 1024 ? 1 : 2;
     if (fused_at(pref)) return kDecodeFirst + pref;
-  } else if (M > kFusedMaxM && M <= kDecodeMax) {
+  } else if (M > kFusedMaxM && M <= kDecodeAutoMax) {
     // narrow N, 8- and 16-token tiles: the most waves that get work quantize
     // x in the launch where light. Above 12 tokens 16 waves do not: at 1024
     // rows and K = 4096 the 8-wave launch on the quantizer's codes is faster
@@ -284,7 +285,7 @@ namespace {
 // narrow N above 4 tokens, the fewest waves that fit, except 16 waves for
 // 256 row tiles with K >= 4096 at W8 or above 32 tokens.
 int decode_packed_config(int64_t M, int64_t N, int64_t K, int W) {
-  if (M < 1 || M > kDecodeMax) return -1;
+  if (M < 1 || M > kDecodeAutoMax) return -1;
   const int64_t tiles = (N + 15) / 16;
   auto packed_at = [&](int c) { return decode_fits((int)K, (int)M, W, kSmallMWaves[c], true, kBF16); };
   int order[3] = {0, 1, 2};
@@ -317,6 +318,18 @@ int packed_default(int64_t M, int64_t N, int64_t K, int W, int A) {
   if (M <= kFusedMaxM) return tiles >= 512 ? kStreamFirst + 1 : 2;
   if (M <= kStreamMax) return tiles >= 512 ? kStreamFirst + 1 : kStreamFirst + 2;
   if (M <= kSmallMMax) return 1;
+  // Narrow problems above 64 tokens (at most 128 tiles of 64 rows x 32
+  // tokens, K <= 4096): the decode kernel in 16-token blocks, which gives
+  // every CU work where the prefill kernel has a few dozen tiles. Measured on
+  // MI355X (us, prefill 64x32 -> decode): W4A4 256x2048 at M = 96 / 256 / 512
+  // 10.3 / 10.4 / 10.9 -> 6.0 / 6.2 / 8.1, W4A4 2048x2048 at M = 128 10.8 ->
+  // 9.3, W4A4 1024x1024 at M = 128 / 256 9.0 / 9.2 -> 6.3 / 8.6, W8A8
+  // 512x4096 at M = 128 / 256 16.9 / 17.6 -> 8.5 / 11.9. Four waves take K <=
+  // 1024, 16 waves K = 4096 from 256 tokens, 8 waves the rest.
+  if (M <= kDecodeMax && K <= 4096 && ((N + 63) / 64) * ((M + 31) / 32) <= 128) {
+    const int c = K <= 1024 ? 0 : (K >= 4096 && M >= 256 ? 2 : 1);
+    if (decode_fits((int)K, (int)M, W, kSmallMWaves[c], true, kBF16)) return kDecodeFirst + c;
+  }
   // Prefill (measured on C3/C4 shapes): the prefill kernel with 64x64 tiles
   // when there are at least two tiles per CU, 64x32 tiles below that (more
   // workgroups for small problems), 128x64 tiles for W <= 4 from four tiles

@@ -38,7 +38,7 @@
 
 namespace actune {
 
-constexpr int kDecodeMaxM = 64;
+constexpr int kDecodeMaxM = 1024;  // 16-token blocks on grid z
 // zero region: a wave's widest K-range (16 groups) of 64-byte zero rows
 constexpr int kDecodeZeroBytes = 16 * kGroup;
 

@@ -142,8 +142,9 @@ int actune_grouped_dots_i32(const uint8_t* a, const uint8_t* w, int64_t M, int64
  *   7, 8, 9  persistent streaming kernel with 4, 8, 16 waves (M <= 16)
  *   10 .. 13 prefill kernel (weights streamed per wave, activations staged
  *            per workgroup) with tiles 128x64, 128x32, 64x64, 64x32 (any M)
- *   14 .. 16 decode kernel with 4, 8, 16 waves (M <= 64 in blocks of 16
- *            tokens; bf16 x quantized in the launch up to M = 8, other
+ *   14 .. 16 decode kernel with 4, 8, 16 waves (M <= 1024 in blocks of 16
+ *            tokens; bf16 x quantized in the launch where the in-launch
+ *            work is light and a wave's K-range fits its passes, other
  *            dtypes, more tokens and longer
  *            K-ranges through the quantizer launch; a K too long for a
  *            wave's load ring and the dots mode run the small-M kernel with

@@ -380,10 +380,10 @@ def test_decode_shared_row_tiles(W, A, m, n):
 
 
 @pytest.mark.parametrize("W,A", [(4, 8), (2, 4), (8, 4)])
-@pytest.mark.parametrize("m", [17, 24, 50, 64])
+@pytest.mark.parametrize("m", [17, 24, 50, 64, 100, 256])
 @pytest.mark.parametrize("k", [1024, 4096])
 def test_decode_token_blocks(W, A, m, k):
-    """M = 17..64 runs the decode kernel in 16-token blocks (the last one
+    """M = 17..1024 runs the decode kernel in 16-token blocks (the last one
     ragged): the GEMM on the quantizer's codes with 4, 8 and 16 waves, the
     forward on bf16 x with each of them (x quantized per block inside the
     launch where a wave's K-range is at most 4 groups, with and without the
@@ -410,5 +410,5 @@ def test_decode_token_blocks(W, A, m, k):
         np.testing.assert_array_equal(bits(out), want, err_msg=f"forward config {config}")
         out = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, input_scale=scale.to(DEV), config=config)
         np.testing.assert_array_equal(bits(out), want_s, err_msg=f"forward config {config}, channel scale")
-    # at K = 1024 the in-launch quantization is light at every M here
-    assert fused_any or k != 1024
+    # at K = 1024 the in-launch quantization is light up to M = 100 here
+    assert fused_any or k != 1024 or m > 100

@@ -58,7 +58,7 @@ def test_config_table():
     assert _native.config_valid(0, 64) and not _native.config_valid(0, 65)
     assert all(_native.config_valid(c, 4096) for c in range(3, 7))
     assert all(_native.config_valid(c, 1) and _native.config_valid(c, 4096) for c in range(10, 14))
-    assert all(_native.config_valid(c, 64) and not _native.config_valid(c, 65) for c in range(14, 17))
+    assert all(_native.config_valid(c, 1024) and not _native.config_valid(c, 1025) for c in range(14, 17))
     assert _native.config_valid(9, 16) and not _native.config_valid(9, 17)
     assert not _native.config_valid(n, 1) and not _native.config_valid(-2, 1)
     for m in (1, 8, 16, 17, 50, 512):
@@ -106,7 +106,13 @@ def test_config_table():
     assert _native.default_config(50, 4096, 1024, 4, 4) == 14
     assert _native.default_config(50, 1024, 4096, 8, 4) == 15
     assert _native.default_config(50, 4096, 4096, 4, 4) == 16
-    assert _native.default_config(65, 4096, 4096, 4, 8) not in (14, 15, 16)  # decode: M <= 64
+    assert _native.default_config(65, 4096, 4096, 4, 8) not in (14, 15, 16)  # 192 prefill tiles
+    # above 64 tokens, narrow problems (at most 128 tiles of 64x32, K <= 4096)
+    # run the decode kernel in 16-token blocks
+    assert _native.default_config(256, 256, 2048, 4, 4) == 15
+    assert _native.default_config(128, 1024, 1024, 4, 4) == 14
+    assert _native.default_config(256, 512, 4096, 8, 8) == 16
+    assert _native.default_config(96, 2048, 16384, 4, 4) == 13  # K above 4096
     # prefill: 64x32 tiles below two 64x64 tiles per CU, 64x64 below four,
     # 128x64 from four for W <= 4 (W8 keeps 64x64), the tiled kernel from eight
     assert _native.default_config(256, 2048, 2048, 4, 4) == 13
@@ -138,6 +144,7 @@ def test_quantize_rejects_bad_arguments(args, msg):
     (dict(K=96), "invalid dimensions"),
     (dict(N=0), "invalid dimensions"),
     (dict(config=0, M=65), "M <= 64"),
+    (dict(config=14, M=1025), "M <= 1024"),
     (dict(config=99), "invalid configuration"),
     (dict(out_dt=9), "dtype"),
     (dict(M=4), "null pointer"),
