@@ -361,34 +361,45 @@ def tokenwise_workspace_bytes(m, n, k, w_layout, a_layout):
     return need
 
 
+def tokenwise_fused_max_k(m):
+    """Longest row actune_tokenwise_linear_x quantizes for m rows (one row:
+    16384; 2, 3-4, 5-8 rows: 16384, 8192, 4096), 0 past 8 rows."""
+    if m == 1:
+        return 16384
+    if not 1 < m <= 8:
+        return 0
+    return 16 * 8 * (256 // (2 if m <= 2 else 4 if m <= 4 else 8))
+
+
 def tokenwise_linear_x(x, as_out, w, w_layout, ws, bias, n, k, epilogue, out, workspace=None):
-    """One row of x ([1, K] bf16 / f16 / f32) quantized to A8 inside the GEMM
-    launch (actune_tokenwise_linear_x): the result of tokenwise_quantize(x, 8)
-    followed by tokenwise_linear on its codes, bit for bit. as_out: float32
-    [1], receives the row's activation scale; w: a K-major layout; workspace
-    as for tokenwise_linear with A8 activations."""
+    """Rows of x ([M, K], M = 1..8; bf16 / f16, or f32 for one row) quantized
+    to A8 inside the GEMM launch (actune_tokenwise_linear_x): the result of
+    tokenwise_quantize(x, 8) followed by tokenwise_linear on its codes, bit
+    for bit. as_out: float32 [M], receives the rows' activation scales; w: a
+    K-major layout; workspace as for tokenwise_linear with A8 activations."""
     _require_cuda(x, as_out, w, ws, bias, out, workspace)
-    if x.dim() != 2 or x.shape[0] != 1 or x.shape[1] != k:
-        raise RuntimeError("fused quantization takes x of shape [1, K]")
+    if x.dim() != 2 or not 1 <= x.shape[0] <= 8 or x.shape[1] != k:
+        raise RuntimeError("fused quantization takes x of shape [M, K] with M <= 8")
+    m = x.shape[0]
     if not (x.is_contiguous() and w.is_contiguous() and ws.is_contiguous()
             and (bias is None or bias.is_contiguous())):
         raise RuntimeError("contiguous operands required")
     if as_out.dtype != torch.float32 or ws.dtype != torch.float32:
         raise RuntimeError("float scales/bias required")
-    if as_out.numel() != 1 or not as_out.is_contiguous() or ws.numel() != n or (bias is not None and bias.numel() != n):
+    if as_out.numel() != m or not as_out.is_contiguous() or ws.numel() != n or (bias is not None and bias.numel() != n):
         raise RuntimeError("scale shape mismatch")
     wbytes = {TW_KMAJOR_W8: k * n, TW_KMAJOR_W4: k // 2 * n, TW_KMAJOR_W2: k // 4 * n}.get(w_layout)
     if wbytes is None:
         raise RuntimeError("fused quantization takes the K-major (A8) weight layouts")
     if w.numel() != wbytes or w.element_size() != 1:
         raise RuntimeError("packed weight shape mismatch")
-    _check_buffer(out, "out", (1, n), out.dtype, x.device)
-    need = tokenwise_workspace_bytes(1, n, k, w_layout, TW_ACT_A8)
+    _check_buffer(out, "out", (m, n), out.dtype, x.device)
+    need = tokenwise_workspace_bytes(m, n, k, w_layout, TW_ACT_A8)
     if need and (workspace is None or workspace.numel() < need or workspace.dtype != torch.uint8):
         raise RuntimeError(f"workspace of at least {need} bytes required")
     _check(lib().actune_tokenwise_linear_x(
         _ptr(x), _dtype_code(x), _ptr(as_out), _ptr(w), w_layout, _ptr(ws), _ptr(bias), _bias_code(bias), _ptr(out),
-        _dtype_code(out), 1, n, k, epilogue, _ptr(workspace) if need else None, need, _stream(x.device)))
+        _dtype_code(out), m, n, k, epilogue, _ptr(workspace) if need else None, need, _stream(x.device)))
     return out
 
 

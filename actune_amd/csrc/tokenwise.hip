@@ -56,6 +56,15 @@ namespace {
 constexpr int kThreads = 256;
 // longest row the fused-quantization launch takes (8 passes of 8 elements per thread)
 constexpr int kTwFusedMaxK = 16384;
+// rows the fused-quantization launch takes: up to 8 (16-bit x), with
+// 256 / P threads per row for the row counts padded to P = 2, 4, 8 and 16
+// passes of 8 elements each, so K <= 32768 / P
+constexpr int kTwFusedMaxRows = 8;
+constexpr int kTwFusedRowPasses = 16;
+inline int tw_fused_rows_pad(int64_t M) { return M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+inline int64_t tw_fused_max_k(int64_t M) {
+  return M == 1 ? kTwFusedMaxK : (int64_t)kTwFusedRowPasses * 8 * (256 / tw_fused_rows_pad(M));
+}
 
 template <int WL> struct WTraits;
 // U: MFMAs per K-step (64 k each); TW: shift of the weight codes;
@@ -201,15 +210,16 @@ constexpr int align_of_stride(int s) { return s % 16 == 0 ? 16 : (s % 8 == 0 ? 8
 // K until it is) is loaded at entry, every load in flight at once, staged into
 // NB LDS buffers and computed after one barrier.
 //
-// XDT >= 0 (fused quantization, one row of A8): the launch reads the row x of
-// dtype XDT instead of codes. Every workgroup loads the whole row for its
-// amax (first, so that the in-order memory counter lets the amax finish
-// before the weights land), then its K-range of x, then its weights; it
-// computes the row scale s = fl(max(amax, 1e-8) * fl(1/127)) and the codes
-// rint(v / s) clamped to [-128, 127] exactly as tw_quantize_kernel does, and
-// stages the codes as the activation tile. The first workgroup writes s to
-// args.as (the integer reduce reads it).
-template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, int XDT = -1>
+// XDT >= 0 (fused quantization, A8): the launch reads the rows x of dtype
+// XDT instead of codes; XR = 1 takes one row, XR = 8 two to eight rows of
+// 16-bit x. Every workgroup loads the whole rows for their amax (first, so
+// that the in-order memory counter lets the amax finish before the weights
+// land), then its K-range of x, then its weights; it computes each row's
+// scale s = fl(max(amax, 1e-8) * fl(1/127)) and the codes rint(v / s)
+// clamped to [-128, 127] exactly as tw_quantize_kernel does, and stages the
+// codes as the activation tile. The first workgroup writes the scales to
+// args.as (the integer reduce reads them).
+template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, int XDT = -1, int XR = 1>
 __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   using T = WTraits<WL>;
   constexpr int WN = 4 / WM;
@@ -226,6 +236,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
 
   constexpr bool FX = XDT >= 0;
   static_assert(!FX || (AL == ACTUNE_TW_ACT_A8 && TM == 16 && T::KM), "fused quantization: A8, 16-row tiles");
+  static_assert(XR == 1 || (XR == kTwFusedMaxRows && XDT != kF32), "fused rows: one, or up to 8 of 16-bit x");
   constexpr int XSZ = XDT == kF32 ? 4 : 2;  // bytes per x element
   constexpr int XRC = kTwFusedMaxK / (kThreads * 8);  // amax passes of 8 elements per thread
 
@@ -245,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   else wbytes = (uint32_t)N * (K / 4);
   const uint32_t arow = AL == ACTUNE_TW_ACT_A4 ? (uint32_t)K / 2 : (uint32_t)K;
   const Rsrc wr = make_rsrc(args.w, wbytes);
-  const Rsrc ar = FX ? make_rsrc(args.x, (uint32_t)K * XSZ) : make_rsrc(args.a, (uint32_t)M * arow);
+  const Rsrc ar = FX ? make_rsrc(args.x, (uint32_t)M * K * XSZ) : make_rsrc(args.a, (uint32_t)M * arow);
 
   // Per-thread base offsets of its weight / activation chunks (step 0) and
   // the per-step byte strides, all 32-bit: a step's loads are then one add
@@ -386,7 +397,97 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   // nothing, so the batch is straight-line code with no bounds tests)
   v4u wreg[NB][NWC], areg[NB][NAC];
   TwArgs fin = args;
-  if constexpr (FX) {
+  if constexpr (FX && XR > 1) {
+    // rows padded to P (2, 4 or 8): thread t reads row t / (256 / P), 16
+    // passes of 8 consecutive elements (the host keeps K <= 32768 / P)
+    __shared__ float rp[2 * (kThreads / 64)];  // per wave: rows at lanes 0 and 32
+    __shared__ float xsc[XR];                  // row scales for the epilogue
+    const int lgt = M <= 2 ? 7 : M <= 4 ? 6 : 5;  // log2 threads per row
+    const int xrow = tid >> lgt, xsub = tid & ((1 << lgt) - 1);
+    v4u xq[kTwFusedRowPasses];
+#pragma unroll
+    for (int p = 0; p < kTwFusedRowPasses; ++p) {
+      const int e = (p << (lgt + 3)) + xsub * 8;
+      xq[p] = __builtin_amdgcn_raw_buffer_load_b128(ar, xrow < M && e < K ? ((uint32_t)xrow * K + e) * XSZ : kOff,
+                                                    0, 0);
+    }
+    // this thread's EPT elements of every row at byte fb of staged step fi
+    constexpr int EPT = NB * ARB / kThreads;
+    static_assert(EPT == 1 || EPT == 2 || EPT == 4, "fused slice: 1, 2 or 4 elements per thread");
+    const int fi = tid * EPT / ARB, fb = tid * EPT % ARB, fc = fb / 16;
+    uint32_t kx;
+    if constexpr (WL == ACTUNE_TW_KMAJOR_W4) kx = (uint32_t)(fc >> 1) * (K / 2) + 16 * (fc & 1);
+    else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) kx = (uint32_t)(fc >> 1) * (K / 4) + 16 * (fc & 1);
+    else kx = 16 * fc;
+    kx += (uint32_t)(fb % 16) + (uint32_t)(g0 + fi) * astep;
+    uint32_t xsl[XR][EPT == 4 ? 2 : 1];
+#pragma unroll
+    for (int m = 0; m < XR; ++m) {
+      const uint32_t off = m < M && g0 + fi < g1 ? ((uint32_t)m * K + kx) * XSZ : kOff;
+      if constexpr (EPT == 4) {
+        const v2u t = __builtin_amdgcn_raw_buffer_load_b64(ar, off, 0, 0);
+        xsl[m][0] = t[0];
+        xsl[m][1] = t[1];
+      } else if constexpr (EPT == 2) {
+        xsl[m][0] = __builtin_amdgcn_raw_buffer_load_b32(ar, off, 0, 0);
+      } else {
+        xsl[m][0] = __builtin_amdgcn_raw_buffer_load_b16(ar, off, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const uint32_t soff = g0 + i < g1 ? 0u : kOff;
+#pragma unroll
+      for (int c = 0; c < NWC; ++c)
+        wreg[i][c] = __builtin_amdgcn_raw_buffer_load_b128(
+            wr, wbase[c] == kOff ? kOff : wbase[c] + (uint32_t)(g0 + i) * wstep, soff, 0);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kTwFusedRowPasses; ++p) {
+      float v8[8];
+      unpack8<XDT>(xq[p], xq[p], v8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v8[e]));
+    }
+    // the lanes of one row: 32 (P = 8) or the whole wave (P = 2, 4)
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+      if (off < (1 << lgt)) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if ((lane & 31) == 0) rp[2 * wave + (lane >> 5)] = amax;
+    __syncthreads();
+    auto row_scale = [&](int m) {
+      const float a = lgt == 5 ? rp[m] : lgt == 6 ? rp[2 * m] : fmaxf(rp[4 * m], rp[4 * m + 2]);
+      return fmaxf(a, 1e-8f) * (1.0f / 127.0f);
+    };
+    if (tid < M) {
+      const float sc = row_scale(tid);
+      xsc[tid] = sc;
+      if (blockIdx.x == 0 && z == 0) const_cast<float*>(args.as)[tid] = sc;
+    }
+    // the codes of rows 0 .. M-1 (rows past M are never stored; their
+    // products are not written out)
+#pragma unroll
+    for (int m = 0; m < XR; ++m) {
+      if (m < M) {
+        const float sc = row_scale(m);
+        uint32_t cw = 0;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          const uint16_t h = (uint16_t)(xsl[m][e / 2] >> (16 * (e % 2)));
+          const float v = XDT == kBF16 ? bf16_to_f32(h) : f16_to_f32(h);
+          cw |= ((uint32_t)(int)fminf(fmaxf(rintf(v / sc), -128.0f), 127.0f) & 0xffu) << (8 * e);
+        }
+        uint8_t* dst = smem + fi * (WBUF + ABUF) + WBUF + m * ASTR + fb;
+        if constexpr (EPT == 4) *reinterpret_cast<uint32_t*>(dst) = cw;
+        else if constexpr (EPT == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)cw;
+        else *dst = (uint8_t)cw;
+      }
+    }
+    fin.as = xsc;  // the epilogue of an unsplit launch reads the scales from LDS
+#pragma unroll
+    for (int i = 0; i < NB; ++i) stage_w(i, wreg[i]);
+  } else if constexpr (FX) {
     __shared__ float xs[kThreads / 64 + 1];
     // 1. the row for its amax, 2. this workgroup's K-range of x (EPT
     // consecutive elements per thread), 3. the weights
@@ -951,11 +1052,11 @@ int pick_splits(int64_t M, int64_t N, int64_t K, int wl, const Geometry& g) {
   return (int)s;
 }
 
-template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, int XDT = -1>
+template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, int XDT = -1, int XR = 1>
 void launch_gemm_t(const TwArgs& a, hipStream_t st) {
   constexpr int TM = 16 * MT * WM, TN = 16 * NT * (4 / WM);
   const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM), (unsigned)a.splits);
-  tw_gemm<WL, AL, EPI, WM, MT, NT, NB, XDT><<<grid, kThreads, 0, st>>>(a);
+  tw_gemm<WL, AL, EPI, WM, MT, NT, NB, XDT, XR><<<grid, kThreads, 0, st>>>(a);
   if (a.splits > 1) {
     const long total = (long)a.M * a.N;
     constexpr int SHIFT = WTraits<WL>::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0);
@@ -996,10 +1097,17 @@ void launch_gemm_g(const TwArgs& a, const Geometry& g, hipStream_t st) {
   else launch_ring_t<WL, AL, EPI, 2, 2, 2, 2, 4>(a, st);
 }
 
-// one A8 row quantized inside the GEMM launch (small-M geometry, 16 x 128 tiles)
+// A8 rows quantized inside the GEMM launch (small-M geometry, 16 x 128 tiles):
+// one row, or two to eight rows of 16-bit x
 template <int WL, int EPI, int XDT>
 void launch_fused_t(const TwArgs& a, hipStream_t st) {
-  launch_gemm_t<WL, ACTUNE_TW_ACT_A8, EPI, 1, 1, 2, (WL == ACTUNE_TW_KMAJOR_W8 ? 4 : 8), XDT>(a, st);
+  constexpr int NB = WL == ACTUNE_TW_KMAJOR_W8 ? 4 : 8;
+  if constexpr (XDT == kF32) {
+    launch_gemm_t<WL, ACTUNE_TW_ACT_A8, EPI, 1, 1, 2, NB, XDT>(a, st);
+  } else {
+    if (a.M == 1) launch_gemm_t<WL, ACTUNE_TW_ACT_A8, EPI, 1, 1, 2, NB, XDT>(a, st);
+    else launch_gemm_t<WL, ACTUNE_TW_ACT_A8, EPI, 1, 1, 2, NB, XDT, kTwFusedMaxRows>(a, st);
+  }
 }
 
 void launch_fused(int wl, int epi, int xdt, const TwArgs& a, hipStream_t st) {
@@ -1186,8 +1294,13 @@ int actune_tokenwise_linear_x(const void* x, int x_dtype, float* a_scales, const
   set_last_error("");
   if (x_dtype != kBF16 && x_dtype != kF16 && x_dtype != kF32) return fail("unsupported activation dtype");
   if (w_layout > ACTUNE_TW_KMAJOR_W2) return fail("fused quantization takes the K-major (A8) weight layouts");
-  if (M != 1) return fail("fused quantization takes one row (M = 1)");
-  if (K > kTwFusedMaxK) return fail("fused quantization takes in_features <= 16384");
+  if (M < 1 || M > kTwFusedMaxRows) return fail("fused quantization takes 1 to 8 rows");
+  if (M > 1 && x_dtype == kF32) return fail("fused quantization of more than one row takes bf16 or f16 x");
+  if (K > tw_fused_max_k(M)) {
+    char msg[96];
+    snprintf(msg, sizeof msg, "fused quantization takes in_features <= %d at M = %d", (int)tw_fused_max_k(M), (int)M);
+    return fail(msg);
+  }
   TwArgs args;
   const int rc = prepare_linear(args, x, ACTUNE_TW_ACT_A8, a_scales, w, w_layout, w_scale, bias, bias_dtype, out,
                                 out_dtype, M, N, K, epilogue, workspace, workspace_bytes);

@@ -319,10 +319,32 @@ class _TokenwiseA8(torch.nn.Module):
             return _quantize_rows_shared(flat if source is None else source, flat, in_features=self.in_features)
         return _native.tokenwise_quantize(flat.contiguous(), 8)
 
+    def _fuses_rows(self, flat):
+        """Two to eight 16-bit rows outside a shared-cache scope: the GEMM
+        launch quantizes them itself (actune_tokenwise_linear_x), one launch
+        fewer than the quantizer + GEMM pair, with the same codes and
+        outputs. Inside an enabled scope the siblings share one quantizer
+        launch instead."""
+        state = _SHARED_A8_STATE.get()
+        m = flat.shape[0]
+        return (self.fused_quantization and 2 <= m <= 8 and flat.dtype in (torch.bfloat16, torch.float16)
+                and self.in_features <= _native.tokenwise_fused_max_k(m)
+                and (state is None or not state.enabled))
+
     def _linear(self, value):
         _require_cuda(value, type(self).__name__)
         original_shape = value.shape[:-1]
         flat = value.reshape(-1, self.in_features)
+        if self._fuses_rows(flat):
+            m = flat.shape[0]
+            out = torch.empty((m, self.out_features), device=flat.device, dtype=value.dtype)
+            scale = torch.empty(m, device=flat.device, dtype=torch.float32)
+            ws = _workspace(self, m, self.out_features, self.in_features, self._layout, _native.TW_ACT_A8,
+                            flat.device)
+            _native.tokenwise_linear_x(flat.contiguous(), scale, getattr(self, self._weight_name), self._layout,
+                                       self.weight_scale, self.bias, self.out_features, self.in_features,
+                                       _native.TW_EPI_A8, out, workspace=ws)
+            return out.reshape(*original_shape, self.out_features)
         activation, scale = self._quantize(flat, source=value)
         if self._layout == _native.TW_KMAJOR_W4 and decode_eligible(flat, k=self.in_features, n=self.out_features):
             state = _DECODE_STATE.get()

@@ -450,7 +450,8 @@ def bench_tokenwise(torch, _native, steps, warmup):
     reference's decode use), rotating over >= 256 MB of distinct weights,
     and M=512 for every pair (the MFMA-bound case: the int32 accumulator
     needs no per-group rescale). Each launch pair = quantizer + GEMM; at M=1
-    also the GEMM that quantizes the row itself (us_quantizer_fused)."""
+    and 8 also the GEMM that quantizes the rows itself where it takes K
+    (us_quantizer_fused)."""
     layouts = {"W4A8": _native.TW_KMAJOR_W4, "W8A8": _native.TW_KMAJOR_W8, "W2A8": _native.TW_KMAJOR_W2,
                "W4A4": _native.TW_ROWS_S4, "W2A4": _native.TW_ROWS_S2, "W8A4": _native.TW_KMAJOR_W8}
     g = torch.Generator(device="cuda").manual_seed(6)
@@ -478,13 +479,14 @@ def bench_tokenwise(torch, _native, steps, warmup):
                 _native.tokenwise_quantize(x, A, act, sc)
                 _native.tokenwise_linear(act, al, sc, w, wl, s, None, n, k, epi, y, workspace=work if need else None)
 
-        def fused():  # one row quantized inside the split GEMM (A8 layouts)
+        def fused():  # the rows quantized inside the split GEMM (A8 layouts)
             for w, s in ws:
                 _native.tokenwise_linear_x(x, sc, w, wl, s, None, n, k, epi, y, workspace=work if need else None)
 
         us = time_launches(torch, gemm_only, steps, warmup) / copies
         us_q = time_launches(torch, with_quant, steps, warmup) / copies
-        us_f = time_launches(torch, fused, steps, warmup) / copies if m == 1 and A == 8 else None
+        takes_x = A == 8 and k <= _native.tokenwise_fused_max_k(m)
+        us_f = time_launches(torch, fused, steps, warmup) / copies if takes_x else None
         del ws
         tops = 2 * m * n * k / us / 1e6
         row = dict(us=round(us, 2), us_with_quantizer=round(us_q, 2), weight_GBps=round(nbytes / us / 1e3, 1),

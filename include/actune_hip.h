@@ -229,16 +229,17 @@ int actune_tokenwise_linear(const void* a, int a_layout, const float* a_scales, 
                             int64_t workspace_bytes, void* stream);
 
 /*
- * One-row tokenwise A8 linear with the per-row quantizer inside the GEMM
+ * Tokenwise A8 linear of 1-8 rows with the per-row quantizer inside the GEMM
  * launch: the result of actune_tokenwise_quantize (A = 8) on x followed by
  * actune_tokenwise_linear on its codes, bit for bit, in one launch fewer
- * (a split call is the split GEMM and the integer reduce). Writes the row's
- * activation scale to a_scales[0]; no codes are written. M must be 1, K at
- * most 16384, the weight layout K-major (the A8 pairs); x: bf16, f16 or f32
- * [1, K], 16-byte aligned. Workspace as for actune_tokenwise_linear with
+ * (a split call is the split GEMM and the integer reduce). Writes the rows'
+ * activation scales to a_scales[0 .. M-1]; no codes are written. M = 1 takes
+ * K <= 16384 and x in bf16, f16 or f32; M = 2, 3-4, 5-8 take K <= 16384,
+ * 8192, 4096 and bf16 or f16 x. The weight layout is K-major (the A8 pairs);
+ * x: [M, K], 16-byte aligned. Workspace as for actune_tokenwise_linear with
  * a_layout = ACTUNE_TW_ACT_A8. No counterpart in the reference, whose decode
  * launches the quantizer on its own (_quantize_decode_kernel,
- * decode_w4a8_triton.py:21-28); for one-token decode callers.
+ * decode_w4a8_triton.py:21-28); for decode callers.
  */
 int actune_tokenwise_linear_x(const void* x, int x_dtype, float* a_scales, const void* w, int w_layout,
                               const float* w_scale, const void* bias, int bias_dtype, void* out, int out_dtype,

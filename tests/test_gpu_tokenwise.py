@@ -272,22 +272,84 @@ def test_fused_row_quantization_magnitudes_against_oracle(scale):
     np.testing.assert_array_equal(s_out.cpu().numpy(), a_scales)
 
 
+@pytest.mark.parametrize("W,wl", [(4, _native.TW_KMAJOR_W4), (8, _native.TW_KMAJOR_W8), (2, _native.TW_KMAJOR_W2)])
+@pytest.mark.parametrize("m,n,k", [(2, 4096, 4096), (2, 256, 16384), (3, 11008, 4096), (4, 128, 8192),
+                                   (5, 4096, 4096), (8, 4096, 4096), (8, 11008, 4096), (8, 48, 256), (7, 64, 64),
+                                   (6, 256, 2048), (2, 32, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fused_rows_quantization_equals_two_step(W, wl, m, n, k, dtype):
+    """Two to eight rows quantized inside the split GEMM (each row padded
+    count P = 2, 4, 8 reads K <= 32768 / P): the quantizer + linear result
+    bit for bit, row scales included; K = 64 is unsplit, so the epilogue
+    reads the scales the launch computed."""
+    if k % {4: 32, 8: 64, 2: 128}[W]:
+        pytest.skip("in_features not allowed for this layout")
+    assert k <= _native.tokenwise_fused_max_k(m)
+    w, ws = _kmajor_weights(n, k, W, seed=n + k + W + m)
+    bias = torch.randn(n, device=DEV).to(dtype) if n % 3 == 0 else None
+    x = torch.randn(m, k, device=DEV) * 3
+    x[m // 2] *= 1e-3  # rows of different magnitude
+    x = x.to(dtype)
+    act, s = _native.tokenwise_quantize(x, 8)
+    need = _native.tokenwise_workspace_bytes(m, n, k, wl, _native.TW_ACT_A8)
+    ws_buf = torch.full((max(need, 1),), 0x5A, dtype=torch.uint8, device=DEV)
+    want = torch.empty(m, n, device=DEV, dtype=dtype)
+    _native.tokenwise_linear(act, _native.TW_ACT_A8, s, w, wl, ws, bias, n, k, _native.TW_EPI_A8, want,
+                             workspace=ws_buf if need else None)
+    got = torch.full((m, n), 3.0, device=DEV, dtype=dtype)
+    s_out = torch.full((m,), -1.0, device=DEV)
+    for _ in range(2):
+        _native.tokenwise_linear_x(x, s_out, w, wl, ws, bias, n, k, _native.TW_EPI_A8, got,
+                                   workspace=ws_buf if need else None)
+    torch.cuda.synchronize()
+    assert torch.equal(s_out, s)
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
+def test_fused_rows_quantization_against_oracle():
+    """Eight rows (zero, tiny, ordinary and large) through the fused launch
+    against the CPU oracle (per-row codes, exact dots, epilogue)."""
+    n, k, m = 256, 4096, 8
+    rng = np.random.default_rng(12)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    codes, wscale = O.weight_codes(w, 4, 8, gpu_division=True)
+    mags = np.array([0.0, 1e-30, 1e-4, 1.0, 3.0, 1e3, 0.5, 7.0], dtype=np.float32)[:, None]
+    x = torch.from_numpy((rng.standard_normal((m, k)) * mags).astype(np.float32)).to(torch.bfloat16)
+    out = torch.empty(m, n, device=DEV, dtype=torch.bfloat16)
+    s_out = torch.empty(m, device=DEV)
+    need = _native.tokenwise_workspace_bytes(m, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8)
+    ws_buf = torch.empty(max(need, 1), dtype=torch.uint8, device=DEV)
+    _native.tokenwise_linear_x(x.to(DEV), s_out, torch.from_numpy(O.pack_kmajor(codes, 4)).to(DEV),
+                               _native.TW_KMAJOR_W4, torch.from_numpy(wscale).to(DEV), None, n, k,
+                               _native.TW_EPI_A8, out, workspace=ws_buf if need else None)
+    a_codes, a_scales = O.tw_quantize_rows(bits(x), 8)
+    want = O.round_out(O.tw_epilogue(O.tw_dots(a_codes, codes), a_scales, wscale, None, 0), "bf16")
+    np.testing.assert_array_equal(bits(out), want)
+    np.testing.assert_array_equal(s_out.cpu().numpy(), a_scales)
+
+
 def test_fused_row_quantization_rejects_what_it_does_not_take():
-    x = torch.randn(2, 256, device=DEV).to(torch.bfloat16)
+    x = torch.randn(9, 256, device=DEV).to(torch.bfloat16)
     w = torch.zeros(256 // 2 * 64, dtype=torch.uint8, device=DEV)
     ws = torch.ones(64, device=DEV)
-    out = torch.empty(2, 64, device=DEV, dtype=torch.bfloat16)
-    s_out = torch.empty(1, device=DEV)
-    with pytest.raises(RuntimeError, match=r"\[1, K\]"):
+    out = torch.empty(9, 64, device=DEV, dtype=torch.bfloat16)
+    s_out = torch.empty(9, device=DEV)
+    with pytest.raises(RuntimeError, match=r"M <= 8"):
         _native.tokenwise_linear_x(x, s_out, w, _native.TW_KMAJOR_W4, ws, None, 64, 256, _native.TW_EPI_A8, out)
     lib = _native.lib()
-    # the C ABI checks the row count, K and the layout itself
+    # the C ABI checks the row count, K, the dtype and the layout itself
     rc = lib.actune_tokenwise_linear_x(x.data_ptr(), 0, s_out.data_ptr(), w.data_ptr(), _native.TW_KMAJOR_W4,
-                                       ws.data_ptr(), None, 0, out.data_ptr(), 0, 2, 64, 256, 0, None, 0, None)
-    assert rc != 0 and b"one row" in lib.actune_last_error()
+                                       ws.data_ptr(), None, 0, out.data_ptr(), 0, 9, 64, 256, 0, None, 0, None)
+    assert rc != 0 and b"1 to 8 rows" in lib.actune_last_error()
     rc = lib.actune_tokenwise_linear_x(x.data_ptr(), 0, s_out.data_ptr(), w.data_ptr(), _native.TW_KMAJOR_W4,
                                        ws.data_ptr(), None, 0, out.data_ptr(), 0, 1, 64, 32768, 0, None, 0, None)
     assert rc != 0 and b"16384" in lib.actune_last_error()
+    rc = lib.actune_tokenwise_linear_x(x.data_ptr(), 0, s_out.data_ptr(), w.data_ptr(), _native.TW_KMAJOR_W4,
+                                       ws.data_ptr(), None, 0, out.data_ptr(), 0, 5, 64, 8192, 0, None, 0, None)
+    assert rc != 0 and b"4096" in lib.actune_last_error()
+    rc = lib.actune_tokenwise_linear_x(x.data_ptr(), 2, s_out.data_ptr(), w.data_ptr(), _native.TW_KMAJOR_W4,
+                                       ws.data_ptr(), None, 0, out.data_ptr(), 0, 2, 64, 256, 0, None, 0, None)
+    assert rc != 0 and b"bf16 or f16" in lib.actune_last_error()
     rc = lib.actune_tokenwise_linear_x(x.data_ptr(), 0, s_out.data_ptr(), w.data_ptr(), _native.TW_ROWS_S4,
                                        ws.data_ptr(), None, 0, out.data_ptr(), 0, 1, 64, 256, 0, None, 0, None)
     assert rc != 0 and b"K-major" in lib.actune_last_error()
