@@ -227,8 +227,9 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
   // Decode (M <= 64, measured on MI355X at Llama/Gemma shapes): the decode
   // kernel beats the small-M and streaming kernels wherever a wave's K-range
   // fits its load ring. Calls that hand over bf16 x first try to quantize it
-  // inside the launch (M <= 8), then use the quantizer's codes
-  // (packed_default).
+  // inside the launch (where light), then use the quantizer's codes
+  // (packed_default, which also sends narrow problems above 64 tokens to the
+  // decode kernel).
   const int64_t tiles = (N + 15) / 16;
   auto fused_at = [&](int c) {
     const int nw = kSmallMWaves[c];

@@ -1,4 +1,5 @@
-// Decode packed group-64 GEMM for gfx950 (M <= 64 tokens): the launch is bound
+// Decode packed group-64 GEMM for gfx950 (M <= 1024 tokens in 16-token
+// blocks; the default up to 64 and for narrow problems): the launch is bound
 // by the HBM read of the packed weights, so the kernel is shaped to start
 // that read early and keep all of it in flight.
 //
