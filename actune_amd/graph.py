@@ -46,13 +46,14 @@ class GraphReplay:
         self.constants = {}
 
     @contextmanager
-    def scope(self):
+    def scope(self, plan=None):
         """Serve small literal GPU constants built inside the function from a
         cache filled during warm-up (a fresh host->device copy cannot be
         captured); each use gets a clone because callers update in place.
         Also bounds the shared activation caches to the call (the tokenwise
         per-row codes, graph.py:18-42, and the group-64 codes), enabled when
-        shared_a8 is set."""
+        shared_a8 is set; yields the group-64 cache. ``plan``: the group-64
+        sharing plan recorded by an earlier pass of the function."""
         make = torch.tensor
 
         def cached_tensor(data, *args, **kwargs):
@@ -69,9 +70,10 @@ class GraphReplay:
 
         from .kernels.grouped import shared_activation_scope
         from .kernels.tokenwise import shared_a8_cache_scope
-        with shared_a8_cache_scope(enabled=self.shared_a8), shared_activation_scope(enabled=self.shared_a8), \
+        with shared_a8_cache_scope(enabled=self.shared_a8), \
+                shared_activation_scope(enabled=self.shared_a8, plan=plan) as group_codes, \
                 patch.object(torch, "tensor", cached_tensor):
-            yield
+            yield group_codes
 
     def _key(self, leaves, spec):
         sig = []
@@ -90,15 +92,20 @@ class GraphReplay:
         args, kwargs = pytree.tree_unflatten(static, spec)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
+        # the first warm-up pass records which group-64 inputs several
+        # linears share; the second pass and the capture follow that plan
+        plan = None
         with torch.cuda.stream(side), torch.inference_mode():
             for _ in range(2):
-                with self.scope():
+                with self.scope(plan) as group_codes:
                     self.function(*args, **kwargs)
+                if plan is None:
+                    plan = group_codes.sharing_plan()
         torch.cuda.current_stream().wait_stream(side)
         for m in self.layers.values():
             m.calls = m.input_elements = 0
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph), torch.inference_mode(), self.scope():
+        with torch.cuda.graph(graph), torch.inference_mode(), self.scope(plan):
             output = self.function(*args, **kwargs)
         counts = {name: (m.calls, m.input_elements) for name, m in self.layers.items()}
         for name, m in self.layers.items():

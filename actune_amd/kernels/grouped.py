@@ -30,15 +30,44 @@ class SharedActivationCache:
     """Group-64 codes of the inputs seen in one scope, keyed by the source
     tensor object, the activation width and the channel scale: linears that
     read the same x at the same width (q/k/v, gate/up) then share one
-    quantizer launch, whatever their weight widths."""
+    quantizer launch, whatever their weight widths.
 
-    __slots__ = ("enabled", "entries", "hits", "misses")
+    The scope also records, per call in order, which source it read (by
+    order of first appearance), at which width and with which channel
+    scale; ``sharing_plan()`` turns that record into one flag per call: True
+    when another call of the pass reads the same input at the same width. A
+    later pass of the same function (GraphReplay's warm-up and capture) can
+    take that plan, so that an input only one linear reads is quantized
+    inside that linear's GEMM launch."""
 
-    def __init__(self, *, enabled=True):
+    __slots__ = ("enabled", "entries", "hits", "misses", "plan", "trace", "_sources")
+
+    def __init__(self, *, enabled=True, plan=None):
         self.enabled = enabled
         self.entries = []
         self.hits = 0
         self.misses = 0
+        self.plan = plan
+        self.trace = []
+        self._sources = []
+
+    def record(self, source, width, scale):
+        """Index of this call in the pass; notes what it reads."""
+        for i, seen in enumerate(self._sources):
+            if seen is source:
+                break
+        else:
+            i = len(self._sources)
+            self._sources.append(source)
+        self.trace.append((i, width, None if scale is None else id(scale)))
+        return len(self.trace) - 1
+
+    def sharing_plan(self):
+        """Per recorded call: True when another call reads the same input."""
+        counts = {}
+        for key in self.trace:
+            counts[key] = counts.get(key, 0) + 1
+        return tuple(counts[key] > 1 for key in self.trace)
 
 
 # largest M at which a call inside an enabled shared scope still quantizes
@@ -50,12 +79,13 @@ _SHARED_GROUP_STATE: ContextVar[SharedActivationCache | None] = ContextVar("actu
 
 
 @contextmanager
-def shared_activation_scope(*, enabled=True):
+def shared_activation_scope(*, enabled=True, plan=None):
     """Bound the group-64 code cache to one forward (GraphReplay enters it
     with its shared_a8 flag, the reference's switch for shared activation
     quantization, graph.py:18-42). Outside a scope nothing is cached, so a
-    tensor reused in place never sees stale codes."""
-    state = SharedActivationCache(enabled=enabled)
+    tensor reused in place never sees stale codes. ``plan``: the
+    sharing_plan() of an earlier pass of the same function."""
+    state = SharedActivationCache(enabled=enabled, plan=plan)
     token = _SHARED_GROUP_STATE.set(state)
     try:
         yield state
@@ -135,14 +165,20 @@ class GroupedLinear(torch.nn.Module):
         state = _SHARED_GROUP_STATE.get()
         m = flat.shape[0]
         if state is not None and state.enabled and m > 0:
+            src = x if source is None else source
+            call = state.record(src, self.a, input_scale)
             # Past _SHARED_FUSED_MAX_M tokens the codes are shared even where
             # the forward would quantize inside its GEMM: the in-launch
             # quantization then costs more than a GEMM on shared codes
             # (measured on MI355X at M = 50, 1024x1024: about 1.5 us per
-            # linear), and the linears of a scope usually read the same x.
-            if m > _SHARED_FUSED_MAX_M or not _native.forward_fuses_quantizer(
+            # linear). Without a plan the linears of a scope are taken to
+            # read the same x; with one, an input no other call of the pass
+            # reads at this width keeps the in-launch quantization.
+            plan = state.plan
+            shared = plan[call] if plan is not None and call < len(plan) else True
+            if (m > _SHARED_FUSED_MAX_M and shared) or not _native.forward_fuses_quantizer(
                     m, self.out_features, self.in_features, self.w, self.a, flat.dtype, self.config):
-                packed, scales = _shared_codes(state, x if source is None else source, flat, self.a, input_scale)
+                packed, scales = _shared_codes(state, src, flat, self.a, input_scale)
                 # an automatic config resolves to the choice for packed codes
                 out = _native.grouped_linear(packed, scales, self.packed_weight, self.weight_scale, self.bias,
                                              flat, self.w, self.a, self.config)

@@ -218,3 +218,27 @@ def test_install_bank_swaps_and_checks_bytes():
     with pytest.raises(ValueError, match="does not match the calibrated matrix: 2"):
         install_bank(wrong, toy_bank(), clips)
     assert isinstance(wrong[0], torch.nn.Linear)  # nothing replaced on failure
+
+
+def test_shared_activation_sharing_plan():
+    """The scope's record of one pass: a call is marked shared when another
+    call of the pass reads the same tensor at the same width and channel
+    scale (q/k/v and gate/up on x), and not when its input is read once (o
+    on the attention output) or at a width no other call uses."""
+    from actune_amd.kernels.grouped import SharedActivationCache, shared_activation_scope
+    x, attn, mlp = torch.zeros(2), torch.zeros(2), torch.zeros(2)
+    scale = torch.ones(2)
+    state = SharedActivationCache()
+    calls = [(x, 4, None), (x, 4, None), (x, 2, None), (attn, 4, None), (x, 4, None), (mlp, 4, None),
+             (mlp, 4, scale), (mlp, 4, scale)]
+    assert [state.record(*c) for c in calls] == list(range(len(calls)))
+    assert state.sharing_plan() == (True, True, False, False, True, False, True, True)
+    # a second pass of the same function reads fresh tensors in the same order
+    again = SharedActivationCache(plan=state.sharing_plan())
+    x2, attn2, mlp2 = torch.zeros(2), torch.zeros(2), torch.zeros(2)
+    for src, w, sc in [(x2, 4, None), (x2, 4, None), (x2, 2, None), (attn2, 4, None), (x2, 4, None),
+                       (mlp2, 4, None), (mlp2, 4, scale), (mlp2, 4, scale)]:
+        again.record(src, w, sc)
+    assert again.sharing_plan() == again.plan
+    with shared_activation_scope(enabled=True, plan=(False,)) as st:
+        assert st.plan == (False,) and st.enabled
