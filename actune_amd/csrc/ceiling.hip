@@ -25,13 +25,17 @@
 //  kind 3: kind 1 without the correction MFMA (its C operand taken from
 //          registers): the bound of an fp8 design whose correction costs
 //          nothing.
-//  kind 4: kind 0 on v_mfma_i32_32x32x32_i8 (the 16x16x64 form issues at
-//          half the int8 rate on gfx950): per 64-K group one 32-row weight
+//  kind 4: kind 0 on v_mfma_i32_32x32x32_i8 (a 32x32 tile holds four
+//          times the outputs per operand load): per 64-K group one 32-row weight
 //          tile unpacked from W4, two chained 32x32x32 MFMAs against each of
 //          two 32-token tiles, then the rescale of the previous group
 //          (16 outputs per lane and tile).
 //  kind 5: MFMAs alone, 16x16x64 (the instruction's own issue rate).
 //  kind 6: MFMAs alone, 32x32x32.
+//
+// It also holds the load floor of the decode launches
+// (actune_ceiling_decode_floor): the memory side of gemm_decode with nothing
+// else, timed by bench.py over the M=1 step's schedule.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -220,9 +224,100 @@ __global__ __launch_bounds__(256) void ceiling_mfma(const uint32_t* in, float* o
   out[blockIdx.x * 256 + threadIdx.x] = (float)t;
 }
 
+// ---------------------------------------------------------------- decode load floor
+// gemm_decode's weight traffic alone: a workgroup per 16-row tile of up to
+// four problems (grid y), nw waves splitting each row's bytes into ranges of
+// `slots` 64-byte slots; lane l loads 16 bytes of row n0 + l % 16 at byte
+// 16 (l / 16) of every slot of its wave's range, all loads issued at entry
+// (slots past the range or the row are switched off and read nothing). The
+// only arithmetic is an XOR of the loaded words, stored once per thread so
+// the loads stay. CONTIG: the same bytes per wave read as whole runs of 1
+// KiB of one row per instruction (lane l: bytes 16 l of the run): the
+// wave's rows are 16 / nw consecutive ones of the tile.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+constexpr uint32_t kOff = 0x80000000u;
+constexpr int kFloorMaxSlots = 8;
+
+struct FloorArgs {
+  const uint8_t* w[4];
+  int n[4];
+  int row_bytes, slots;
+  uint32_t* sink;
+};
+
+__device__ __forceinline__ Rsrc floor_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+template <bool CONTIG>
+__global__ __launch_bounds__(1024) void decode_load_floor(const FloorArgs a) {
+  const int p = (int)blockIdx.y, N = a.n[p], n0 = (int)blockIdx.x * 16;
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6, nw = (int)blockDim.x >> 6;
+  uint32_t x = 0;
+  if (n0 < N) {
+    const uint32_t rb = (uint32_t)a.row_bytes;
+    const Rsrc r = floor_rsrc(a.w[p], (uint32_t)N * rb);
+    v4u q[kFloorMaxSlots];
+    if constexpr (!CONTIG) {
+      const uint32_t start = (uint32_t)wave * (uint32_t)a.slots * 64u;
+      const uint32_t base = (uint32_t)(n0 + (lane & 15)) * rb + (uint32_t)(lane >> 4) * 16u + start;
+#pragma unroll
+      for (int s = 0; s < kFloorMaxSlots; ++s) {
+        const bool live = s < a.slots && start + (uint32_t)s * 64u < rb;
+        q[s] = __builtin_amdgcn_raw_buffer_load_b128(r, base + (uint32_t)s * 64u, live ? 0u : kOff, 0);
+      }
+    } else {
+      const int rpw = 16 / nw, runs = (int)((rb + 1023u) / 1024u);
+#pragma unroll
+      for (int s = 0; s < kFloorMaxSlots; ++s) {
+        const int row = n0 + wave * rpw + s / runs;
+        const uint32_t at = (uint32_t)(s % runs) * 1024u + (uint32_t)lane * 16u;
+        const bool live = s < rpw * runs && at < rb;
+        q[s] = __builtin_amdgcn_raw_buffer_load_b128(r, live ? (uint32_t)row * rb + at : kOff, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < kFloorMaxSlots; ++s) x ^= q[s][0] ^ q[s][1] ^ q[s][2] ^ q[s][3];
+  }
+  a.sink[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x] = x;
+}
+
 }  // namespace
 
 extern "C" {
+
+// Load floor of one decode launch: nprob (1-4) problems of n[p] rows of
+// row_bytes packed bytes at w[p], nw (4, 8, 16) waves per 16-row tile, the
+// decode kernel's 16-row x 64-byte loads (contig = 0) or whole 1 KiB row runs
+// per instruction (contig = 1). sink: at least ceil(max n / 16) * nprob * nw
+// * 64 dwords. 0 on success, -1 for arguments outside that (or a row split
+// needing more than 8 loads per wave), -2 on a launch error.
+int actune_ceiling_decode_floor(const void* const* w, const int64_t* n, int nprob, int64_t row_bytes, int nw,
+                                int contig, uint32_t* sink, int64_t sink_words, void* stream) {
+  if (!w || !n || !sink || nprob < 1 || nprob > 4 || (nw != 4 && nw != 8 && nw != 16) || row_bytes <= 0)
+    return -1;
+  FloorArgs a{};
+  int64_t nmax = 0;
+  for (int p = 0; p < nprob; ++p) {
+    if (!w[p] || n[p] <= 0 || n[p] * row_bytes >= ((int64_t)1 << 31)) return -1;
+    a.w[p] = static_cast<const uint8_t*>(w[p]);
+    a.n[p] = (int)n[p];
+    nmax = n[p] > nmax ? n[p] : nmax;
+  }
+  a.row_bytes = (int)row_bytes;
+  a.slots = (int)((row_bytes + 64 * nw - 1) / (64 * nw));
+  a.sink = sink;
+  const int64_t runs = (row_bytes + 1023) / 1024;
+  if (a.slots > kFloorMaxSlots || (contig && (16 / nw) * runs > kFloorMaxSlots)) return -1;
+  const int64_t tiles = (nmax + 15) / 16;
+  if (sink_words < tiles * nprob * nw * 64) return -1;
+  const dim3 grid((unsigned)tiles, (unsigned)nprob);
+  const hipStream_t st = (hipStream_t)stream;
+  if (contig) decode_load_floor<true><<<grid, nw * 64, 0, st>>>(a);
+  else decode_load_floor<false><<<grid, nw * 64, 0, st>>>(a);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
 
 // Input dwords per thread the kernels read (the caller passes blocks * 256 *
 // this many) and int8-equivalent multiply-accumulates per wave iteration of

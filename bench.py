@@ -283,6 +283,50 @@ def run_schedule(torch, _native, stack, W, A, siblings, steps, warmup):
     return ms, len(groups)
 
 
+def decode_floor(torch, _native, stack, W, A, steps, warmup):
+    """Load floor of the M=1 step: the sibling schedule over the same weight
+    buffers, each launch replaced by libactune_ceiling.so's decode load floor
+    (gemm_decode's weight loads with the wave count and grid the default
+    config gives the launch; no activations, no arithmetic beyond an XOR),
+    so the time is what the launch structure and the weight reads alone
+    cost. contig: the same bytes read as whole 1 KiB row runs per load."""
+    import ctypes
+    from actune_amd import build as _build
+    lib = ctypes.CDLL(str(_build.CEILING_LIB))
+    fn = lib.actune_ceiling_decode_floor
+    fn.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int64), ctypes.c_int, ctypes.c_int64,
+                   ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    sink = torch.empty(1 << 20, dtype=torch.int32, device="cuda")
+    by_layer = [stack[i:i + len(SHAPES)] for i in range(0, len(stack), len(SHAPES))]
+    launches = []
+    for layer in by_layer:
+        names = {e["name"]: e for e in layer}
+        for grp in ([names["q"], names["k"], names["v"]], [names["o"]], [names["gate"], names["up"]],
+                    [names["down"]]):
+            n_total, k = sum(e["n"] for e in grp), grp[0]["k"]
+            cfg = _native.default_config(1, n_total, k, W, A)
+            if cfg < 14:
+                return None
+            ptrs = (ctypes.c_void_p * len(grp))(*[e["w"].data_ptr() for e in grp])
+            rows = (ctypes.c_int64 * len(grp))(*[e["n"] for e in grp])
+            launches.append((ptrs, rows, len(grp), k * W // 8, (4, 8, 16)[cfg - 14]))
+    out = {}
+    for contig in (0, 1):
+        def step(contig=contig):
+            st = torch.cuda.current_stream().cuda_stream
+            for ptrs, rows, nprob, rb, nw in launches:
+                rc = fn(ptrs, rows, nprob, rb, nw, contig, sink.data_ptr(), sink.numel(), st)
+                if rc:
+                    raise RuntimeError(f"decode load floor failed ({rc})")
+        graph = capture(torch, step)
+        ms = time_graph(torch, graph, steps, warmup)
+        del graph
+        wbytes = sum(e["n"] * e["k"] * W // 8 for e in stack)
+        out["contiguous_1KiB" if contig else "decode_pattern"] = dict(
+            ms_per_step=round(ms, 4), weight_GBps=round(wbytes / (ms * 1e-3) / 1e9, 1))
+    return out
+
+
 def load_traffic(m):
     """Per-launch HBM bytes of the M=m step measured with rocprofv3 PMC
     counters (FETCH_SIZE / WRITE_SIZE scaled by a copy-kernel calibration),
@@ -386,8 +430,8 @@ def bench_ceilings(torch):
       cvt/fma rescale, kind 1 = exact fp8 32x32x64 MFMA for W, A <= 4 (one fma per
       output after an offset-correction MFMA), kind 2 = the same for A8 as two
       hi/lo planes, kind 3 = kind 1 with the correction taken for free, kind 4 =
-      kind 0 on int8 32x32x32 MFMAs (the 16x16x64 form issues at half the int8
-      rate on gfx950), kinds 5 / 6 = 16x16x64 / 32x32x32 int8 MFMAs alone."""
+      kind 0 on int8 32x32x32 MFMAs, kinds 5 / 6 = 16x16x64 / 32x32x32 int8
+      MFMAs alone."""
     import ctypes
     from actune_amd import build as _build
     lib = ctypes.CDLL(str(_build.CEILING_LIB))
@@ -688,6 +732,8 @@ def main():
                                          config=_native.default_config(m, n, k, W, A))
             del gph
         r["per_shape"] = per_shape
+        if m == 1:
+            r["floor"] = decode_floor(torch, _native, stack, W, A, args.steps, args.warmup)
         r["wbytes"] = sum(e["n"] * e["k"] * W // 8 for e in stack)
         r["abytes"] = sum(gemm_bytes(e["n"], e["k"], m, W, A) for e in stack)
         r["ops"] = sum(2 * m * e["n"] * e["k"] for e in stack)
@@ -739,6 +785,13 @@ def main():
             "siblings_warm_cache": {"ms_per_step": round(r["ms_warm"], 4),
                                     "note": "every layer reads the first layer's weights (cache-resident)"},
         }
+        if r.get("floor"):
+            fl = dict(r["floor"])
+            fl["step_vs_floor"] = round(fl["decode_pattern"]["ms_per_step"] / r["ms_sib"], 4)
+            fl["note"] = ("the same schedule and weight buffers with every launch reduced to the decode "
+                          "kernel's weight loads (libactune_ceiling.so): what the 48-launch structure costs "
+                          "with no compute; step_vs_floor = floor time / step time")
+            line["detail"][f"M={m}"]["load_floor"] = fl
     if not args.no_extra:
         line["detail"]["C3_prefill_M512"] = bench_prefill(torch, _native, 10, 3)
         line["detail"]["C4_gemma_W4A4"] = bench_gemma(torch, _native, 20, 5)

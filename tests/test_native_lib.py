@@ -45,6 +45,18 @@ def test_ceiling_library_loads_and_rejects_bad_arguments():
     buf = ctypes.create_string_buffer(16)
     assert lib.actune_ceiling_run(7, buf, buf, 1, 1, None) == -1     # unknown kind
     assert lib.actune_ceiling_run(0, buf, buf, 0, 1, None) == -1     # no workgroups
+    # the decode load floor checks its problems, wave count, row split and sink
+    f = lib.actune_ceiling_decode_floor
+    f.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int64), ctypes.c_int, ctypes.c_int64,
+                  ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    w = (ctypes.c_void_p * 1)(ctypes.addressof(buf))
+    n = (ctypes.c_int64 * 1)(4096)
+    sink = ctypes.create_string_buffer(4)
+    assert f(w, n, 0, 2048, 4, 0, sink, 1 << 20, None) == -1          # no problem
+    assert f(w, n, 1, 2048, 6, 0, sink, 1 << 20, None) == -1          # 6 waves
+    assert f(w, n, 1, 2048 * 9, 4, 0, sink, 1 << 20, None) == -1      # 9 slots per wave
+    assert f(w, n, 1, 2048, 4, 0, sink, 100, None) == -1              # sink too small
+    assert f(w, n, 1, 1 << 20, 4, 0, sink, 1 << 30, None) == -1       # buffer past 2 GiB
 
 
 def test_version_and_layout_selftest():
