@@ -231,9 +231,11 @@ __global__ __launch_bounds__(256) void ceiling_mfma(const uint32_t* in, float* o
 // 16 (l / 16) of every slot of its wave's range, all loads issued at entry
 // (slots past the range or the row are switched off and read nothing). The
 // only arithmetic is an XOR of the loaded words, stored once per thread so
-// the loads stay. CONTIG: the same bytes per wave read as whole runs of 1
+// the loads stay. MODE 1: the same bytes per wave read as whole runs of 1
 // KiB of one row per instruction (lane l: bytes 16 l of the run): the
-// wave's rows are 16 / nw consecutive ones of the tile.
+// wave's rows are 16 / nw consecutive ones of the tile. MODE 2: the wave's
+// K-range as in MODE 0, read 8 rows x 128 bytes per instruction (lane l: row
+// l % 8 of the instruction's half of the tile, bytes 16 (l / 8)).
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 constexpr uint32_t kOff = 0x80000000u;
@@ -250,7 +252,7 @@ __device__ __forceinline__ Rsrc floor_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-template <bool CONTIG>
+template <int MODE>
 __global__ __launch_bounds__(1024) void decode_load_floor(const FloorArgs a) {
   const int p = (int)blockIdx.y, N = a.n[p], n0 = (int)blockIdx.x * 16;
   const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6, nw = (int)blockDim.x >> 6;
@@ -259,7 +261,16 @@ __global__ __launch_bounds__(1024) void decode_load_floor(const FloorArgs a) {
     const uint32_t rb = (uint32_t)a.row_bytes;
     const Rsrc r = floor_rsrc(a.w[p], (uint32_t)N * rb);
     v4u q[kFloorMaxSlots];
-    if constexpr (!CONTIG) {
+    if constexpr (MODE == 2) {
+      const uint32_t start = (uint32_t)wave * (uint32_t)a.slots * 64u;
+#pragma unroll
+      for (int s = 0; s < kFloorMaxSlots; ++s) {
+        const uint32_t at = start + (uint32_t)(s >> 1) * 128u + (uint32_t)(lane >> 3) * 16u;
+        const int row = n0 + (lane & 7) + 8 * (s & 1);
+        const bool live = s < a.slots && start + (uint32_t)(s >> 1) * 128u < rb && at < rb;
+        q[s] = __builtin_amdgcn_raw_buffer_load_b128(r, live ? (uint32_t)row * rb + at : kOff, 0, 0);
+      }
+    } else if constexpr (MODE == 0) {
       const uint32_t start = (uint32_t)wave * (uint32_t)a.slots * 64u;
       const uint32_t base = (uint32_t)(n0 + (lane & 15)) * rb + (uint32_t)(lane >> 4) * 16u + start;
 #pragma unroll
@@ -289,8 +300,8 @@ extern "C" {
 
 // Load floor of one decode launch: nprob (1-4) problems of n[p] rows of
 // row_bytes packed bytes at w[p], nw (4, 8, 16) waves per 16-row tile, the
-// decode kernel's 16-row x 64-byte loads (contig = 0) or whole 1 KiB row runs
-// per instruction (contig = 1). sink: at least ceil(max n / 16) * nprob * nw
+// decode kernel's 16-row x 64-byte loads (contig = 0), whole 1 KiB row runs
+// per instruction (contig = 1) or 8-row x 128-byte loads (contig = 2). sink: at least ceil(max n / 16) * nprob * nw
 // * 64 dwords. 0 on success, -1 for arguments outside that (or a row split
 // needing more than 8 loads per wave), -2 on a launch error.
 int actune_ceiling_decode_floor(const void* const* w, const int64_t* n, int nprob, int64_t row_bytes, int nw,
@@ -309,13 +320,15 @@ int actune_ceiling_decode_floor(const void* const* w, const int64_t* n, int npro
   a.slots = (int)((row_bytes + 64 * nw - 1) / (64 * nw));
   a.sink = sink;
   const int64_t runs = (row_bytes + 1023) / 1024;
-  if (a.slots > kFloorMaxSlots || (contig && (16 / nw) * runs > kFloorMaxSlots)) return -1;
+  if (a.slots > kFloorMaxSlots || (contig == 1 && (16 / nw) * runs > kFloorMaxSlots)) return -1;
   const int64_t tiles = (nmax + 15) / 16;
   if (sink_words < tiles * nprob * nw * 64) return -1;
   const dim3 grid((unsigned)tiles, (unsigned)nprob);
   const hipStream_t st = (hipStream_t)stream;
-  if (contig) decode_load_floor<true><<<grid, nw * 64, 0, st>>>(a);
-  else decode_load_floor<false><<<grid, nw * 64, 0, st>>>(a);
+  if (contig == 1) decode_load_floor<1><<<grid, nw * 64, 0, st>>>(a);
+  else if (contig == 2) decode_load_floor<2><<<grid, nw * 64, 0, st>>>(a);
+  else if (contig == 0) decode_load_floor<0><<<grid, nw * 64, 0, st>>>(a);
+  else return -1;
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -289,7 +289,9 @@ def decode_floor(torch, _native, stack, W, A, steps, warmup):
     (gemm_decode's weight loads with the wave count and grid the default
     config gives the launch; no activations, no arithmetic beyond an XOR),
     so the time is what the launch structure and the weight reads alone
-    cost. contig: the same bytes read as whole 1 KiB row runs per load."""
+    cost. contiguous_1KiB: the same bytes read as whole 1 KiB row runs per
+    load; rows8x128B: each wave's K-range as in the decode kernel, read 8
+    rows x 128 bytes per load."""
     import ctypes
     from actune_amd import build as _build
     lib = ctypes.CDLL(str(_build.CEILING_LIB))
@@ -311,7 +313,7 @@ def decode_floor(torch, _native, stack, W, A, steps, warmup):
             rows = (ctypes.c_int64 * len(grp))(*[e["n"] for e in grp])
             launches.append((ptrs, rows, len(grp), k * W // 8, (4, 8, 16)[cfg - 14]))
     out = {}
-    for contig in (0, 1):
+    for contig in (0, 1, 2):
         def step(contig=contig):
             st = torch.cuda.current_stream().cuda_stream
             for ptrs, rows, nprob, rb, nw in launches:
@@ -322,7 +324,7 @@ def decode_floor(torch, _native, stack, W, A, steps, warmup):
         ms = time_graph(torch, graph, steps, warmup)
         del graph
         wbytes = sum(e["n"] * e["k"] * W // 8 for e in stack)
-        out["contiguous_1KiB" if contig else "decode_pattern"] = dict(
+        out[("decode_pattern", "contiguous_1KiB", "rows8x128B")[contig]] = dict(
             ms_per_step=round(ms, 4), weight_GBps=round(wbytes / (ms * 1e-3) / 1e9, 1))
     return out
 
