@@ -44,6 +44,8 @@ class GraphReplay:
         self.replays = 0
         self.fallbacks = 0
         self.constants = {}
+        # per graph key: the group-64 sharing plan its capture followed
+        self.sharing_plans = {}
 
     @contextmanager
     def scope(self, plan=None):
@@ -107,6 +109,7 @@ class GraphReplay:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph), torch.inference_mode(), self.scope(plan):
             output = self.function(*args, **kwargs)
+        self.sharing_plans[self._key(leaves, spec)] = plan
         counts = {name: (m.calls, m.input_elements) for name, m in self.layers.items()}
         for name, m in self.layers.items():
             m.calls, m.input_elements = saved[name]

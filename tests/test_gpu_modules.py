@@ -244,6 +244,11 @@ def test_graph_replay_precision_schedule_matches_eager(fused, shared):
             assert torch.equal(t_e, t_g), (i, profiles[i])
     assert torch.equal(x_eager, x_graph)
     assert {n: (m.calls, m.input_elements) for n, m in runtime.modules.items()} == eager_counts
+    if shared:
+        # x is read by k, v, gate, up and q; o's and down's inputs by one linear each
+        plans = list(replay.sharing_plans.values())
+        assert len(plans) == len(set(profiles))
+        assert all(len(p) == 7 and p[5:] == (False, False) and p[0] and p[1] for p in plans), plans
     for q in set(profiles):
         per_call = {n: 50 * EXPERT[n][1] for n in EXPERT}
         bank.check_request(q, per_call)
