@@ -32,6 +32,13 @@
 //          (16 outputs per lane and tile).
 //  kind 5: MFMAs alone, 16x16x64 (the instruction's own issue rate).
 //  kind 6: MFMAs alone, 32x32x32.
+//  kind 7: bf6 (e3m2) for W4A4: per group the W4 operand (32 two's-complement
+//          codes per lane) converted in registers to sign-magnitude e3m2
+//          fields (|c| <= 8 is the 4-bit exponent-mantissa field itself) and
+//          packed densely into six dwords, then v_mfma_scale_f32_32x32x64_f8f6f4
+//          on bf6 x bf6 against two 32-token tiles of pre-packed bf6
+//          activations, and one fma per output for the rescale.
+//  kind 8: bf6 x bf6 32x32x64 MFMAs alone (the format's own rate).
 //
 // It also holds the load floor of the decode launches
 // (actune_ceiling_decode_floor): the memory side of gemm_decode with nothing
@@ -224,6 +231,97 @@ __global__ __launch_bounds__(256) void ceiling_mfma(const uint32_t* in, float* o
   out[blockIdx.x * 256 + threadIdx.x] = (float)t;
 }
 
+// Six dwords of densely packed 6-bit fields from 32 two's-complement W4
+// codes (four dwords of nibbles): field = sign << 5 | |c|, which is the e3m2
+// encoding of c in units of 1/16 (the block scale restores the unit).
+__device__ __forceinline__ void w4_to_bf6(const uint32_t wp[4], v8i& out) {
+  uint32_t c24[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t b = (j & 1 ? wp[j >> 1] >> 4 : wp[j >> 1]) & 0x0F0F0F0Fu;  // four codes, one per byte
+    const uint32_t sg = (b >> 3) & 0x01010101u;
+    const uint32_t f = ((b ^ (sg * 0x0Fu)) + sg) | (sg << 5);                // sign-magnitude per byte
+    c24[j] = (f & 0x3Fu) | ((f >> 2) & 0xFC0u) | ((f >> 4) & 0x3F000u) | ((f >> 6) & 0xFC0000u);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t* c = c24 + 4 * h;
+    out[3 * h + 0] = (int)(c[0] | (c[1] << 24));
+    out[3 * h + 1] = (int)((c[1] >> 8) | (c[2] << 16));
+    out[3 * h + 2] = (int)((c[2] >> 16) | (c[3] << 8));
+  }
+  out[6] = out[7] = 0;
+}
+
+__global__ __launch_bounds__(256) void ceiling_bf6(const uint32_t* in, float* out, int iters) {
+  const uint32_t* s = in + (size_t)(blockIdx.x * 256 + threadIdx.x) * kWords;
+  uint32_t wp[4];
+  for (int j = 0; j < 4; ++j) wp[j] = s[j];
+  v8i a[2];
+  for (int t = 0; t < 2; ++t)
+    for (int j = 0; j < 8; ++j) a[t][j] = j < 6 ? (int)(s[4 + 6 * t + j] & 0x37DF7DF7u) : 0;
+  float sc[2][16];
+  for (int t = 0; t < 2; ++t)
+    for (int r = 0; r < 16; ++r) sc[t][r] = __uint_as_float(s[16 + 16 * t + r] & 0x3fffffffu);
+  v16f D[2][2];
+  float p[2][16], acc[2][16];
+  for (int t = 0; t < 2; ++t)
+    for (int r = 0; r < 16; ++r) { p[t][r] = acc[t][r] = 0.f; D[0][t][r] = D[1][t][r] = 0.f; }
+  const v16f zero16 = {};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      ACT_OPAQUE(wp[0]);
+      ACT_OPAQUE(wp[1]);
+      ACT_OPAQUE(wp[2]);
+      ACT_OPAQUE(wp[3]);
+      v8i w;
+      w4_to_bf6(wp, w);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        ACT_OPAQUE(a[t]);
+        // format 3 = bf6 (e3m2) for both operands; E8M0 scales 2^4 each undo
+        // the two 1/16 units
+        D[g & 1][t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a[t], zero16, 3, 3, 0, 131, 0, 131);
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[t][r] = __builtin_fmaf(D[(g + 1) & 1][t][r], sc[t][r], p[t][r]);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { acc[t][r] += p[t][r]; p[t][r] = 0.f; }
+  }
+  float t = 0.f;
+  for (int u = 0; u < 2; ++u)
+    for (int r = 0; r < 16; ++r) t += acc[u][r];
+  out[blockIdx.x * 256 + threadIdx.x] = t;
+}
+
+__global__ __launch_bounds__(256) void ceiling_bf6_mfma(const uint32_t* in, float* out, int iters) {
+  const uint32_t* s = in + (size_t)(blockIdx.x * 256 + threadIdx.x) * kWords;
+  v8i a, b;
+  for (int j = 0; j < 8; ++j) {
+    a[j] = j < 6 ? (int)(s[j] & 0x37DF7DF7u) : 0;
+    b[j] = j < 6 ? (int)(s[8 + j] & 0x37DF7DF7u) : 0;
+  }
+  v16f c[4];
+  for (int j = 0; j < 4; ++j)
+    for (int r = 0; r < 16; ++r) c[j][r] = 0.f;
+  for (int it = 0; it < iters; ++it) {
+    ACT_OPAQUE(a);
+    ACT_OPAQUE(b);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c[j & 3], 3, 3, 0, 127, 0, 127);
+  }
+  float t = 0.f;
+  for (int j = 0; j < 4; ++j)
+    for (int r = 0; r < 16; ++r) t += c[j][r];
+  out[blockIdx.x * 256 + threadIdx.x] = t;
+}
+
 // ---------------------------------------------------------------- decode load floor
 // gemm_decode's weight traffic alone: a workgroup per 16-row tile of up to
 // four problems (grid y), nw waves splitting each row's bytes into ranges of
@@ -336,14 +434,15 @@ int actune_ceiling_decode_floor(const void* const* w, const int64_t* n, int npro
 // this many) and int8-equivalent multiply-accumulates per wave iteration of
 // a kind: 4 groups of 64 K against a 16 x 64 tile (kind 0) or a 32 x 32 tile
 // (kinds 1-3), 4 * 65536, and the MFMA-only kinds 5 and 6 the same; kind 4
-// against a 32 x 64 tile, 8 * 65536. -1 for an unknown kind.
+// against a 32 x 64 tile, 8 * 65536; kind 7 two 32-token tiles and kind 8
+// eight 32x32x64 MFMAs, 8 * 65536 each. -1 for an unknown kind.
 int actune_ceiling_words(void) { return kWords; }
 long actune_ceiling_macs_per_iter(int kind) {
-  if (kind < 0 || kind > 6) return -1;
-  return kind == 4 ? 8L * 65536L : 4L * 65536L;
+  if (kind < 0 || kind > 8) return -1;
+  return kind == 4 || kind == 7 || kind == 8 ? 8L * 65536L : 4L * 65536L;
 }
 
-// Runs kind 0 .. 6 on `blocks` workgroups of 4 waves; 0 on success.
+// Runs kind 0 .. 8 on `blocks` workgroups of 4 waves; 0 on success.
 int actune_ceiling_run(int kind, const uint32_t* in, float* out, int blocks, int iters, void* stream) {
   if (!in || !out || blocks <= 0 || iters <= 0) return -1;
   const hipStream_t st = (hipStream_t)stream;
@@ -354,6 +453,8 @@ int actune_ceiling_run(int kind, const uint32_t* in, float* out, int blocks, int
   else if (kind == 4) ceiling_int8_32<<<blocks, 256, 0, st>>>(in, out, iters);
   else if (kind == 5) ceiling_mfma<false><<<blocks, 256, 0, st>>>(in, out, iters);
   else if (kind == 6) ceiling_mfma<true><<<blocks, 256, 0, st>>>(in, out, iters);
+  else if (kind == 7) ceiling_bf6<<<blocks, 256, 0, st>>>(in, out, iters);
+  else if (kind == 8) ceiling_bf6_mfma<<<blocks, 256, 0, st>>>(in, out, iters);
   else return -1;
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }

@@ -433,7 +433,10 @@ def bench_ceilings(torch):
       output after an offset-correction MFMA), kind 2 = the same for A8 as two
       hi/lo planes, kind 3 = kind 1 with the correction taken for free, kind 4 =
       kind 0 on int8 32x32x32 MFMAs, kinds 5 / 6 = 16x16x64 / 32x32x32 int8
-      MFMAs alone."""
+      MFMAs alone, kind 7 = bf6 (e3m2) 32x32x64 for W4A4 with the W4 codes
+      converted to packed 6-bit fields in registers (each conversion feeding
+      two token tiles), kind 8 = bf6 MFMAs alone. frac is against the int8
+      peak for every kind."""
     import ctypes
     from actune_amd import build as _build
     lib = ctypes.CDLL(str(_build.CEILING_LIB))
@@ -458,7 +461,9 @@ def bench_ceilings(torch):
              3: "fp8 32x32x64, W,A <= 4, correction for free (unreachable bound)",
              4: "int8 32x32x32 + cvt/fma rescale",
              5: "int8 16x16x64 MFMAs alone",
-             6: "int8 32x32x32 MFMAs alone"}
+             6: "int8 32x32x32 MFMAs alone",
+             7: "bf6 32x32x64, W4A4: W4 codes converted to packed e3m2 in registers, 2 token tiles",
+             8: "bf6 32x32x64 MFMAs alone (the fp6 peak is twice int8's)"}
     iters, st = 4000, torch.cuda.current_stream()
     ceil = {}
     for waves_per_simd in (2, 4):

@@ -37,13 +37,14 @@ def test_ceiling_library_loads_and_rejects_bad_arguments():
     lib.actune_ceiling_macs_per_iter.restype = ctypes.c_long
     lib.actune_ceiling_macs_per_iter.argtypes = [ctypes.c_int]
     assert lib.actune_ceiling_words() == 48
-    assert [lib.actune_ceiling_macs_per_iter(k) for k in range(7)] == [4 * 65536] * 4 + [8 * 65536] + [4 * 65536] * 2
-    assert lib.actune_ceiling_macs_per_iter(7) == -1
+    assert [lib.actune_ceiling_macs_per_iter(k) for k in range(9)] == \
+        [4 * 65536] * 4 + [8 * 65536] + [4 * 65536] * 2 + [8 * 65536] * 2
+    assert lib.actune_ceiling_macs_per_iter(9) == -1
     lib.actune_ceiling_run.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                        ctypes.c_void_p]
     assert lib.actune_ceiling_run(0, None, None, 1, 1, None) == -1
     buf = ctypes.create_string_buffer(16)
-    assert lib.actune_ceiling_run(7, buf, buf, 1, 1, None) == -1     # unknown kind
+    assert lib.actune_ceiling_run(9, buf, buf, 1, 1, None) == -1     # unknown kind
     assert lib.actune_ceiling_run(0, buf, buf, 0, 1, None) == -1     # no workgroups
     # the decode load floor checks its problems, wave count, row split and sink
     f = lib.actune_ceiling_decode_floor
