@@ -1038,9 +1038,15 @@ Geometry pick_geometry(int64_t M, int64_t N, int wl) {
 }
 
 // K splits. Small M: enough splits that each workgroup's range fits its
-// entry loads and the grid holds about two workgroups per CU. Large M: a
-// split only for grids below half a workgroup per CU, while the partials
-// (S x M x N int32) stay small against the operands.
+// entry loads and the grid holds about two workgroups per CU. Large M: the
+// split doubles while the grid holds fewer workgroups than CUs and the
+// partials (S x M x N int32) stay within 8 MiB; below half a workgroup per
+// CU each split keeps at least 4 K-steps, from there to one per CU at least
+// 16. Measured on MI355X over the K-major layouts at M = 64-448 on the
+// Llama-2-7B shapes, the second rule (a 128-workgroup grid split in two)
+// takes M = 256 at N = 4096 from 27.7 to 23.2 us (K = 4096) and from 52.9
+// to 33.9 us (K = 11008, W4A8), and M = 96-128 at K = 11008 by 19-32%;
+// splitting to fewer than 16 K-steps lost up to 13%.
 int pick_splits(int64_t M, int64_t N, int64_t K, int wl, const Geometry& g) {
   const int64_t tiles = tiles_of(M, N, g), steps = steps_of(K, wl);
   if (g.ns > 0) {
@@ -1048,7 +1054,8 @@ int pick_splits(int64_t M, int64_t N, int64_t K, int wl, const Geometry& g) {
     return (int)std::min(s, steps);
   }
   int64_t s = 1;
-  while (tiles * s < 128 && s * 8 <= steps && 2 * s * M * N * 4 <= ((int64_t)8 << 20)) s *= 2;
+  while (tiles * s < 256 && s * (tiles * s < 128 ? 8 : 32) <= steps && 2 * s * M * N * 4 <= ((int64_t)8 << 20))
+    s *= 2;
   return (int)s;
 }
 

@@ -499,7 +499,7 @@ def bench_tokenwise(torch, _native, steps, warmup):
     the reference's weight layouts (K-major nibble pairs / int8 / quarters,
     row-major S4 / S2). M=1 and M=8 on the Llama-2-7B shapes for W4A8 (the
     reference's decode use), rotating over >= 256 MB of distinct weights,
-    and M=512 for every pair (the MFMA-bound case: the int32 accumulator
+    M=256 for W4A8, and M=512 for every pair (the MFMA-bound case: the int32 accumulator
     needs no per-group rescale). Each launch pair = quantizer + GEMM; at M=1
     and 8 also the GEMM that quantizes the rows itself where it takes K
     (us_quantizer_fused)."""
@@ -553,6 +553,10 @@ def bench_tokenwise(torch, _native, steps, warmup):
             copies = max(12, (300 << 20) // (n * k // 2))
             row[f"{n}x{k}"] = run("W4A8", 4, 8, m, n, k, copies)
         out[f"W4A8_M={m}"] = row
+    row = {}  # M = 256: half a workgroup per CU at N = 4096, where the GEMM splits K in two
+    for _, n, k in (SHAPES[0], SHAPES[4], SHAPES[6]):
+        row[f"{n}x{k}"] = run("W4A8", 4, 8, 256, n, k, 4)
+    out["W4A8_M=256"] = row
     for name, W, A in TW_PAIRS:
         row = {}
         for _, n, k in (SHAPES[0], SHAPES[4], SHAPES[6]):

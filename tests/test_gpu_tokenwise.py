@@ -130,13 +130,13 @@ def test_w4a8_ragged_k_tail():
 # ---------------------------------------------------------------- split-K and decode
 @pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (1, 11008, 4096), (1, 4096, 11008), (8, 4096, 4096),
                                    (2, 256, 2048), (64, 512, 4096), (512, 4096, 4096), (512, 8192, 2048),
-                                   (200, 11008, 512)])
+                                   (200, 11008, 512), (256, 4096, 4096), (128, 4096, 11008)])
 def test_split_k_full_size_sampled(m, n, k):
     """Llama-2-7B / Gemma shapes through the C ABI with every layout pair:
     the K split the library picks is exact, and so is each large-M ring
     configuration (M = 512 at N = 4096: fewer than 512 tiles of 64 x 128;
-    N = 8192: 512 tiles; M = 200: a ragged last row tile), checked on 64
-    sampled columns."""
+    N = 8192: 512 tiles; M = 200: a ragged last row tile; M = 256 and 128:
+    ring grids split in two or four), checked on 64 sampled columns."""
     x, w, _ = seeded_inputs(m, k, n, seed=m + n + k)
     xd = x.to(DEV)
     cols = np.sort(np.random.default_rng(n).choice(n, size=64, replace=False))

@@ -181,6 +181,28 @@ def test_streaming_config_reports_its_own_limit():
     assert rc == 1 and "M <= 16" in _err()
 
 
+def test_tokenwise_large_m_split_rule():
+    """Tokenwise ring GEMM (M > 32) K splits, read from the workspace the
+    library asks for (S x M x N int32 when S > 1): the split doubles while the
+    64 x 128 grid has fewer workgroups than the 256 CUs and the partials stay
+    within 8 MiB, each split keeping 4 K-steps below 128 workgroups and 16
+    from there."""
+    a8, w4, w2 = _native.TW_ACT_A8, _native.TW_KMAJOR_W4, _native.TW_KMAJOR_W2
+
+    def split_of(m, n, k, wl=w4):
+        need = _native.tokenwise_workspace_bytes(m, n, k, wl, a8)
+        assert need % (m * n * 4) == 0
+        return max(1, need // (m * n * 4))
+
+    assert split_of(512, 4096, 4096) == 1    # 256 workgroups
+    assert split_of(256, 4096, 4096) == 2    # 128 workgroups, 64 K-steps
+    assert split_of(128, 4096, 11008) == 4   # 64 workgroups, 172 K-steps, 8 MiB of partials
+    assert split_of(64, 4096, 4096) == 4     # a third doubling would leave 8 K-steps
+    assert split_of(128, 4096, 4096, w2) == 2  # 32 K-steps of 128
+    assert split_of(320, 4096, 4096) == 1    # two splits would hold 10 MiB of partials
+    assert split_of(64, 512, 4096) == 16     # 4 workgroups: down to 4 K-steps
+
+
 @pytest.mark.parametrize("M", range(1, 17))
 def test_decode_row_division_is_exact_over_its_range(M):
     """gemm_decode divides group-row indices r = group * M + token by M as
