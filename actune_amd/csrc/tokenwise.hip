@@ -908,26 +908,52 @@ __global__ __launch_bounds__(kThreads) void tw_gemm_ring(const TwArgs args) {
   finish_tile<WL, AL, EPI, MT, NT>(args, acc, m0 + wm * 16 * MT + 4 * kb, n0 + wn * 16 * NT + r16, z);
 }
 
-// Adds the K splits' partial sums of one output each and finishes it.
-template <int EPI>
+// Adds the K splits' partial sums and finishes the outputs: a thread takes
+// CPT consecutive columns (1 or 4) of row blockIdx.y (+ gridDim.y ...), with
+// all of up to NS splits' loads in flight at once (one round trip; more
+// splits loop by NS). The partials of split s sit at s * M * N + m * N + n.
+// With four columns and N a multiple of 4 (16-byte aligned quads) each split
+// is one 16-byte load, otherwise one 4-byte load per column; columns past N
+// are loaded as zeros and not stored.
+template <int EPI, int NS, int CPT>
 __global__ __launch_bounds__(kThreads) void tw_reduce(const TwArgs args, int shift) {
-  const long total = (long)args.M * args.N;
-  const long idx = (long)blockIdx.x * kThreads + threadIdx.x;
-  if (idx >= total) return;
-  // all splits' loads in flight at once (splits past S read zeros), one
-  // round trip for up to 32 splits
-  const Rsrc pr = make_rsrc(args.partial, (uint32_t)((size_t)args.splits * total * 4));
-  int32_t sum = 0;
-  for (int s0 = 0; s0 < args.splits; s0 += 32) {
-    int32_t v[32];
+  static_assert(CPT == 1 || CPT == 4, "one or four columns per thread");
+  const int M = args.M, N = args.N, S = args.splits;
+  const int n0 = CPT * ((int)blockIdx.x * kThreads + (int)threadIdx.x);
+  if (n0 >= N) return;
+  const uint32_t total = (uint32_t)M * (uint32_t)N;
+  const Rsrc pr = make_rsrc(args.partial, (uint32_t)S * total * 4u);
+  const bool quads = CPT == 4 && (N & 3) == 0;
+  for (int m = (int)blockIdx.y; m < M; m += (int)gridDim.y) {
+    const uint32_t base = (uint32_t)m * (uint32_t)N + (uint32_t)n0;
+    int32_t sum[CPT] = {};
+    for (int s0 = 0; s0 < S; s0 += NS) {
+      int32_t v[NS][CPT];
+      if (quads) {
 #pragma unroll
-    for (int j = 0; j < 32; ++j)
-      v[j] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(
-          pr, s0 + j < args.splits ? (uint32_t)(((size_t)(s0 + j) * total + idx) * 4) : kOff, 0, 0);
+        for (int j = 0; j < NS; ++j) {
+          const v4u q = __builtin_amdgcn_raw_buffer_load_b128(
+              pr, s0 + j < S ? ((uint32_t)(s0 + j) * total + base) * 4u : kOff, 0, 0);
 #pragma unroll
-    for (int j = 0; j < 32; ++j) sum += v[j];
+          for (int r = 0; r < CPT; ++r) v[j][r] = (int32_t)q[r];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < NS; ++j)
+#pragma unroll
+          for (int r = 0; r < CPT; ++r)
+            v[j][r] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                pr, s0 + j < S && n0 + r < N ? ((uint32_t)(s0 + j) * total + base + (uint32_t)r) * 4u : kOff, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < NS; ++j)
+#pragma unroll
+        for (int r = 0; r < CPT; ++r) sum[r] += v[j][r];
+    }
+#pragma unroll
+    for (int r = 0; r < CPT; ++r)
+      if (n0 + r < N) store_result<EPI>(args, m, n0 + r, sum[r] >> shift);
   }
-  store_result<EPI>(args, (int)(idx / args.N), (int)(idx % args.N), sum >> shift);
 }
 
 // ---------------------------------------------------------------- quantizer
@@ -1059,16 +1085,34 @@ int pick_splits(int64_t M, int64_t N, int64_t K, int wl, const Geometry& g) {
   return (int)s;
 }
 
+// The reduce of a split launch: loads per round trip sized to the splits;
+// rows on grid y (at most 65535, more rows loop); four columns per thread
+// only where that still leaves at least 256 workgroups (one per CU). Measured
+// on MI355X (W4A8): four columns took M = 256 at N = 4096 from 23.1 to 20.4
+// us (2 splits, K = 4096), while at M = 1 and 8 the 4-16 workgroups it left
+// made the linear 0.4-1.1 us slower than one column per thread.
+template <int EPI, int CPT>
+void launch_reduce_c(const TwArgs& a, int shift, hipStream_t st) {
+  const dim3 grid((unsigned)((a.N + CPT * kThreads - 1) / (CPT * kThreads)), (unsigned)std::min(a.M, 65535));
+  if (a.splits <= 2) tw_reduce<EPI, 2, CPT><<<grid, kThreads, 0, st>>>(a, shift);
+  else if (a.splits <= 4) tw_reduce<EPI, 4, CPT><<<grid, kThreads, 0, st>>>(a, shift);
+  else if (a.splits <= 8) tw_reduce<EPI, 8, CPT><<<grid, kThreads, 0, st>>>(a, shift);
+  else if (a.splits <= 16) tw_reduce<EPI, 16, CPT><<<grid, kThreads, 0, st>>>(a, shift);
+  else tw_reduce<EPI, 32, CPT><<<grid, kThreads, 0, st>>>(a, shift);
+}
+
+template <int EPI>
+void launch_reduce(const TwArgs& a, int shift, hipStream_t st) {
+  if ((int64_t)a.M * a.N >= (int64_t)4 * kThreads * 256) launch_reduce_c<EPI, 4>(a, shift, st);
+  else launch_reduce_c<EPI, 1>(a, shift, st);
+}
+
 template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, int XDT = -1, int XR = 1>
 void launch_gemm_t(const TwArgs& a, hipStream_t st) {
   constexpr int TM = 16 * MT * WM, TN = 16 * NT * (4 / WM);
   const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM), (unsigned)a.splits);
   tw_gemm<WL, AL, EPI, WM, MT, NT, NB, XDT, XR><<<grid, kThreads, 0, st>>>(a);
-  if (a.splits > 1) {
-    const long total = (long)a.M * a.N;
-    constexpr int SHIFT = WTraits<WL>::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0);
-    tw_reduce<EPI><<<(unsigned)((total + kThreads - 1) / kThreads), kThreads, 0, st>>>(a, SHIFT);
-  }
+  if (a.splits > 1) launch_reduce<EPI>(a, WTraits<WL>::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0), st);
 }
 
 // LDS bytes of a tw_gemm_ring launch: D slots, and the junk KiB per wave when
@@ -1088,11 +1132,7 @@ void launch_ring_t(const TwArgs& a, hipStream_t st) {
   if constexpr (lds > 64 * 1024) allow_dynamic_lds<tw_gemm_ring<WL, AL, EPI, WM, MT, NT, KS, D>>();
   const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM), (unsigned)a.splits);
   tw_gemm_ring<WL, AL, EPI, WM, MT, NT, KS, D><<<grid, kThreads, lds, st>>>(a);
-  if (a.splits > 1) {
-    const long total = (long)a.M * a.N;
-    constexpr int SHIFT = WTraits<WL>::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0);
-    tw_reduce<EPI><<<(unsigned)((total + kThreads - 1) / kThreads), kThreads, 0, st>>>(a, SHIFT);
-  }
+  if (a.splits > 1) launch_reduce<EPI>(a, WTraits<WL>::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0), st);
 }
 
 template <int WL, int AL, int EPI>

@@ -160,6 +160,31 @@ def test_split_k_full_size_sampled(m, n, k):
         np.testing.assert_array_equal(bits(out)[:, cols], want, err_msg=f"W{W}A{A}")
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 50, 2048), (3, 1001, 4096), (40, 30, 4096), (8, 4095, 1024), (1, 128, 8192),
+                                   (40, 7001, 1024)])
+def test_split_reduce_columns(m, n, k):
+    """The row-major S4 / S2 layouts take any out_features. The reduce adds
+    the K splits one column per thread, or four where M * N >= 262144 (M =
+    40, N = 7001: four 4-byte loads per split, zeros past N; N a multiple of
+    4 takes one 16-byte load, as in the full-size cases above); more than 32
+    splits (N = 1001 at K = 4096: 64; N = 128 at K = 8192: 128) take several
+    rounds. Every column against the oracle."""
+    x, w, _ = seeded_inputs(m, k, n, seed=m * 7 + n)
+    xd = x.to(DEV)
+    for W, wl in ((4, _native.TW_ROWS_S4), (2, _native.TW_ROWS_S2)):
+        codes, scale = O.weight_codes(w.float().numpy(), W, 4, gpu_division=True)
+        act, s = _native.tokenwise_quantize(xd, 4)
+        need = _native.tokenwise_workspace_bytes(m, n, k, wl, _native.TW_ACT_A4)
+        assert need >= 2 * m * n * 4, "the case must split K"
+        ws = torch.full((need,), 0x5A, dtype=torch.uint8, device=DEV)
+        out = torch.empty(m, n, device=DEV, dtype=torch.bfloat16)
+        _native.tokenwise_linear(act, _native.TW_ACT_A4, s, torch.from_numpy(O.pack_rows(codes, W)).to(DEV), wl,
+                                 torch.from_numpy(scale).to(DEV), None, n, k, _native.TW_EPI_A4, out, workspace=ws)
+        a_codes, a_scales = O.tw_quantize_rows(bits(x), 4)
+        want = O.round_out(O.tw_epilogue(O.tw_dots(a_codes, codes), a_scales, scale, None, 1), "bf16")
+        np.testing.assert_array_equal(bits(out), want, err_msg=f"W{W}A4")
+
+
 def test_w4a8_decode_graph_plan_and_counters():
     """M = 1 bf16: the module replays its DecodeGraphPlan (quantizer + split-K
     GEMM in one hipGraph); outputs equal the direct path and the oracle, and
