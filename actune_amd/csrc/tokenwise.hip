@@ -1063,8 +1063,13 @@ Geometry pick_geometry(int64_t M, int64_t N, int wl) {
   return km ? Geometry{2, 2, 4, 0, 2, 4} : Geometry{2, 2, 2, 0, 2, 4};
 }
 
-// K splits. Small M: enough splits that each workgroup's range fits its
-// entry loads and the grid holds about two workgroups per CU. Large M: the
+// K splits. Small M: the fewest splits whose ranges fit a workgroup's entry
+// loads (each workgroup then has the most bytes in flight, and the reduce
+// the fewest partials). Measured on MI355X (W4A8, M = 1 and 8) against
+// splitting further until the grid held 512 workgroups: 4096x4096 8.1 ->
+// 7.6 us, 1024x4096 8.7 -> 6.7 us, 256x2048 6.9 -> 6.1 us, and with the rows
+// quantized in the launch at M = 8, 4096x4096 10.6 -> 8.2 us; grids of 1024
+// or 2048 workgroups were slower still. Large M: the
 // split doubles while the grid holds fewer workgroups than CUs and the
 // partials (S x M x N int32) stay within 8 MiB; below half a workgroup per
 // CU each split keeps at least 4 K-steps, from there to one per CU at least
@@ -1075,10 +1080,7 @@ Geometry pick_geometry(int64_t M, int64_t N, int wl) {
 // splitting to fewer than 16 K-steps lost up to 13%.
 int pick_splits(int64_t M, int64_t N, int64_t K, int wl, const Geometry& g) {
   const int64_t tiles = tiles_of(M, N, g), steps = steps_of(K, wl);
-  if (g.ns > 0) {
-    int64_t s = std::max((steps + g.ns - 1) / g.ns, (512 + tiles - 1) / tiles);
-    return (int)std::min(s, steps);
-  }
+  if (g.ns > 0) return (int)((steps + g.ns - 1) / g.ns);
   int64_t s = 1;
   while (tiles * s < 256 && s * (tiles * s < 128 ? 8 : 32) <= steps && 2 * s * M * N * 4 <= ((int64_t)8 << 20))
     s *= 2;
@@ -1098,6 +1100,7 @@ void launch_reduce_c(const TwArgs& a, int shift, hipStream_t st) {
   else if (a.splits <= 4) tw_reduce<EPI, 4, CPT><<<grid, kThreads, 0, st>>>(a, shift);
   else if (a.splits <= 8) tw_reduce<EPI, 8, CPT><<<grid, kThreads, 0, st>>>(a, shift);
   else if (a.splits <= 16) tw_reduce<EPI, 16, CPT><<<grid, kThreads, 0, st>>>(a, shift);
+  else if (a.splits <= 24) tw_reduce<EPI, 24, CPT><<<grid, kThreads, 0, st>>>(a, shift);
   else tw_reduce<EPI, 32, CPT><<<grid, kThreads, 0, st>>>(a, shift);
 }
 

@@ -160,15 +160,15 @@ def test_split_k_full_size_sampled(m, n, k):
         np.testing.assert_array_equal(bits(out)[:, cols], want, err_msg=f"W{W}A{A}")
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 50, 2048), (3, 1001, 4096), (40, 30, 4096), (8, 4095, 1024), (1, 128, 8192),
-                                   (40, 7001, 1024)])
+@pytest.mark.parametrize("m,n,k", [(1, 50, 2048), (3, 1001, 4096), (40, 30, 4096), (8, 4095, 1024), (1, 128, 20480),
+                                   (2, 75, 20480), (40, 7001, 1024)])
 def test_split_reduce_columns(m, n, k):
     """The row-major S4 / S2 layouts take any out_features. The reduce adds
     the K splits one column per thread, or four where M * N >= 262144 (M =
     40, N = 7001: four 4-byte loads per split, zeros past N; N a multiple of
     4 takes one 16-byte load, as in the full-size cases above); more than 32
-    splits (N = 1001 at K = 4096: 64; N = 128 at K = 8192: 128) take several
-    rounds. Every column against the oracle."""
+    splits (K = 20480: 40) take two rounds. Every column against the
+    oracle."""
     x, w, _ = seeded_inputs(m, k, n, seed=m * 7 + n)
     xd = x.to(DEV)
     for W, wl in ((4, _native.TW_ROWS_S4), (2, _native.TW_ROWS_S2)):

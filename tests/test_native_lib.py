@@ -181,12 +181,13 @@ def test_streaming_config_reports_its_own_limit():
     assert rc == 1 and "M <= 16" in _err()
 
 
-def test_tokenwise_large_m_split_rule():
-    """Tokenwise ring GEMM (M > 32) K splits, read from the workspace the
-    library asks for (S x M x N int32 when S > 1): the split doubles while the
-    64 x 128 grid has fewer workgroups than the 256 CUs and the partials stay
-    within 8 MiB, each split keeping 4 K-steps below 128 workgroups and 16
-    from there."""
+def test_tokenwise_split_rule():
+    """Tokenwise GEMM K splits, read from the workspace the library asks for
+    (S x M x N int32 when S > 1). Ring GEMM (M > 32): the split doubles while
+    the 64 x 128 grid has fewer workgroups than the 256 CUs and the partials
+    stay within 8 MiB, each split keeping 4 K-steps below 128 workgroups and
+    16 from there. M <= 32: the fewest splits whose ranges fit the entry
+    loads."""
     a8, w4, w2 = _native.TW_ACT_A8, _native.TW_KMAJOR_W4, _native.TW_KMAJOR_W2
 
     def split_of(m, n, k, wl=w4):
@@ -201,6 +202,13 @@ def test_tokenwise_large_m_split_rule():
     assert split_of(128, 4096, 4096, w2) == 2  # 32 K-steps of 128
     assert split_of(320, 4096, 4096) == 1    # two splits would hold 10 MiB of partials
     assert split_of(64, 512, 4096) == 16     # 4 workgroups: down to 4 K-steps
+    # M <= 32: the fewest splits whose ranges fit the 8 K-steps a workgroup
+    # loads at entry (4 for the int8 K-major layout)
+    assert split_of(1, 4096, 4096) == 8
+    assert split_of(8, 4096, 11008) == 22
+    assert split_of(1, 256, 2048) == 4
+    assert split_of(1, 4096, 4096, _native.TW_KMAJOR_W8) == 16
+    assert split_of(32, 128, 512) == 1       # one workgroup range: no reduce
 
 
 @pytest.mark.parametrize("M", range(1, 17))
