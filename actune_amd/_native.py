@@ -32,6 +32,11 @@ class _Target(ctypes.Structure):
     _fields_ = [("w", _P), ("w_scale", _P), ("bias", _P), ("out", _P), ("N", _I64)]
 
 
+class _TwTarget(ctypes.Structure):
+    """actune_tw_target"""
+    _fields_ = [("w", _P), ("w_scale", _P), ("bias", _P), ("out", _P)]
+
+
 def lib():
     """The loaded library; raises if it has not been built."""
     global _LIB
@@ -57,6 +62,8 @@ def lib():
                                                _I64, _P]
         so.actune_tokenwise_linear_x.argtypes = [_P, _I, _P, _P, _I, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I,
                                                  _P, _I64, _P]
+        so.actune_tokenwise_linear_multi.argtypes = [_P, _I, _P, _I, _P, _I, ctypes.POINTER(_TwTarget), _I, _I, _I,
+                                                     _I64, _I64, _I64, _I, _P, _I64, _P]
         so.actune_forward_fuses_quantizer.argtypes = [_I64, _I64, _I64, _I, _I, _I, _I]
         so.actune_config_valid.argtypes = [_I, _I64]
         so.actune_default_config.argtypes = [_I64, _I64, _I64, _I, _I]
@@ -76,6 +83,30 @@ def _ptr(t):
 
 def _stream(device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+_HIP = None
+
+
+def capture_id(device=None) -> int:
+    """Id of the stream capture the current stream of `device` is recording
+    (hipStreamGetCaptureInfo), 0 when it records none. Caches of device
+    tensors use it so that a captured launch never reads a tensor written
+    outside its graph, nor an eager call one written only at replay."""
+    global _HIP
+    if not torch.cuda.is_current_stream_capturing():
+        return 0
+    if _HIP is None:
+        # resolved through the library's handle: the HIP runtime it (and
+        # torch) run on, not a second copy
+        fn = lib().hipStreamGetCaptureInfo
+        fn.argtypes = [_P, ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_ulonglong)]
+        _HIP = fn
+    status, ident = _I(0), ctypes.c_ulonglong(0)
+    rc = _HIP(_stream(device), ctypes.byref(status), ctypes.byref(ident))
+    if rc != 0:
+        raise RuntimeError(f"hipStreamGetCaptureInfo failed ({rc})")
+    return int(ident.value) if status.value == 1 else 0
 
 
 def _dtype_code(t: torch.Tensor) -> int:
@@ -432,3 +463,58 @@ def tokenwise_linear(a, a_layout, as_, w, w_layout, ws, bias, n, k, epilogue, ou
         _ptr(a), a_layout, _ptr(as_), _ptr(w), w_layout, _ptr(ws), _ptr(bias), _bias_code(bias), _ptr(out),
         _dtype_code(out), m, n, k, epilogue, _ptr(workspace) if need else None, need, _stream(a.device)))
     return out
+
+
+def tokenwise_linear_multi(targets, w_layout, n, k, epilogue, scales, *, codes=None, a_layout=TW_ACT_A8, x=None,
+                           workspace=None):
+    """1 to MAX_TARGETS sibling projections on the same rows in one GEMM
+    launch (and one reduce when K is split): actune_tokenwise_linear_multi.
+    targets: [(w, ws, bias, out)] sharing n, k and w_layout, out [M, N]
+    preallocated; each bias may be None, those present share one dtype.
+    Pass either codes (in a_layout; scales [M] read) or x (rows [M, K]
+    quantized to A8 in the launch; scales [M] written).
+    workspace: u8 tensor of at least len(targets) x tokenwise_workspace_bytes()
+    bytes (None when that is 0). Each output equals the single-target call."""
+    if (codes is None) == (x is None):
+        raise ValueError("pass either codes or x")
+    if not 1 <= len(targets) <= MAX_TARGETS:
+        raise ValueError(f"1 to {MAX_TARGETS} targets")
+    act = codes if codes is not None else x
+    _require_cuda(act, scales, workspace, *[t for tgt in targets for t in tgt])
+    if x is not None:
+        a_layout = TW_ACT_A8
+        if x.dim() != 2 or not 1 <= x.shape[0] <= 8 or x.shape[1] != k or not x.is_contiguous():
+            raise RuntimeError("fused quantization takes contiguous x of shape [M, K] with M <= 8")
+        _dtype_code(x)
+    else:
+        abytes = k if a_layout == TW_ACT_A8 else k // 2
+        if codes.dim() != 2 or codes.shape[1] != abytes or codes.element_size() != 1 or not codes.is_contiguous():
+            raise RuntimeError("packed activation shape mismatch")
+    m = act.shape[0]
+    if scales.dtype != torch.float32 or scales.numel() != m or not scales.is_contiguous():
+        raise RuntimeError("scale shape mismatch")
+    wbytes = {TW_KMAJOR_W8: k * n, TW_KMAJOR_W4: k // 2 * n, TW_KMAJOR_W2: k // 4 * n,
+              TW_ROWS_S4: n * k // 2, TW_ROWS_S2: n * k // 4}[w_layout]
+    out_dtype = targets[0][3].dtype
+    present = [t[2] for t in targets if t[2] is not None]
+    bias0 = present[0] if present else None
+    structs = (_TwTarget * len(targets))()
+    for i, (w, ws, bias, out) in enumerate(targets):
+        if not (w.is_contiguous() and ws.is_contiguous() and (bias is None or bias.is_contiguous())):
+            raise RuntimeError("contiguous operands required")
+        if w.numel() != wbytes or w.element_size() != 1:
+            raise RuntimeError("packed weight shape mismatch")
+        if ws.dtype != torch.float32 or ws.numel() != n or (bias is not None and bias.numel() != n):
+            raise RuntimeError("scale shape mismatch")
+        if bias is not None and bias.dtype != bias0.dtype:
+            raise RuntimeError("the sibling biases present must share one dtype")
+        _check_buffer(out, "out", (m, n), out_dtype, act.device)
+        structs[i] = _TwTarget(w.data_ptr(), ws.data_ptr(), None if bias is None else bias.data_ptr(), out.data_ptr())
+    need = len(targets) * tokenwise_workspace_bytes(m, n, k, w_layout, a_layout)
+    if need and (workspace is None or workspace.numel() < need or workspace.dtype != torch.uint8):
+        raise RuntimeError(f"workspace of at least {need} bytes required")
+    _check(lib().actune_tokenwise_linear_multi(
+        _ptr(codes), a_layout, _ptr(x), _dtype_code(x) if x is not None else 0, _ptr(scales), w_layout, structs,
+        len(targets), _bias_code(bias0), _dtype_code(targets[0][3]), m, n, k, epilogue,
+        _ptr(workspace) if need else None, need, _stream(act.device)))
+    return [t[3] for t in targets]

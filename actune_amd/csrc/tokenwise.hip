@@ -111,6 +111,15 @@ constexpr int w_stride(int wl, int tn) {
 constexpr int a_row_bytes(int wl, int al) { return al == ACTUNE_TW_ACT_A4 ? 32 : (wl == ACTUNE_TW_KMAJOR_W2 ? 128 : 64); }
 constexpr int a_stride(int wl, int al) { return al == ACTUNE_TW_ACT_A4 ? 40 : a_row_bytes(wl, al) + 16; }
 
+// Per-target operands of a launch over sibling projections (same activation
+// rows, K, N and layouts); target 0 is also held in TwArgs' own fields.
+struct TwTarget {
+  const uint8_t* w;
+  const float* ws;
+  const void* bias;
+  void* out;
+};
+
 struct TwArgs {
   const uint8_t* a;     // int8 codes [M, K] or packed A4 [M, K/2]
   const void* x;        // activation rows [M, K] (fused quantization; a unused)
@@ -119,9 +128,25 @@ struct TwArgs {
   const float* ws;      // [N]
   const void* bias;     // [N] or nullptr
   void* out;            // [M, N]
-  int32_t* partial;     // [S, M, N] int32 raw (shifted) partial sums (S > 1)
+  int32_t* partial;     // [T, S, M, N] int32 raw (shifted) partial sums (S > 1)
   int M, N, K, bias_dt, out_dt, splits, steps;
+  int targets;          // T: grid z = S x T (GEMM), T (reduce)
+  TwTarget t[ACTUNE_MAX_TARGETS];
 };
+
+// The launch's arguments as seen by the workgroups of target `i`: its
+// weights, scales, bias and output, and its slice of the partial sums.
+__device__ __forceinline__ TwArgs for_target(const TwArgs& in, int i) {
+  TwArgs a = in;
+  if (i > 0) {
+    a.w = in.t[i].w;
+    a.ws = in.t[i].ws;
+    a.bias = in.t[i].bias;
+    a.out = in.t[i].out;
+    if (in.partial) a.partial = in.partial + (size_t)i * in.splits * in.M * in.N;
+  }
+  return a;
+}
 
 // y for output (m, n) from the true int32 accumulator, in the family's
 // fixed fp32 sequence, stored in out_dt.
@@ -220,7 +245,9 @@ constexpr int align_of_stride(int s) { return s % 16 == 0 ? 16 : (s % 8 == 0 ? 8
 // codes as the activation tile. The first workgroup writes the scales to
 // args.as (the integer reduce reads them).
 template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, int XDT = -1, int XR = 1>
-__global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
+__global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args_in) {
+  const int target = (int)blockIdx.z / args_in.splits;
+  const TwArgs args = for_target(args_in, target);
   using T = WTraits<WL>;
   constexpr int WN = 4 / WM;
   constexpr int TM = 16 * MT * WM, TN = 16 * NT * WN;
@@ -244,7 +271,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int n0 = (int)blockIdx.x * TN, m0 = (int)blockIdx.y * TM;
-  const int S = args.splits, z = (int)blockIdx.z;
+  const int S = args.splits, z = (int)blockIdx.z % S;
   const int g0 = (int)((long)z * args.steps / S), g1 = (int)((long)(z + 1) * args.steps / S);
 
   // buffer resources: reads past the end return zeros
@@ -463,7 +490,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
     if (tid < M) {
       const float sc = row_scale(tid);
       xsc[tid] = sc;
-      if (blockIdx.x == 0 && z == 0) const_cast<float*>(args.as)[tid] = sc;
+      if (blockIdx.x == 0 && blockIdx.z == 0) const_cast<float*>(args.as)[tid] = sc;
     }
     // the codes of rows 0 .. M-1 (rows past M are never stored; their
     // products are not written out)
@@ -561,7 +588,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args) {
     const float sc = fmaxf(amax, 1e-8f) * (1.0f / 127.0f);
     if (tid == 0) {
       xs[kThreads / 64] = sc;
-      if (blockIdx.x == 0 && z == 0) const_cast<float*>(args.as)[0] = sc;
+      if (blockIdx.x == 0 && blockIdx.z == 0) const_cast<float*>(args.as)[0] = sc;
     }
     // this thread's codes into row 0 of step fi's activation tile (out of
     // range steps hold x = 0: code 0; rows 1-15 are never stored)
@@ -635,7 +662,8 @@ __device__ __forceinline__ constexpr int lds_pos(int r, int b) {
 // registers held for them. A lane's global offsets are fixed; the K-step
 // advance is the scalar offset (out of range past the workgroup's K-range).
 template <int WL, int AL, int EPI, int WM, int MT, int NT, int KS, int D>
-__global__ __launch_bounds__(kThreads) void tw_gemm_ring(const TwArgs args) {
+__global__ __launch_bounds__(kThreads) void tw_gemm_ring(const TwArgs args_in) {
+  const TwArgs args = for_target(args_in, (int)blockIdx.z / args_in.splits);
   using T = WTraits<WL>;
   constexpr int WN = 4 / WM;
   constexpr int TM = 16 * MT * WM, TN = 16 * NT * WN;
@@ -652,7 +680,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm_ring(const TwArgs args) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int n0 = (int)blockIdx.x * TN, m0 = (int)blockIdx.y * TM;
-  const int z = (int)blockIdx.z;
+  const int z = (int)blockIdx.z % args.splits;
   const int g0 = (int)((long)z * args.steps / args.splits), g1 = (int)((long)(z + 1) * args.steps / args.splits);
 
   uint32_t wbytes;
@@ -908,15 +936,17 @@ __global__ __launch_bounds__(kThreads) void tw_gemm_ring(const TwArgs args) {
   finish_tile<WL, AL, EPI, MT, NT>(args, acc, m0 + wm * 16 * MT + 4 * kb, n0 + wn * 16 * NT + r16, z);
 }
 
-// Adds the K splits' partial sums and finishes the outputs: a thread takes
-// CPT consecutive columns (1 or 4) of row blockIdx.y (+ gridDim.y ...), with
+// Adds the K splits' partial sums and finishes the outputs of target
+// blockIdx.z: a thread takes CPT consecutive columns (1 or 4) of row
+// blockIdx.y (+ gridDim.y ...), with
 // all of up to NS splits' loads in flight at once (one round trip; more
 // splits loop by NS). The partials of split s sit at s * M * N + m * N + n.
 // With four columns and N a multiple of 4 (16-byte aligned quads) each split
 // is one 16-byte load, otherwise one 4-byte load per column; columns past N
 // are loaded as zeros and not stored.
 template <int EPI, int NS, int CPT>
-__global__ __launch_bounds__(kThreads) void tw_reduce(const TwArgs args, int shift) {
+__global__ __launch_bounds__(kThreads) void tw_reduce(const TwArgs args_in, int shift) {
+  const TwArgs args = for_target(args_in, (int)blockIdx.z);
   static_assert(CPT == 1 || CPT == 4, "one or four columns per thread");
   const int M = args.M, N = args.N, S = args.splits;
   const int n0 = CPT * ((int)blockIdx.x * kThreads + (int)threadIdx.x);
@@ -1095,7 +1125,8 @@ int pick_splits(int64_t M, int64_t N, int64_t K, int wl, const Geometry& g) {
 // made the linear 0.4-1.1 us slower than one column per thread.
 template <int EPI, int CPT>
 void launch_reduce_c(const TwArgs& a, int shift, hipStream_t st) {
-  const dim3 grid((unsigned)((a.N + CPT * kThreads - 1) / (CPT * kThreads)), (unsigned)std::min(a.M, 65535));
+  const dim3 grid((unsigned)((a.N + CPT * kThreads - 1) / (CPT * kThreads)), (unsigned)std::min(a.M, 65535),
+                  (unsigned)a.targets);
   if (a.splits <= 2) tw_reduce<EPI, 2, CPT><<<grid, kThreads, 0, st>>>(a, shift);
   else if (a.splits <= 4) tw_reduce<EPI, 4, CPT><<<grid, kThreads, 0, st>>>(a, shift);
   else if (a.splits <= 8) tw_reduce<EPI, 8, CPT><<<grid, kThreads, 0, st>>>(a, shift);
@@ -1113,7 +1144,8 @@ void launch_reduce(const TwArgs& a, int shift, hipStream_t st) {
 template <int WL, int AL, int EPI, int WM, int MT, int NT, int NB, int XDT = -1, int XR = 1>
 void launch_gemm_t(const TwArgs& a, hipStream_t st) {
   constexpr int TM = 16 * MT * WM, TN = 16 * NT * (4 / WM);
-  const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM), (unsigned)a.splits);
+  const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM),
+                  (unsigned)(a.splits * a.targets));
   tw_gemm<WL, AL, EPI, WM, MT, NT, NB, XDT, XR><<<grid, kThreads, 0, st>>>(a);
   if (a.splits > 1) launch_reduce<EPI>(a, WTraits<WL>::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0), st);
 }
@@ -1133,7 +1165,8 @@ void launch_ring_t(const TwArgs& a, hipStream_t st) {
   constexpr size_t lds = ring_lds_bytes<WL, AL, WM, MT, NT, KS, D>();
   static_assert(lds <= kStreamLdsMax, "ring exceeds the LDS budget");
   if constexpr (lds > 64 * 1024) allow_dynamic_lds<tw_gemm_ring<WL, AL, EPI, WM, MT, NT, KS, D>>();
-  const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM), (unsigned)a.splits);
+  const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM),
+                  (unsigned)(a.splits * a.targets));
   tw_gemm_ring<WL, AL, EPI, WM, MT, NT, KS, D><<<grid, kThreads, lds, st>>>(a);
   if (a.splits > 1) launch_reduce<EPI>(a, WTraits<WL>::TW + (AL == ACTUNE_TW_ACT_A4 ? 4 : 0), st);
 }
@@ -1299,12 +1332,27 @@ int prepare_linear(TwArgs& args, const void* act, int a_layout, const float* a_s
   args.out_dt = out_dtype;
   args.splits = S;
   args.steps = (int)steps_of(K, w_layout);
+  args.targets = 1;
   if (S > 1) {
     const int64_t need = (int64_t)S * M * N * 4;
     if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 16))
       return fail("workspace missing, misaligned or smaller than actune_tokenwise_workspace_bytes()");
     if (need >= ((int64_t)1 << 31)) return fail("split-K partials too large");
     args.partial = static_cast<int32_t*>(workspace);
+  }
+  return ACTUNE_OK;
+}
+
+// Checks of a launch that quantizes the rows x itself.
+int check_fused(int x_dtype, int w_layout, int64_t M, int64_t K) {
+  if (x_dtype != kBF16 && x_dtype != kF16 && x_dtype != kF32) return fail("unsupported activation dtype");
+  if (w_layout > ACTUNE_TW_KMAJOR_W2) return fail("fused quantization takes the K-major (A8) weight layouts");
+  if (M < 1 || M > kTwFusedMaxRows) return fail("fused quantization takes 1 to 8 rows");
+  if (M > 1 && x_dtype == kF32) return fail("fused quantization of more than one row takes bf16 or f16 x");
+  if (K > tw_fused_max_k(M)) {
+    snprintf(g_tw_msg, sizeof g_tw_msg, "fused quantization takes in_features <= %d at M = %d",
+             (int)tw_fused_max_k(M), (int)M);
+    return fail(g_tw_msg);
   }
   return ACTUNE_OK;
 }
@@ -1342,21 +1390,56 @@ int actune_tokenwise_linear_x(const void* x, int x_dtype, float* a_scales, const
                               int64_t M, int64_t N, int64_t K, int epilogue, void* workspace,
                               int64_t workspace_bytes, void* stream) {
   set_last_error("");
-  if (x_dtype != kBF16 && x_dtype != kF16 && x_dtype != kF32) return fail("unsupported activation dtype");
-  if (w_layout > ACTUNE_TW_KMAJOR_W2) return fail("fused quantization takes the K-major (A8) weight layouts");
-  if (M < 1 || M > kTwFusedMaxRows) return fail("fused quantization takes 1 to 8 rows");
-  if (M > 1 && x_dtype == kF32) return fail("fused quantization of more than one row takes bf16 or f16 x");
-  if (K > tw_fused_max_k(M)) {
-    char msg[96];
-    snprintf(msg, sizeof msg, "fused quantization takes in_features <= %d at M = %d", (int)tw_fused_max_k(M), (int)M);
-    return fail(msg);
-  }
-  TwArgs args;
-  const int rc = prepare_linear(args, x, ACTUNE_TW_ACT_A8, a_scales, w, w_layout, w_scale, bias, bias_dtype, out,
-                                out_dtype, M, N, K, epilogue, workspace, workspace_bytes);
+  const int rc = check_fused(x_dtype, w_layout, M, K);
   if (rc) return rc;
+  TwArgs args;
+  const int rc2 = prepare_linear(args, x, ACTUNE_TW_ACT_A8, a_scales, w, w_layout, w_scale, bias, bias_dtype, out,
+                                 out_dtype, M, N, K, epilogue, workspace, workspace_bytes);
+  if (rc2) return rc2;
   args.x = x;
   launch_fused(w_layout, epilogue, x_dtype, args, (hipStream_t)stream);
+  return launch_status();
+}
+
+int actune_tokenwise_linear_multi(const void* a, int a_layout, const void* x, int x_dtype, float* a_scales,
+                                  int w_layout, const actune_tw_target* targets, int ntargets, int bias_dtype,
+                                  int out_dtype, int64_t M, int64_t N, int64_t K, int epilogue, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  set_last_error("");
+  if ((a == nullptr) == (x == nullptr)) return fail("pass either activation codes or activation rows");
+  if (ntargets < 1 || ntargets > ACTUNE_MAX_TARGETS) return fail("1 to ACTUNE_MAX_TARGETS targets");
+  if (!targets) return fail("null pointer");
+  if (x) {
+    const int rc = check_fused(x_dtype, w_layout, M, K);
+    if (rc) return rc;
+    a_layout = ACTUNE_TW_ACT_A8;
+  }
+  // every target is checked as a single call would be; the splits and the
+  // per-target partial size do not depend on the target
+  const int64_t per = actune_tokenwise_workspace_bytes(M, N, K, w_layout, a_layout);
+  if (per < 0) return ACTUNE_ERR_INVALID;
+  TwArgs args;
+  for (int i = ntargets - 1; i >= 0; --i) {
+    const actune_tw_target& t = targets[i];
+    const int rc = prepare_linear(args, x ? x : a, a_layout, a_scales, t.w, w_layout, t.w_scale, t.bias, bias_dtype,
+                                  t.out, out_dtype, M, N, K, epilogue, per ? workspace : nullptr, per);
+    if (rc) return rc;
+  }
+  if (M == 0) return ACTUNE_OK;
+  if (per && (int64_t)ntargets * per > workspace_bytes)
+    return fail("workspace missing, misaligned or smaller than ntargets x actune_tokenwise_workspace_bytes()");
+  args.targets = ntargets;
+  for (int i = 0; i < ntargets; ++i)
+    args.t[i] = TwTarget{static_cast<const uint8_t*>(targets[i].w), targets[i].w_scale, targets[i].bias,
+                         targets[i].out};
+  hipStream_t st = (hipStream_t)stream;
+  if (x) {
+    args.x = x;
+    launch_fused(w_layout, epilogue, x_dtype, args, st);
+  } else {
+    args.a = static_cast<const uint8_t*>(a);
+    launch_gemm(w_layout, a_layout, epilogue, args, pick_geometry(M, N, w_layout), st);
+  }
   return launch_status();
 }
 

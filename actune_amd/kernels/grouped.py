@@ -27,10 +27,11 @@ CONFIG_AUTO = _native.CONFIG_AUTO
 
 
 class SharedActivationCache:
-    """Group-64 codes of the inputs seen in one scope, keyed by the source
-    tensor object, the activation width and the channel scale: linears that
-    read the same x at the same width (q/k/v, gate/up) then share one
-    quantizer launch, whatever their weight widths.
+    """Group-64 codes of the most recent input seen in one scope, keyed by
+    the source tensor object (and its version counter), the activation width
+    and the channel scale: linears that read the same x at the same width
+    one after another (q/k/v, gate/up) then share one quantizer launch,
+    whatever their weight widths.
 
     The scope also records, per call in order, which source it read (by
     order of first appearance), at which width and with which channel
@@ -93,17 +94,30 @@ def shared_activation_scope(*, enabled=True, plan=None):
         _SHARED_GROUP_STATE.reset(token)
 
 
+def _version(tensor):
+    """In-place writes bump a tensor's version counter (shared with its
+    views); inference tensors have none."""
+    return None if tensor.is_inference() else tensor._version
+
+
 def _shared_codes(state, source, flat, a, input_scale):
     """(packed, scales) of flat at width a from the scope's cache, quantizing
-    on a miss."""
-    for entry in state.entries:
-        src, shape, width, scale, packed, scales = entry
-        if src is source and shape == flat.shape and width == a and scale is input_scale:
+    on a miss. The cache holds the codes of ONE input (the most recent
+    source, one entry per width and channel scale): a call on another
+    tensor, on the same tensor after an in-place write, or under another
+    stream capture (or none) drops them, so codes never outlive the values
+    they were computed from, a captured launch never reads codes written
+    outside its graph, and at most one input's codes stay alive."""
+    stamp = (_version(source), _native.capture_id(flat.device))
+    if state.entries and (state.entries[0][0] is not source or state.entries[0][1] != stamp):
+        state.entries.clear()
+    for _, _, shape, width, scale, packed, scales in state.entries:
+        if shape == flat.shape and width == a and scale is input_scale:
             state.hits += 1
             return packed, scales
     packed, scales = _native.quantize_groups(flat, a, input_scale)
     state.misses += 1
-    state.entries.append((source, flat.shape, a, input_scale, packed, scales))
+    state.entries.append((source, stamp, flat.shape, a, input_scale, packed, scales))
     return packed, scales
 
 
@@ -137,7 +151,11 @@ class GroupedLinear(torch.nn.Module):
             raise ValueError("Grouped backend requires K divisible by 64")
         if w not in (2, 4, 8) or a not in (2, 4, 8):
             raise ValueError("Unsupported integer width")
-        codes, scale = weight_codes(linear.weight, w, a, clip_ratios=ratios)
+        # codes as torch computes them where the layer lives (grouped.py:120
+        # runs weight_codes on linear.weight's device): a CUDA layer divides
+        # by 7 and 127 through their fp32 reciprocals, a CPU layer exactly
+        codes, scale = weight_codes(linear.weight, w, a, clip_ratios=ratios,
+                                    gpu_division=linear.weight.is_cuda)
         self.register_buffer("packed_weight", pack_rows(codes, w))
         self.register_buffer("weight_scale", scale.contiguous())
         bias = None

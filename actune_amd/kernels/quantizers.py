@@ -5,11 +5,14 @@ scale amax*r, signed W4 {-8..7} with scale amax*r/7, the nested W8 code
 16*q4 + r4 used with A4 activations (scale s4/16), and plain W8 with scale
 amax/127 (clip ratios ignored). amax is clamped to >= 1e-8.
 
-Arithmetic is done in fp32 on the CPU, so every division is the IEEE
-quotient (torch-CPU divides exactly; a GPU tensor/scalar division would
-multiply by a rounded reciprocal instead). The resulting codes and scales are
-returned on the weight's device. This runs once per (layer, mode) at install
-time; the per-call path is the HIP library.
+Arithmetic is done in fp32 on the CPU. Every tensor/tensor division is the
+IEEE quotient on either device; the divisions by the constants 7 and 127 are
+the IEEE quotient by default and, with ``gpu_division``, a multiply by the
+fp32 reciprocal, which is what torch computes for a GPU tensor divided by a
+Python scalar. Callers pass ``gpu_division=weight.is_cuda`` to get the codes
+the reference computes on the layer's own device. The resulting codes and
+scales are returned on the weight's device. This runs once per (layer, mode)
+at install time; the per-call path is the HIP library.
 """
 from __future__ import annotations
 
@@ -93,9 +96,9 @@ def symmetric_int2_quantize(weight, *, clip_ratios=None):
 def weight_codes(weight, w, a, *, clip_ratios=None, gpu_division=False):
     """(int8 codes [N, K], fp32 scale [N]) for weight width w used with
     activation width a (quantizers.py:83-94). gpu_division: divide by the
-    constants 7 and 127 as torch does on a GPU (see _div_const); the
-    group-64 backend keeps the IEEE quotient, the tokenwise modules follow
-    the device of the layer they are built from."""
+    constants 7 and 127 as torch does on a GPU (see _div_const); every
+    module (group-64 and tokenwise) passes the device of the layer it is
+    built from, as the reference evaluates these formulas there."""
     if w == 2:
         return symmetric_int2_quantize(weight, clip_ratios=clip_ratios)
     if w == 4:

@@ -13,10 +13,18 @@ One module for the reference's tokenwise family, with its public names:
   ``DecodeStats``, ``decode_eligible``, ``decode_linear``, ``launch_decode``,
   ``launch_decode_group``, ``DecodeGraphPlan``, ``graph_decode_linear``,
   ``graph_plan_key``, ``decode_workspace_summary``
-  (decode_w4a8_triton.py:113-480);
+  (decode_w4a8_triton.py:113-480); sibling projections run as one GEMM
+  launch plus one integer reduce (actune_tokenwise_linear_multi);
 * ``runtime_optimization_scope`` / ``RuntimeStats`` / ``runtime_stats_dict``
   (runtime_options.py) and ``resident_a8_eligible`` / ``launch_resident_a8``
   (resident_a8_triton.py).
+
+The request-scoped switches and counters live in two context variables of
+this module (one immutable set of switches, one pair of counter objects),
+read through ``decode_enabled()``, ``dense_candidates_enabled()`` and
+``current_shared_a8_cache()``. Split-K partial sums get a fresh workspace
+per call from the caching allocator (stream-ordered, and from the graph's
+private pool under capture).
 
 Buffers keep the reference's names, layouts, dtypes and byte counts
 (``packed_weight`` K-major nibble pairs [K/2, N] for W4A8, ``weight_int8``
@@ -34,35 +42,168 @@ the grid would otherwise be too small, so results never depend on the split.
 from __future__ import annotations
 
 import threading
+from collections import OrderedDict
 from contextlib import contextmanager
 from contextvars import ContextVar
-from dataclasses import asdict, dataclass, field
-from typing import Any, Iterator
+from dataclasses import asdict, dataclass
+from typing import Iterator, NamedTuple
 
 import torch
 
 from .. import _native
 from . import quantizers
 
-# ---------------------------------------------------------------- workspaces
+# ---------------------------------------------------------------- request-scoped state
+@dataclass(frozen=True)
+class _Switches:
+    """The request's tokenwise switches: ``runtime`` and ``dense`` belong to
+    runtime_optimization_scope, ``decode`` to decode_optimization_scope.
+    Replaced as a whole by each scope, so nested scopes restore cleanly."""
+
+    runtime: bool = True
+    dense: bool = False
+    decode: bool = True
 
 
-def _workspace(owner, m, n, k, w_layout, a_layout, device):
-    """The owner's split-K partial-sum workspace, grown when a call needs
-    more; None when the call runs unsplit."""
+_SWITCHES: ContextVar[_Switches] = ContextVar("actune_tokenwise_switches", default=_Switches())
+# (RuntimeStats or None, DecodeStats or None) of the innermost scopes
+_COUNTERS: ContextVar[tuple] = ContextVar("actune_tokenwise_counters", default=(None, None))
+
+
+@contextmanager
+def _scoped(switches=None, runtime_stats=..., decode_stats=...):
+    """Install new switches and / or counters for the body of a with-block."""
+    old_rt, old_dec = _COUNTERS.get()
+    counters = (old_rt if runtime_stats is ... else runtime_stats, old_dec if decode_stats is ... else decode_stats)
+    tokens = [_COUNTERS.set(counters)]
+    if switches is not None:
+        tokens.append(_SWITCHES.set(switches))
+    try:
+        yield
+    finally:
+        for token in reversed(tokens):
+            token.var.reset(token)
+
+
+def _count(kind, **increments):
+    """Add to the innermost scope's RuntimeStats (kind 0) or DecodeStats
+    (kind 1), if a scope is open."""
+    stats = _COUNTERS.get()[kind]
+    if stats is not None:
+        for name, value in increments.items():
+            setattr(stats, name, getattr(stats, name) + value)
+
+
+def decode_enabled() -> bool:
+    """The decode switch of the innermost decode_optimization_scope (True
+    outside any scope)."""
+    return _SWITCHES.get().decode
+
+
+def dense_candidates_enabled() -> bool:
+    """The dense_candidates switch of the innermost runtime scope."""
+    return _SWITCHES.get().dense
+
+
+@dataclass
+class RuntimeStats:
+    """Counters of runtime_optimization_scope (runtime_options.py:13-17).
+    resident_a8_kernels counts the dense-candidate row quantizations; this
+    backend has no MLP graph controller and no pre-decoded R4 GEMM, so the
+    other two stay 0 (the fields are kept for readers of the reference's
+    dict)."""
+
+    resident_a8_kernels: int = 0
+    mlp_graph_replays: int = 0
+    predecoded_r4_gemms: int = 0
+
+
+@contextmanager
+def runtime_optimization_scope(*, enabled=True, dense_candidates=None):
+    """Request-local runtime switches with fresh counters; dense_candidates
+    None keeps the enclosing setting (runtime_options.py:20-35)."""
+    now = _SWITCHES.get()
+    switches = _Switches(runtime=enabled, dense=now.dense if dense_candidates is None else bool(dense_candidates),
+                         decode=now.decode)
+    stats = RuntimeStats()
+    with _scoped(switches, runtime_stats=stats):
+        yield stats
+
+
+def runtime_stats_dict(state):
+    return asdict(state)
+
+
+@dataclass
+class DecodeStats:
+    """Counters of one decode_optimization_scope (decode_w4a8_triton.py:242-257):
+    every split decode linear (split_k_calls), every sibling group launched
+    together (projection_groups, with its projections in
+    projection_calls_fused), the split GEMM / integer reduce launches, the
+    row quantizations on the decode path and the graph replays."""
+
+    split_k_calls: int = 0
+    projection_groups: int = 0
+    projection_calls_fused: int = 0
+    partial_kernels: int = 0
+    reduction_kernels: int = 0
+    resident_quantization_kernels: int = 0
+    graph_replays: int = 0
+    graph_quantization_kernels: int = 0
+
+    def metrics(self) -> dict:
+        return asdict(self)
+
+
+@contextmanager
+def decode_optimization_scope(*, enabled: bool = True):
+    """Decode switch and fresh counters for one model forward."""
+    now = _SWITCHES.get()
+    stats = DecodeStats()
+    with _scoped(_Switches(runtime=now.runtime, dense=now.dense, decode=enabled), decode_stats=stats):
+        yield stats
+
+
+def decode_eligible(value: torch.Tensor, *, k: int, n: int | None = None) -> bool:
+    """Single-token bf16 calls take the split-K decode path. The reference
+    restricts it to its measured shapes on one GPU generation
+    (decode_w4a8_triton.py:297-309); here every shape the kernel takes
+    qualifies (the split is chosen per shape)."""
+    return (decode_enabled() and value.is_cuda and value.dtype == torch.bfloat16 and value.numel() == k
+            and value.shape[-1] == k and value.is_contiguous() and k % 64 == 0
+            and (n is None or n % 16 == 0))
+
+
+def resident_a8_eligible(value):
+    """Opt-in dense candidate (resident_a8_triton.py:24-34): any contiguous
+    bf16 activation on the GPU while every switch allows it."""
+    sw = _SWITCHES.get()
+    return (sw.dense and sw.runtime and sw.decode and value.is_cuda and value.dtype == torch.bfloat16
+            and value.dim() == 2 and value.is_contiguous())
+
+
+def launch_resident_a8(value, activation, scale):
+    """Per-row A8 quantization into caller-owned buffers (resident_a8_triton.py:37-42)."""
+    _native.tokenwise_quantize(value, 8, activation, scale)
+    _count(0, resident_a8_kernels=1)
+
+
+# ---------------------------------------------------------------- split-K workspace and packing
+def _split_workspace(m, n, k, w_layout, a_layout, device, targets=1):
+    """A fresh workspace for one call's K-split partial sums (None when the
+    call runs unsplit). Allocated per call from the caching allocator on the
+    current stream: stream-ordered, and taken from the graph's private pool
+    while a capture is recording, so no captured launch ever points at a
+    buffer a later call could replace."""
     need = _native.tokenwise_workspace_bytes(m, n, k, w_layout, a_layout)
     if need == 0:
         return None
-    ws = getattr(owner, "_tw_workspace", None)
-    if ws is None or ws.numel() < need or ws.device != device:
-        ws = torch.empty(need, dtype=torch.uint8, device=device)
-        owner._tw_workspace = ws
-    return ws
+    return torch.empty(need * targets, dtype=torch.uint8, device=device)
 
 
-def _gemm(owner, activation, a_layout, scale, weight, w_layout, weight_scale, bias, n, k, epilogue, dtype):
+def _gemm(activation, a_layout, scale, weight, w_layout, weight_scale, bias, n, k, epilogue, dtype):
     out = torch.empty((activation.shape[0], n), device=activation.device, dtype=dtype)
-    ws = _workspace(owner, activation.shape[0], n, k, w_layout, a_layout, activation.device)
+    ws = _split_workspace(activation.shape[0], n, k, w_layout, a_layout, activation.device)
     return _native.tokenwise_linear(activation, a_layout, scale, weight, w_layout, weight_scale, bias, n, k,
                                     epilogue, out, workspace=ws)
 
@@ -98,134 +239,38 @@ def _require_cuda(value, what):
         raise ValueError(f"{what} requires a CUDA input")
 
 
+_KMAJOR_WIDTH_MSG = "K-major tokenwise weights need out_features divisible by 16 on this backend"
+
+
 def _kmajor_width_ok(out_features):
     if out_features % 16:
-        raise ValueError("K-major tokenwise weights need out_features divisible by 16 on this backend")
+        raise ValueError(_KMAJOR_WIDTH_MSG)
 
 
-# ---------------------------------------------------------------- runtime options
-_RUNTIME_ENABLED: ContextVar[bool] = ContextVar("vla_runtime_optimization_enabled", default=True)
-_DENSE_CANDIDATES: ContextVar[bool] = ContextVar("vla_dense_runtime_candidates", default=False)
-_RUNTIME_STATE: ContextVar[Any] = ContextVar("vla_runtime_optimization_stats", default=None)
+# ---------------------------------------------------------------- shared per-row codes
+class _Codes(NamedTuple):
+    """Per-row codes of one input tensor at one width: what a later sibling
+    on the same tensor may reuse while the tensor is unchanged and while the
+    same stream capture (or none) is recording."""
+
+    source: torch.Tensor
+    version: int | None
+    capture: int
+    in_features: int
+    codes: torch.Tensor
+    scale: torch.Tensor
 
 
-@dataclass
-class RuntimeStats:
-    resident_a8_kernels: int = 0
-    mlp_graph_replays: int = 0
-    predecoded_r4_gemms: int = 0
-
-
-@contextmanager
-def runtime_optimization_scope(*, enabled=True, dense_candidates=None):
-    """Request-local runtime switches and counters (runtime_options.py:20-35)."""
-    dense_token = None if dense_candidates is None else _DENSE_CANDIDATES.set(dense_candidates)
-    state = RuntimeStats()
-    switch = _RUNTIME_ENABLED.set(enabled)
-    token = _RUNTIME_STATE.set(state)
-    try:
-        yield state
-    finally:
-        _RUNTIME_STATE.reset(token)
-        _RUNTIME_ENABLED.reset(switch)
-        if dense_token is not None:
-            _DENSE_CANDIDATES.reset(dense_token)
-
-
-def runtime_stats_dict(state):
-    return asdict(state)
-
-
-# ---------------------------------------------------------------- decode switches and counters
-_DECODE_ENABLED: ContextVar[bool] = ContextVar("vla_decode_optimization_enabled", default=True)
-
-
-@dataclass
-class DecodeStats:
-    split_k_calls: int = 0
-    projection_groups: int = 0
-    projection_calls_fused: int = 0
-    partial_kernels: int = 0
-    reduction_kernels: int = 0
-    resident_quantization_kernels: int = 0
-    graph_replays: int = 0
-    graph_quantization_kernels: int = 0
-    pending: dict = field(default_factory=dict, repr=False)
-
-    def metrics(self) -> dict:
-        return {name: getattr(self, name) for name in (
-            "split_k_calls", "projection_groups", "projection_calls_fused", "partial_kernels",
-            "reduction_kernels", "resident_quantization_kernels", "graph_replays", "graph_quantization_kernels")}
-
-
-_DECODE_STATE: ContextVar[DecodeStats | None] = ContextVar("vla_decode_state", default=None)
-
-
-@contextmanager
-def decode_optimization_scope(*, enabled: bool = True):
-    """Bound decode fusion results and counters to one model forward
-    (decode_w4a8_triton.py:278-289)."""
-    state = DecodeStats()
-    switch = _DECODE_ENABLED.set(enabled)
-    token = _DECODE_STATE.set(state)
-    try:
-        yield state
-    finally:
-        state.pending.clear()
-        _DECODE_STATE.reset(token)
-        _DECODE_ENABLED.reset(switch)
-
-
-def decode_eligible(value: torch.Tensor, *, k: int, n: int | None = None) -> bool:
-    """Single-token bf16 calls take the split-K decode path. The reference
-    restricts it to its measured shapes on one GPU generation
-    (decode_w4a8_triton.py:297-309); here every shape the kernel takes
-    qualifies (the split is chosen per shape)."""
-    return (_DECODE_ENABLED.get() and value.is_cuda and value.dtype == torch.bfloat16 and value.numel() == k
-            and value.shape[-1] == k and value.is_contiguous() and k % 64 == 0
-            and (n is None or n % 16 == 0))
-
-
-def resident_a8_eligible(value):
-    """Opt-in dense candidate (resident_a8_triton.py:24-34): any contiguous
-    bf16 activation on the GPU while the runtime switches allow it."""
-    return (_DENSE_CANDIDATES.get() and _RUNTIME_ENABLED.get() and _DECODE_ENABLED.get() and value.is_cuda
-            and value.dtype == torch.bfloat16 and value.dim() == 2 and value.is_contiguous())
-
-
-def launch_resident_a8(value, activation, scale):
-    """Per-row A8 quantization into caller-owned buffers (resident_a8_triton.py:37-42)."""
-    _native.tokenwise_quantize(value, 8, activation, scale)
-    state = _RUNTIME_STATE.get()
-    if state is not None:
-        state.resident_a8_kernels += 1
-
-
-# ---------------------------------------------------------------- shared dynamic-A8 cache
-class _SharedA8Entry:
-    """One task-local dynamic-A8 result shared by sibling projections."""
-
-    __slots__ = ("source", "in_features", "activation", "scale")
-
-    def __init__(self, source, in_features, activation, scale):
-        self.source = source
-        self.in_features = in_features
-        self.activation = activation
-        self.scale = scale
-
-
-class _A4Entry:
-    __slots__ = ("source", "in_features", "packed", "scale")
-
-    def __init__(self, source, in_features, packed, scale):
-        self.source = source
-        self.in_features = in_features
-        self.packed = packed
-        self.scale = scale
+def _version_of(tensor):
+    return None if tensor.is_inference() else tensor._version
 
 
 class SharedA8CacheStats:
-    """Mutable statistics and one-entry workspace for a policy forward."""
+    """One forward's sibling-projection cache (w4a8_triton.py:227-237 names
+    its fields): at most one input's per-row A8 codes and one input's A4
+    codes (``entry`` / ``a4_entry``), reused by the next linears that read
+    the very same tensor, unmodified, at the same K; ``hits`` / ``misses``
+    count the A8 lookups."""
 
     __slots__ = ("enabled", "entry", "a4_entry", "hits", "misses")
 
@@ -236,74 +281,86 @@ class SharedA8CacheStats:
         self.hits = 0
         self.misses = 0
 
+    def lookup(self, slot, source, flat, in_features):
+        held = getattr(self, slot)
+        if (not self.enabled or held is None or held.source is not source or held.in_features != in_features
+                or held.version != _version_of(source) or held.codes.shape[0] != flat.shape[0]
+                or held.capture != _native.capture_id(flat.device)):
+            return None
+        return held
 
-_SHARED_A8_STATE: ContextVar[SharedA8CacheStats | None] = ContextVar("vla_shared_dynamic_a8_state", default=None)
+    def keep(self, slot, source, in_features, codes, scale):
+        entry = _Codes(source, _version_of(source), _native.capture_id(codes.device), in_features, codes, scale)
+        setattr(self, slot, entry if self.enabled else None)
+
+
+_SHARED_A8: ContextVar[SharedA8CacheStats | None] = ContextVar("actune_tokenwise_shared_codes", default=None)
+
+
+def current_shared_a8_cache():
+    """The cache of the innermost shared_a8_cache_scope (None outside any)."""
+    return _SHARED_A8.get()
 
 
 def clear_shared_a8_cache() -> None:
-    """Drop the task-local sibling-projection activation cache."""
-    state = _SHARED_A8_STATE.get()
+    """Forget the codes held for sibling projections (a cache is opened for
+    the current context if none is)."""
+    state = _SHARED_A8.get()
     if state is None:
-        _SHARED_A8_STATE.set(SharedA8CacheStats())
-    else:
-        state.entry = None
-        state.a4_entry = None
+        _SHARED_A8.set(SharedA8CacheStats())
+        return
+    state.entry = state.a4_entry = None
 
 
 @contextmanager
 def shared_a8_cache_scope(*, enabled: bool = True) -> Iterator[SharedA8CacheStats]:
-    """Bound cache lifetime to one policy forward and release its workspace."""
+    """A fresh cache for the body (one model forward); its codes are dropped
+    on exit."""
     state = SharedA8CacheStats(enabled=enabled)
-    token = _SHARED_A8_STATE.set(state)
+    token = _SHARED_A8.set(state)
     try:
         yield state
     finally:
-        _SHARED_A8_STATE.reset(token)
+        _SHARED_A8.reset(token)
 
 
 def _quantize_rows_shared(source, flat, *, in_features):
-    """Quantize once and reuse for adjacent linears on the same tensor
-    (w4a8_triton.py:270-325): per-row A8 depends only on the input and K,
-    so q/k/v (or gate/up) share one quantizer launch whatever their weights."""
+    """Per-row A8 codes of flat, reused from the cache when the previous
+    quantization was of the same, unmodified source tensor: the codes depend
+    only on the input and K, so q/k/v (or gate/up) share one quantizer launch
+    whatever their weights (w4a8_triton.py:270-325)."""
     if not source.is_cuda or flat.shape[-1] != in_features:
         raise ValueError("shared A8 quantization requires a CUDA input with matching K")
-    state = _SHARED_A8_STATE.get()
+    state = _SHARED_A8.get()
     if state is None:
-        state = SharedA8CacheStats()
-        _SHARED_A8_STATE.set(state)
-    entry = state.entry
-    if (state.enabled and entry is not None and entry.source is source and entry.in_features == in_features
-            and entry.activation.shape == flat.shape):
+        clear_shared_a8_cache()
+        state = _SHARED_A8.get()
+    held = state.lookup("entry", source, flat, in_features)
+    if held is not None:
         state.hits += 1
-        return entry.activation, entry.scale
-    flat = flat.contiguous()
-    activation, scale = _native.tokenwise_quantize(flat, 8)
+        return held.codes, held.scale
+    codes, scale = _native.tokenwise_quantize(flat.contiguous(), 8)
     if resident_a8_eligible(flat):
-        rstate = _RUNTIME_STATE.get()
-        if rstate is not None:
-            rstate.resident_a8_kernels += 1
+        _count(0, resident_a8_kernels=1)
     elif decode_eligible(flat, k=in_features):
-        dstate = _DECODE_STATE.get()
-        if dstate is not None:
-            dstate.resident_quantization_kernels += 1
+        _count(1, resident_quantization_kernels=1)
     state.misses += 1
-    state.entry = _SharedA8Entry(source, in_features, activation, scale) if state.enabled else None
-    return activation, scale
+    state.keep("entry", source, in_features, codes, scale)
+    return codes, scale
 
 
 def _quantize_a4_shared(source, flat, *, in_features):
-    """Per-row A4 codes (wxa4_native.py:123-160), reused inside an enabled
-    shared-cache scope for the same source tensor."""
+    """Per-row A4 codes (wxa4_native.py:123-160), reused inside a scope for
+    the same unmodified source tensor."""
     if not source.is_cuda or flat.shape[-1] != in_features:
         raise ValueError("native A4 quantization requires a CUDA input with matching K")
-    state = _SHARED_A8_STATE.get()
-    entry = None if state is None else state.a4_entry
-    if (entry is not None and entry.source is source and entry.in_features == in_features
-            and entry.packed.shape[0] == flat.shape[0]):
-        return entry.packed, entry.scale
+    state = _SHARED_A8.get()
+    held = None if state is None else state.lookup("a4_entry", source, flat, in_features)
+    if held is not None:
+        return held.codes, held.scale
     packed, scale = _native.tokenwise_quantize(flat.contiguous(), 4)
-    if state is not None and state.enabled:
-        state.a4_entry = _A4Entry(source, in_features, packed, scale)
+    if state is not None:
+        state.keep("a4_entry", source, in_features, packed, scale)
     return packed, scale
 
 
@@ -325,7 +382,7 @@ class _TokenwiseA8(torch.nn.Module):
         fewer than the quantizer + GEMM pair, with the same codes and
         outputs. Inside an enabled scope the siblings share one quantizer
         launch instead."""
-        state = _SHARED_A8_STATE.get()
+        state = _SHARED_A8.get()
         m = flat.shape[0]
         return (self.fused_quantization and 2 <= m <= 8 and flat.dtype in (torch.bfloat16, torch.float16)
                 and self.in_features <= _native.tokenwise_fused_max_k(m)
@@ -335,26 +392,21 @@ class _TokenwiseA8(torch.nn.Module):
         _require_cuda(value, type(self).__name__)
         original_shape = value.shape[:-1]
         flat = value.reshape(-1, self.in_features)
+        m = flat.shape[0]
+        weight = getattr(self, self._weight_name)
         if self._fuses_rows(flat):
-            m = flat.shape[0]
             out = torch.empty((m, self.out_features), device=flat.device, dtype=value.dtype)
             scale = torch.empty(m, device=flat.device, dtype=torch.float32)
-            ws = _workspace(self, m, self.out_features, self.in_features, self._layout, _native.TW_ACT_A8,
-                            flat.device)
-            _native.tokenwise_linear_x(flat.contiguous(), scale, getattr(self, self._weight_name), self._layout,
-                                       self.weight_scale, self.bias, self.out_features, self.in_features,
-                                       _native.TW_EPI_A8, out, workspace=ws)
+            ws = _split_workspace(m, self.out_features, self.in_features, self._layout, _native.TW_ACT_A8,
+                                  flat.device)
+            _native.tokenwise_linear_x(flat.contiguous(), scale, weight, self._layout, self.weight_scale, self.bias,
+                                       self.out_features, self.in_features, _native.TW_EPI_A8, out, workspace=ws)
             return out.reshape(*original_shape, self.out_features)
         activation, scale = self._quantize(flat, source=value)
         if self._layout == _native.TW_KMAJOR_W4 and decode_eligible(flat, k=self.in_features, n=self.out_features):
-            state = _DECODE_STATE.get()
-            if state is not None:
-                state.split_k_calls += 1
-                state.partial_kernels += 1
-                state.reduction_kernels += 1
-        output = _gemm(self, activation, _native.TW_ACT_A8, scale, getattr(self, self._weight_name), self._layout,
-                       self.weight_scale, self.bias, self.out_features, self.in_features, _native.TW_EPI_A8,
-                       value.dtype)
+            _count_split_decode(1, self.out_features, self.in_features)
+        output = _gemm(activation, _native.TW_ACT_A8, scale, weight, self._layout, self.weight_scale, self.bias,
+                       self.out_features, self.in_features, _native.TW_EPI_A8, value.dtype)
         return output.reshape(*original_shape, self.out_features)
 
 
@@ -446,15 +498,24 @@ class W2A8TritonLinear(_TokenwiseA8):
         return self._linear(value)
 
 
-def _replace(module, filter_fn, factory):
-    replaced = 0
+def _selected(module, filter_fn):
+    """(parent, attribute, child) for every child the filter selects, in the
+    reference's walk order: a selected child is not descended into."""
     for name, child in list(module.named_children()):
         if filter_fn(child, name):
-            setattr(module, name, factory(child))
-            replaced += 1
+            yield module, name, child
         else:
-            replaced += _replace(child, filter_fn, factory)
-    return replaced
+            yield from _selected(child, filter_fn)
+
+
+def _replace(module, filter_fn, factory):
+    """Build the replacement of every selected child first, then swap them
+    in: a layer this backend cannot take (its constructor raises) leaves the
+    model untouched instead of half replaced."""
+    built = [(parent, name, factory(child)) for parent, name, child in _selected(module, filter_fn)]
+    for parent, name, replacement in built:
+        setattr(parent, name, replacement)
+    return len(built)
 
 
 def replace_with_w4a8_triton_(module, filter_fn) -> int:
@@ -510,7 +571,7 @@ class _WxA4NativeLinear(torch.nn.Module):
         flat = value.reshape(-1, self.in_features)
         packed, activation_scale = _quantize_a4_shared(value, flat, in_features=self.in_features)
         layout = _native.TW_ROWS_S4 if self.weight_bits == 4 else _native.TW_ROWS_S2
-        output = _gemm(self, packed, _native.TW_ACT_A4, activation_scale, self.packed_weight, layout,
+        output = _gemm(packed, _native.TW_ACT_A4, activation_scale, self.packed_weight, layout,
                        self.weight_scale, self.bias if self.bias.numel() else None, self.out_features,
                        self.in_features, _native.TW_EPI_A4, value.dtype)
         return output.reshape(*original_shape, self.out_features)
@@ -561,217 +622,199 @@ class W8A4NativeLinear(torch.nn.Module):
         original_shape = value.shape[:-1]
         flat = value.reshape(-1, self.in_features)
         packed, activation_scale = _quantize_a4_shared(value, flat, in_features=self.in_features)
-        output = _gemm(self, packed, _native.TW_ACT_A4, activation_scale, self.weight_int8, _native.TW_KMAJOR_W8,
+        output = _gemm(packed, _native.TW_ACT_A4, activation_scale, self.weight_int8, _native.TW_KMAJOR_W8,
                        self.weight_scale, self.bias if self.bias.numel() else None, self.out_features,
                        self.in_features, _native.TW_EPI_A8, value.dtype)
         return output.reshape(*original_shape, self.out_features)
 
 
 # ---------------------------------------------------------------- exact split-K decode
-# longest row the GEMM launch quantizes itself (actune_tokenwise_linear_x)
+# longest row a GEMM launch quantizes itself (actune_tokenwise_linear_x, one row)
 _FUSED_MAX_K = 16384
+# decode graph plans a module keeps (least recently used dropped first)
+_PLANS_PER_MODULE = 4
 
 
-class _WorkspaceOwner:
-    pass
-
-
-_LAUNCH_OWNER = _WorkspaceOwner()
-
-
-def _decode_check_residual(residual):
-    if residual is not None:
+def _no_residual(residuals):
+    if any(r is not None for r in residuals):
         raise NotImplementedError("the signed-R4 residual decode layout is not part of this backend")
+
+
+def _w4_shape(packed):
+    """(N, K) of K-major nibble-pair weights [K/2, N]."""
+    return packed.shape[1], packed.shape[0] * 2
+
+
+def _count_split_decode(groups, n, k):
+    """DecodeStats of one decode of `groups` sibling projections on one row:
+    the GEMM launch (a partial kernel) and, when the library splits K for
+    this shape, the integer reduce."""
+    split = _native.tokenwise_workspace_bytes(1, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8) > 0
+    kind = dict(split_k_calls=1) if groups == 1 else dict(projection_groups=1, projection_calls_fused=groups)
+    _count(1, partial_kernels=1, reduction_kernels=int(split), **kind)
+
+
+def _caller_workspace(partial, need):
+    """The caller's partial-sum buffer as bytes (any dtype; its contents do
+    not matter), or None when the call runs unsplit."""
+    if not need:
+        return None
+    raw = partial.reshape(-1).view(torch.uint8)
+    if raw.numel() < need:
+        raise ValueError(f"partial workspace too small: {need} bytes needed")
+    return raw
+
+
+def launch_decode_group(activation, weights, residuals, activation_scale, scales, biases, outputs, partial, *,
+                        splits=None, bn=None):
+    """Decode of 1 to 4 sibling projections (K-major W4 weights) sharing one
+    quantized row, into caller-owned buffers: ONE GEMM launch over every
+    projection's column tiles and K splits, then one integer reduce for all
+    of them (decode_w4a8_triton.py:150-239 launches the same pair).
+    ``splits`` and ``bn`` are accepted for call compatibility: the library
+    sizes the split per shape, and results do not depend on it. ``partial``:
+    at least len(weights) x actune_tokenwise_workspace_bytes() bytes."""
+    _no_residual(residuals)
+    n, k = _w4_shape(weights[0])
+    m = activation.numel() // k
+    need = len(weights) * _native.tokenwise_workspace_bytes(m, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8)
+    targets = [(w, s, b, o.view(m, n)) for w, s, b, o in zip(weights, scales, biases, outputs)]
+    return _native.tokenwise_linear_multi(targets, _native.TW_KMAJOR_W4, n, k, _native.TW_EPI_A8,
+                                          activation_scale.reshape(-1), codes=activation.reshape(m, k),
+                                          workspace=_caller_workspace(partial, need))
 
 
 def launch_decode(activation, packed, residual, activation_scale, weight_scale, bias, output, partial, *,
                   config=None):
-    """Launch into caller-owned buffers (decode_w4a8_triton.py:113-149).
-    ``partial`` is the caller's split-K workspace (any dtype, at least the
-    bytes actune_tokenwise_workspace_bytes() asks for; nothing in it needs
-    to start at any value). ``config`` is accepted for signature parity; the
-    split is chosen per shape."""
-    _decode_check_residual(residual)
-    n = packed.shape[1]
-    k = packed.shape[0] * 2
-    m = activation.numel() // k
-    need = _native.tokenwise_workspace_bytes(m, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8)
-    ws = None
-    if need:
-        ws = partial.view(-1).view(torch.uint8)
-        if ws.numel() < need:
-            raise ValueError(f"partial workspace too small: {need} bytes needed")
-    return _native.tokenwise_linear(activation.reshape(m, k), _native.TW_ACT_A8, activation_scale.reshape(-1),
-                                    packed, _native.TW_KMAJOR_W4, weight_scale, bias, n, k, _native.TW_EPI_A8,
-                                    output.view(m, n), workspace=ws)
-
-
-def launch_decode_group(activation, weights, residuals, activation_scale, scales, biases, outputs, partial, *,
-                        splits=16, bn=128):
-    """Two or three projections sharing one quantized activation
-    (decode_w4a8_triton.py:205-239): one split-K launch per projection
-    on the shared codes."""
-    for r in residuals:
-        _decode_check_residual(r)
-    n = weights[0].shape[1]
-    k = weights[0].shape[0] * 2
-    ws = partial.view(-1).view(torch.uint8)
-    need = _native.tokenwise_workspace_bytes(1, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8)
-    if need and ws.numel() < need:
-        raise ValueError(f"partial workspace too small: {need} bytes needed")
-    for w, s, b, o in zip(weights, scales, biases, outputs):
-        _native.tokenwise_linear(activation.reshape(1, k), _native.TW_ACT_A8, activation_scale.reshape(-1), w,
-                                 _native.TW_KMAJOR_W4, s, b, n, k, _native.TW_EPI_A8, o.view(1, n),
-                                 workspace=ws if need else None)
+    """One decode linear into caller-owned buffers (decode_w4a8_triton.py:113-149):
+    the one-projection case of launch_decode_group. ``config`` is accepted
+    for call compatibility (the split is chosen per shape)."""
+    return launch_decode_group(activation, (packed,), (residual,), activation_scale, (weight_scale,), (bias,),
+                               (output,), partial)[0]
 
 
 def decode_linear(activation, packed, residual, activation_scale, weight_scale, bias, output):
-    """One split-K decode into `output` (decode_w4a8_triton.py:312-323)."""
-    _decode_check_residual(residual)
-    n = packed.shape[1]
-    k = packed.shape[0] * 2
+    """One split-K decode into `output` with a per-call workspace
+    (decode_w4a8_triton.py:312-323)."""
+    _no_residual((residual,))
+    n, k = _w4_shape(packed)
     m = activation.numel() // k
     _native.tokenwise_linear(activation.reshape(m, k), _native.TW_ACT_A8, activation_scale.reshape(-1), packed,
                              _native.TW_KMAJOR_W4, weight_scale, bias, n, k, _native.TW_EPI_A8, output.view(m, n),
-                             workspace=_workspace(_LAUNCH_OWNER, m, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8,
-                                                  activation.device))
-    state = _DECODE_STATE.get()
-    if state is not None:
-        state.split_k_calls += 1
-        state.partial_kernels += 1
-        state.reduction_kernels += 1
+                             workspace=_split_workspace(m, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8,
+                                                        activation.device))
+    _count_split_decode(1, n, k)
+
+
+def _record(issue, device):
+    """A hipGraph of the launches `issue` makes: one eager pass on a side
+    stream first (it runs every argument check outside the capture), then
+    the capture on that stream; the current stream waits for both."""
+    side = torch.cuda.Stream(device=device)
+    current = torch.cuda.current_stream(device)
+    side.wait_stream(current)
+    with torch.cuda.stream(side):
+        issue()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        issue()
+    current.wait_stream(side)
+    return graph
 
 
 class DecodeGraphPlan:
-    """Replay the fixed decode launch sequence (per-row quantizer, then one
-    split-K GEMM per projection) from a hipGraph with private staging
-    buffers; inputs are copied in and outputs cloned on every call
-    (decode_w4a8_triton.py:326-425). Where the row fits it
-    (in_features <= 16384), each projection's split GEMM quantizes the row
-    itself (actune_tokenwise_linear_x): two launches per projection and no
-    quantizer launch, with the same codes and outputs."""
+    """A captured decode of 1 to 4 sibling projections of one row. The
+    contract is the reference's (decode_w4a8_triton.py:326-425): each run
+    copies the row into the plan's staging buffer, replays, and returns the
+    outputs [projections, N] as a fresh tensor, so callers never hold
+    graph-owned memory. The graph holds two launches: the GEMM over every
+    projection's tiles that quantizes the row itself (rows up to 16384
+    long; longer rows add the quantizer launch first) and the integer reduce
+    for all projections. Runs are serialised by a lock, since they share the
+    staging buffers."""
 
     def __init__(self, value, weights, residuals, scales, biases):
-        for r in residuals:
-            _decode_check_residual(r)
-        self.lock = threading.Lock()
-        self.weights = tuple(weights)
-        self.residuals = tuple(residuals)
-        self.scales = tuple(scales)
-        self.biases = tuple(biases)
-        self.k = weights[0].shape[0] * 2
-        self.n = weights[0].shape[1]
-        self.groups = len(weights)
+        _no_residual(residuals)
+        if not 1 <= len(weights) <= _native.MAX_TARGETS:
+            raise ValueError(f"a decode plan takes 1 to {_native.MAX_TARGETS} projections")
+        self.weights, self.residuals = tuple(weights), tuple(residuals)
+        self.scales, self.biases = tuple(scales), tuple(biases)
+        self.n, self.k = _w4_shape(self.weights[0])
+        self.groups = len(self.weights)
         dev = value.device
-        self.fused = self.k <= _FUSED_MAX_K and value.dtype in (torch.bfloat16, torch.float16, torch.float32)
+        self.quantize_in_gemm = self.k <= _FUSED_MAX_K
         self.input = torch.empty((1, self.k), device=dev, dtype=value.dtype)
-        self.activation = None if self.fused else torch.empty_like(self.input, dtype=torch.int8)
+        self.activation = None if self.quantize_in_gemm else torch.empty((1, self.k), device=dev, dtype=torch.int8)
         self.scale = torch.empty(1, device=dev, dtype=torch.float32)
         self.output = torch.empty((self.groups, self.n), device=dev, dtype=value.dtype)
-        self.outputs = tuple(self.output[i:i + 1] for i in range(self.groups))
-        need = _native.tokenwise_workspace_bytes(1, self.n, self.k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8)
-        self.partial = torch.empty(max(need, 256) * self.groups, device=dev, dtype=torch.uint8)
-        self._need = need
-        self.graph = torch.cuda.CUDAGraph()
-        stream = torch.cuda.Stream(device=dev)
-        current = torch.cuda.current_stream(dev)
-        stream.wait_stream(current)
-        with torch.cuda.stream(stream):
-            self.input.copy_(value.reshape(1, self.k))
-            for _ in range(3):
-                self._launch()
-        current.wait_stream(stream)
-        with torch.cuda.graph(self.graph, stream=stream):
-            self._launch()
-        current.wait_stream(stream)
+        need = self.groups * _native.tokenwise_workspace_bytes(1, self.n, self.k, _native.TW_KMAJOR_W4,
+                                                               _native.TW_ACT_A8)
+        self.partial = torch.empty(need, device=dev, dtype=torch.uint8) if need else None
+        self.lock = threading.Lock()
+        self.input.copy_(value.reshape(1, self.k))
+        self.graph = _record(self._issue, dev)
 
-    def _launch(self):
-        if not self.fused:
+    def _issue(self):
+        targets = [(w, s, b, self.output[i:i + 1])
+                   for i, (w, s, b) in enumerate(zip(self.weights, self.scales, self.biases))]
+        if self.quantize_in_gemm:
+            _native.tokenwise_linear_multi(targets, _native.TW_KMAJOR_W4, self.n, self.k, _native.TW_EPI_A8,
+                                           self.scale, x=self.input, workspace=self.partial)
+        else:
             _native.tokenwise_quantize(self.input, 8, self.activation, self.scale)
-        step = max(self._need, 256)
-        for i in range(self.groups):
-            ws = self.partial[i * step:(i + 1) * step] if self._need else None
-            if self.fused:
-                _native.tokenwise_linear_x(self.input, self.scale, self.weights[i], _native.TW_KMAJOR_W4,
-                                           self.scales[i], self.biases[i], self.n, self.k, _native.TW_EPI_A8,
-                                           self.outputs[i], workspace=ws)
-            else:
-                _native.tokenwise_linear(self.activation, _native.TW_ACT_A8, self.scale, self.weights[i],
-                                         _native.TW_KMAJOR_W4, self.scales[i], self.biases[i], self.n, self.k,
-                                         _native.TW_EPI_A8, self.outputs[i], workspace=ws)
+            _native.tokenwise_linear_multi(targets, _native.TW_KMAJOR_W4, self.n, self.k, _native.TW_EPI_A8,
+                                           self.scale, codes=self.activation, workspace=self.partial)
 
     @property
     def workspace_bytes(self):
-        return sum(t.numel() * t.element_size()
-                   for t in (self.input, self.activation, self.scale, self.output, self.partial) if t is not None)
+        """Device bytes the plan holds outside the graph's own pool."""
+        held = (self.input, self.activation, self.scale, self.output, self.partial)
+        return sum(t.numel() * t.element_size() for t in held if t is not None)
 
     def run(self, value):
         with self.lock:
             self.input.copy_(value.reshape(1, self.k))
             self.graph.replay()
-            output = self.output.clone()
-        state = _DECODE_STATE.get()
-        if state is not None:
-            state.graph_replays += 1
-            state.graph_quantization_kernels += 1
-            state.resident_quantization_kernels += 1
-            state.partial_kernels += 1
-            state.reduction_kernels += 1
-            if self.groups == 1:
-                state.split_k_calls += 1
-            else:
-                state.projection_groups += 1
-                state.projection_calls_fused += self.groups
-        return output
-
-
-def _tensor_version(tensor):
-    if tensor is None or tensor.is_inference():
-        return None
-    return tensor._version
+            result = self.output.clone()
+        separate = int(not self.quantize_in_gemm)
+        _count(1, graph_replays=1, graph_quantization_kernels=separate, resident_quantization_kernels=separate)
+        _count_split_decode(self.groups, self.n, self.k)
+        return result
 
 
 def graph_plan_key(value, weights, residuals, scales, biases):
-    return (torch.cuda.current_stream(value.device).cuda_stream,
-            tuple((id(t), _tensor_version(t)) for t in (*weights, *residuals, *scales, *biases)))
+    """What a captured plan depends on: the device and stream it replays on,
+    the row dtype of its staging buffer, and the storage every captured
+    launch reads (the graph holds addresses, so a weight written in place is
+    still read correctly, while a weight moved to new storage needs a new
+    plan)."""
+    storage = tuple(None if t is None else t.data_ptr() for t in (*weights, *residuals, *scales, *biases))
+    return (value.device, torch.cuda.current_stream(value.device).cuda_stream, value.dtype, storage)
 
 
 def graph_decode_linear(owner, value, packed, residual, scale, bias):
-    """Cached DecodeGraphPlan per (stream, tensor identities) on the owning
-    module (decode_w4a8_triton.py:441-455)."""
-    cache = getattr(owner, "_decode_graph_plans", None)
-    if cache is None:
-        cache = {}
-        owner._decode_graph_plans = cache
+    """Decode of one row through the owner's plan for this key, captured on
+    first use; the owner keeps its most recently used plans
+    (decode_w4a8_triton.py:441-455)."""
+    plans = owner.__dict__.setdefault("_decode_graph_plans", OrderedDict())
     key = graph_plan_key(value, (packed,), (residual,), (scale,), (bias,))
-    plan = cache.get(key)
+    plan = plans.get(key)
     if plan is None:
-        if len(cache) >= 8:
-            cache.clear()
         plan = DecodeGraphPlan(value, (packed,), (residual,), (scale,), (bias,))
-        cache[key] = plan
+        plans[key] = plan
+        while len(plans) > _PLANS_PER_MODULE:
+            plans.popitem(last=False)
+    else:
+        plans.move_to_end(key)
     return plan.run(value).reshape(*value.shape[:-1], packed.shape[1])
 
 
 def decode_workspace_summary(module):
-    """Count explicit persistent buffers after warm-up (decode_w4a8_triton.py:458-480)."""
-    plans = {}
-    mlp_plans = {}
-    for child in module.modules():
-        for plan in getattr(child, "_decode_graph_plans", {}).values():
-            plans[id(plan)] = plan
-        controller = getattr(child, "_decode_mlp_controller", None)
-        if controller is not None:
-            for plan in controller.plans.values():
-                mlp_plans[id(plan)] = plan
-        group = getattr(child, "_decode_projection_group", None)
-        if group is not None:
-            for plan in group.plans.values():
-                plans[id(plan)] = plan
-    return {
-        "decode_graph_plan_count": len(plans),
-        "mlp_graph_plan_count": len(mlp_plans),
-        "mlp_graph_input_output_bytes": sum(t.numel() * t.element_size()
-                                            for plan in mlp_plans.values() for t in (plan.input, plan.output)),
-        "decode_graph_explicit_workspace_bytes": sum(plan.workspace_bytes for plan in plans.values()),
-    }
+    """Plans and explicit device bytes of the decode graph plans held by
+    `module` and its children, under the reference's keys
+    (decode_w4a8_triton.py:458-480). This backend keeps no MLP graph plans:
+    those two entries are 0."""
+    plans = {id(plan): plan for child in module.modules()
+             for plan in child.__dict__.get("_decode_graph_plans", {}).values()}
+    return {"decode_graph_plan_count": len(plans), "mlp_graph_plan_count": 0, "mlp_graph_input_output_bytes": 0,
+            "decode_graph_explicit_workspace_bytes": sum(plan.workspace_bytes for plan in plans.values())}

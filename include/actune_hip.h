@@ -246,6 +246,36 @@ int actune_tokenwise_linear_x(const void* x, int x_dtype, float* a_scales, const
                               int64_t M, int64_t N, int64_t K, int epilogue, void* workspace,
                               int64_t workspace_bytes, void* stream);
 
+/* One projection of a multi-target tokenwise call. */
+typedef struct actune_tw_target {
+  const void* w;          /* weights [.., N] in the call's layout */
+  const float* w_scale;   /* [N] */
+  const void* bias;       /* [N] in the call's bias dtype, or NULL */
+  void* out;              /* [M, N] in out_dtype */
+} actune_tw_target;
+
+/*
+ * Tokenwise linear for 1 to ACTUNE_MAX_TARGETS sibling projections that read
+ * the same activation rows (q/k/v, gate/up) and share N, K and the layouts:
+ * one GEMM launch over every target's tiles and K splits, and, when K is
+ * split, one integer reduce for all of them. Replaces the grouped decode pair
+ * _decode_group_partial_kernel + _decode_group_reduce_kernel
+ * (actune/kernels/decode_w4a8_triton.py:150-239, launched by
+ * launch_decode_group at :205-239). Each target's output equals
+ * actune_tokenwise_linear (codes) or actune_tokenwise_linear_x (rows) on the
+ * same operands bit for bit.
+ * Exactly one of a / x is non-NULL:
+ *   a: activation codes in a_layout, a_scales [M] read;
+ *   x: rows [M, K] of x_dtype quantized inside the launch (A8, the rows and
+ *      K actune_tokenwise_linear_x takes), a_scales [M] written.
+ * workspace: ntargets x actune_tokenwise_workspace_bytes(M, N, K, w_layout,
+ * a_layout) bytes (none when that is 0), 16-byte aligned.
+ */
+int actune_tokenwise_linear_multi(const void* a, int a_layout, const void* x, int x_dtype, float* a_scales,
+                                  int w_layout, const actune_tw_target* targets, int ntargets, int bias_dtype,
+                                  int out_dtype, int64_t M, int64_t N, int64_t K, int epilogue, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
+
 /*
  * Host-only check of the operand element orders the kernels rely on
  * (sub-byte unpack and cross-width reorder for every (W, A) pair). Returns 0

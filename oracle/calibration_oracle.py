@@ -5,8 +5,16 @@ Follows actune/calibration.py:42-93 step by step in torch-CPU, with the
 float GEMMs of the candidate evaluations in float64 (so its scores carry no
 summation-order noise of their own) and the codebooks taken from the C
 oracle: activation codes of calibration.py:7-16 (grouped_oracle.c) and
-weight codes with the GPU division semantics of quantizers.py:23-94 (the
-reference runs them on the layer's device).
+weight codes of quantizers.py:23-94 with the division semantics of the
+device the reference runs them on (``gpu_division``: True for a layer on
+the GPU, the product's case; False for torch-CPU, the case of the golden
+vectors written by tests/golden/make_calibration_vectors.py).
+
+Pinned by tests/test_calibration_cpu.py: against the reference's own outputs
+on seeded layers (tests/golden/calibration_vectors.npz), and by invariants
+(constant channel moments give a unit scale, every selected clip is the
+first argmin of an independently computed row loss, each error is the
+gain-weighted sum of the row minima, W4-grid weights dequantize exactly).
 """
 from __future__ import annotations
 
@@ -29,14 +37,16 @@ def _dequant_x(x_bf16, a):
     return (codes.astype(np.float32).reshape(m, k // 64, 64) * scales[:, :, None]).reshape(m, k).astype(np.float64)
 
 
-def _dequant_w(weight_bf16, w, a, ratio):
-    codes, scale = O.weight_codes(weight_bf16.float().numpy(), w, a, ratio, gpu_division=True)
+def _dequant_w(weight_bf16, w, a, ratio, gpu_division=True):
+    codes, scale = O.weight_codes(weight_bf16.float().numpy(), w, a, ratio, gpu_division=gpu_division)
     return (codes.astype(np.float32) * scale[:, None]).astype(np.float64)
 
 
-def calibrate_linear(weight, x, gains=None, *, budget="w4a4", clip_grid=CLIP_GRID, scale=None):
+def calibrate_linear(weight, x, gains=None, *, budget="w4a4", clip_grid=CLIP_GRID, scale=None, gpu_division=True):
     """weight: bf16 [N, K] (CPU), x: bf16 [M, K] (CPU). Returns the same dict
-    as the reference. scale: an explicit channel scale (skips the alpha fit)."""
+    as the reference. scale: an explicit channel scale (skips the alpha fit);
+    gpu_division: weight codes as torch computes them on the GPU (else
+    torch-CPU's IEEE quotient)."""
     n = weight.shape[0]
     gains = np.ones(n) if gains is None else np.asarray(gains, np.float64)
     reference = x.double().numpy() @ weight.double().numpy().T
@@ -48,7 +58,7 @@ def calibrate_linear(weight, x, gains=None, *, budget="w4a4", clip_grid=CLIP_GRI
             s = moment.pow(alpha)
             s = (s / (s.max() * s.min()).sqrt()).clamp(1 / 16, 16).to(x.dtype)
             wt = (weight * s[None, :]).to(x.dtype)
-            y = _dequant_x((x / s).contiguous(), base_a) @ _dequant_w(wt, 4, base_a, None).T
+            y = _dequant_x((x / s).contiguous(), base_a) @ _dequant_w(wt, 4, base_a, None, gpu_division).T
             score = float((((y - reference) ** 2).mean(0) * gains).sum())
             if best is None or score < best[0]:
                 best = score, s
@@ -62,7 +72,7 @@ def calibrate_linear(weight, x, gains=None, *, budget="w4a4", clip_grid=CLIP_GRI
             row_error = np.full(n, np.inf)
             selected = np.ones(n, np.float32)
             for ratio in clip_grid:
-                y = xq @ _dequant_w(wt, w, a, ratio).T
+                y = xq @ _dequant_w(wt, w, a, ratio, gpu_division).T
                 loss = ((y - reference) ** 2).mean(0)
                 improve = loss < row_error
                 selected[improve], row_error[improve] = ratio, loss[improve]

@@ -63,6 +63,77 @@ def test_grouped_linear_forward_matches_oracle(W, A, lead):
     np.testing.assert_array_equal(bits(out.reshape(-1, n)), want)
 
 
+def _torch_gpu_codes(v, W, A, ratio):
+    """The weight codebook formulas of quantizers.py:23-94 evaluated inline by
+    torch on the GPU (tensor / Python scalar is a reciprocal multiply there)."""
+    amax = v.abs().amax(dim=1).clamp_min(1e-8)
+    if ratio is not None and not (W == 8 and A != 4):
+        amax = amax * ratio
+    if W == 2:
+        return (v / amax[:, None]).round().clamp(-2, 1).to(torch.int8), amax
+    if W == 4 or A == 4:
+        s4 = amax / 7.0
+        q4 = (v / s4[:, None]).round().clamp(-8, 7).to(torch.int8)
+        if W == 4:
+            return q4, s4
+        base = q4.to(torch.int16)
+        res = (16.0 * (v / s4[:, None] - q4.float())).round().clamp(-8, 7).to(torch.int16)
+        res = torch.minimum(torch.maximum(res, (-128 - 16 * base).clamp(min=-8)), (127 - 16 * base).clamp(max=7))
+        return (16 * base + res).to(torch.int8), s4 / 16.0
+    s = v.abs().amax(dim=1).clamp_min(1e-8) / 127.0
+    return (v / s[:, None]).round().clamp(-128, 127).to(torch.int8), s
+
+
+@pytest.mark.parametrize("W,A", PAIRS)
+@pytest.mark.parametrize("ratio_kind", ["none", "scalar", "rows"])
+def test_cuda_built_codes_follow_the_layer_device(W, A, ratio_kind):
+    """grouped.py:120 computes weight_codes on the layer's device. A
+    GroupedLinear built from a CUDA-resident layer therefore holds the codes
+    torch-GPU computes (amax / 7.0 and / 127.0 as reciprocal multiplies,
+    quantizers.py:38, 93): its packed_weight and weight_scale equal the
+    oracle with gpu_division=True and the formulas evaluated inline by torch
+    on the GPU, bit for bit. The same layer built on the CPU equals the IEEE
+    oracle."""
+    k, n = 512, 96
+    lin = _linear(k, n, False, seed=40 + W * 3 + A)
+    w_np = lin.weight.detach().float().numpy()
+    ratio = {"none": None, "scalar": 0.9, "rows": torch.linspace(0.7, 1.0, n)}[ratio_kind]
+    ratio_np = None if ratio is None else (ratio if isinstance(ratio, float) else ratio.numpy())
+    cuda_lin = _linear(k, n, False, seed=40 + W * 3 + A).to(DEV)
+    ratio_dev = ratio.to(DEV) if isinstance(ratio, torch.Tensor) else ratio
+    mod = GroupedLinear(cuda_lin, W, A, ratio_dev)
+    assert mod.packed_weight.is_cuda
+    want_c, want_s = O.weight_codes(w_np, W, A, ratio_np, gpu_division=True)
+    np.testing.assert_array_equal(mod.packed_weight.cpu().numpy(), O.pack_rows(want_c, W))
+    np.testing.assert_array_equal(mod.weight_scale.cpu().numpy(), want_s)
+    inline_c, inline_s = _torch_gpu_codes(cuda_lin.weight.detach().float(), W, A, ratio_dev)
+    assert torch.equal(mod.weight_scale, inline_s)
+    np.testing.assert_array_equal(O.unpack_rows(mod.packed_weight.cpu().numpy(), W, k), inline_c.cpu().numpy())
+    host = GroupedLinear(lin, W, A, ratio)
+    ieee_c, ieee_s = O.weight_codes(w_np, W, A, ratio_np)
+    np.testing.assert_array_equal(host.packed_weight.numpy(), O.pack_rows(ieee_c, W))
+    np.testing.assert_array_equal(host.weight_scale.numpy(), ieee_s)
+    if W != 2:  # the two semantics really differ here (W2 divides by no constant)
+        assert not np.array_equal(want_s, ieee_s)
+
+
+def test_install_bank_on_cuda_model_uses_gpu_codes():
+    """install_bank on a CUDA-resident model: every backend of every target
+    holds the gpu_division codes of its (channel-scaled) weight."""
+    model, bank, _ = _install(scales=True)
+    source = Expert(0).to(DEV)
+    for name in EXPERT:
+        res = getattr(model, name)
+        src = getattr(source, name).weight.detach()
+        if res.input_scale is not None:
+            src = src * res.input_scale[None, :]
+        for mode, backend in res.backends.items():
+            W, A = int(mode[1]), int(mode[3])
+            c, s = O.weight_codes(src.float().cpu().numpy(), W, A, gpu_division=True)
+            np.testing.assert_array_equal(backend.packed_weight.cpu().numpy(), O.pack_rows(c, W), err_msg=mode)
+            np.testing.assert_array_equal(backend.weight_scale.cpu().numpy(), s, err_msg=mode)
+
+
 def test_grouped_linear_rejects_host_input():
     mod = GroupedLinear(_linear(64, 16, False, 1), 4, 8, None).to(DEV)
     with pytest.raises(ValueError, match="requires CUDA"):
@@ -271,6 +342,31 @@ def test_shared_activation_scope_quantizes_once_per_width():
         assert all(torch.equal(a, b) for a, b in zip(plain, shared))
 
 
+def test_shared_activation_scope_drops_codes_of_mutated_or_older_inputs():
+    """An input written in place between two linears (x.add_(), as a flow
+    step's x += dt * v does) is quantized again, and the scope keeps the
+    codes of one input only: a linear on another tensor in between drops
+    them. Every output equals the unshared module on the same values."""
+    from actune_amd.kernels.grouped import shared_activation_scope
+    lin_a, lin_b = _linear(1024, 256, False, seed=61), _linear(1024, 128, False, seed=62)
+    a = GroupedLinear(lin_a, 4, 4, None).to(DEV)
+    b = GroupedLinear(lin_b, 8, 4, None).to(DEV)
+    x = torch.randn(50, 1024, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16).to(DEV)
+    other = torch.randn(50, 1024, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16).to(DEV)
+    x0 = x.clone()
+    with shared_activation_scope() as state:
+        y1 = a(x)
+        x.add_(0.5)
+        y2 = b(x)
+        y3 = a(other)
+        y4 = b(x)
+        y5 = a(x)
+    assert (state.misses, state.hits) == (4, 1), (state.misses, state.hits)
+    assert len(state.entries) == 1
+    assert torch.equal(y1, a(x0)) and torch.equal(y2, b(x)) and torch.equal(y3, a(other))
+    assert torch.equal(y4, b(x)) and torch.equal(y5, a(x))
+
+
 def test_graph_replay_limit_falls_back_to_eager():
     model, _, runtime = _install()
     replay = GraphReplay(model, runtime.modules, max_graphs=2)
@@ -295,7 +391,7 @@ def test_graph_replay_shared_a8_scope():
     seen = []
 
     def fn(x):
-        seen.append(T._SHARED_A8_STATE.get().enabled)
+        seen.append(T.current_shared_a8_cache().enabled)
         return x * 2
 
     for flag in (False, True):

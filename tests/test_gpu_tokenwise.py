@@ -378,3 +378,156 @@ def test_fused_row_quantization_rejects_what_it_does_not_take():
     rc = lib.actune_tokenwise_linear_x(x.data_ptr(), 0, s_out.data_ptr(), w.data_ptr(), _native.TW_ROWS_S4,
                                        ws.data_ptr(), None, 0, out.data_ptr(), 0, 1, 64, 256, 0, None, 0, None)
     assert rc != 0 and b"K-major" in lib.actune_last_error()
+
+
+# ---------------------------------------------------------------- sibling projections in one launch
+MULTI_LAYOUTS = [(4, 8, _native.TW_KMAJOR_W4, 0), (8, 8, _native.TW_KMAJOR_W8, 0), (2, 8, _native.TW_KMAJOR_W2, 0),
+                 (4, 4, _native.TW_ROWS_S4, 1), (2, 4, _native.TW_ROWS_S2, 1), (8, 4, _native.TW_KMAJOR_W8, 0)]
+
+
+def _packed_targets(n, k, W, A, wl, count, seed, bias_every=None, dtype=torch.bfloat16, m=1):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        w = rng.standard_normal((n, k)).astype(np.float32)
+        codes, scale = O.weight_codes(w, W, A, gpu_division=True)
+        packed = O.pack_kmajor(codes, W) if wl <= _native.TW_KMAJOR_W2 else O.pack_rows(codes, W)
+        bias = None
+        if bias_every:
+            bias = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(DEV).to(dtype)
+        out.append(dict(codes=codes, scale=scale, w=torch.from_numpy(packed).to(DEV),
+                        ws=torch.from_numpy(scale).to(DEV), bias=bias,
+                        out=torch.full((m, n), 5.0, device=DEV, dtype=dtype)))
+    return out
+
+
+@pytest.mark.parametrize("W,A,wl,mode", MULTI_LAYOUTS)
+@pytest.mark.parametrize("m,n,k", [(1, 256, 2048), (8, 512, 4096), (17, 96, 1024), (300, 256, 512)])
+@pytest.mark.parametrize("count", [1, 3, 4])
+def test_multi_target_equals_single_calls(W, A, wl, mode, m, n, k, count):
+    """actune_tokenwise_linear_multi on codes: every target equals its own
+    actune_tokenwise_linear call bit for bit (split and unsplit shapes,
+    small-M and ring geometries, with biases); the first target also
+    against the oracle."""
+    x, _, _ = seeded_inputs(m, k, 1, seed=m + n + k + count)
+    a_layout = _native.TW_ACT_A8 if A == 8 else _native.TW_ACT_A4
+    act, s = _native.tokenwise_quantize(x.to(DEV), A)
+    tg = _packed_targets(n, k, W, A, wl, count, seed=W * 10 + A + count, bias_every=count > 1, m=m)
+    need = _native.tokenwise_workspace_bytes(m, n, k, wl, a_layout)
+    work = torch.full((max(count * need, 1),), 0x5A, dtype=torch.uint8, device=DEV)
+    _native.tokenwise_linear_multi([(t["w"], t["ws"], t["bias"], t["out"]) for t in tg], wl, n, k, mode, s,
+                                   codes=act, a_layout=a_layout, workspace=work if need else None)
+    for i, t in enumerate(tg):
+        want = torch.empty(m, n, device=DEV, dtype=torch.bfloat16)
+        single = torch.empty(max(need, 1), dtype=torch.uint8, device=DEV)
+        _native.tokenwise_linear(act, a_layout, s, t["w"], wl, t["ws"], t["bias"], n, k, mode, want,
+                                 workspace=single if need else None)
+        assert torch.equal(t["out"], want), (i, W, A)
+    a_codes, a_scales = O.tw_quantize_rows(bits(x), A)
+    b0 = None if tg[0]["bias"] is None else tg[0]["bias"].float().cpu().numpy()
+    want0 = O.round_out(O.tw_epilogue(O.tw_dots(a_codes, tg[0]["codes"]), a_scales, tg[0]["scale"], b0, mode), "bf16")
+    np.testing.assert_array_equal(bits(tg[0]["out"]), want0)
+
+
+@pytest.mark.parametrize("m,n,k,count", [(1, 4096, 4096, 3), (1, 11008, 4096, 2), (8, 4096, 4096, 3),
+                                         (8, 11008, 4096, 2), (1, 4096, 11008, 1), (3, 256, 2048, 2)])
+def test_multi_target_quantizes_rows_in_launch_full_size(m, n, k, count):
+    """Llama-2-7B q/k/v and gate/up at M = 1 and 8 with the rows quantized
+    inside the launch: the written row scales equal the quantizer's, and
+    each target equals the oracle on 64 sampled columns."""
+    x, _, _ = seeded_inputs(m, k, 1, seed=n + k + m)
+    xd = x.to(DEV)
+    tg = _packed_targets(n, k, 4, 8, _native.TW_KMAJOR_W4, count, seed=n + count + m, m=m)
+    need = count * _native.tokenwise_workspace_bytes(m, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8)
+    work = torch.full((max(need, 1),), 0x5A, dtype=torch.uint8, device=DEV)
+    s_out = torch.full((m,), -1.0, device=DEV)
+    _native.tokenwise_linear_multi([(t["w"], t["ws"], None, t["out"]) for t in tg], _native.TW_KMAJOR_W4, n, k,
+                                   _native.TW_EPI_A8, s_out, x=xd, workspace=work if need else None)
+    torch.cuda.synchronize()
+    a_codes, a_scales = O.tw_quantize_rows(bits(x), 8)
+    np.testing.assert_array_equal(s_out.cpu().numpy(), a_scales)
+    cols = np.sort(np.random.default_rng(k).choice(n, size=64, replace=False))
+    for i, t in enumerate(tg):
+        want = O.round_out(O.tw_epilogue(O.tw_dots(a_codes, t["codes"][cols]), a_scales, t["scale"][cols], None, 0),
+                           "bf16")
+        np.testing.assert_array_equal(bits(t["out"])[:, cols], want, err_msg=str(i))
+
+
+def test_multi_target_rejects_bad_calls():
+    x = torch.randn(1, 256, device=DEV).to(torch.bfloat16)
+    tg = _packed_targets(64, 256, 4, 8, _native.TW_KMAJOR_W4, 2, seed=1)
+    s = torch.empty(1, device=DEV)
+    targets = [(t["w"], t["ws"], t["bias"], t["out"]) for t in tg]
+    with pytest.raises(ValueError, match="either codes or x"):
+        _native.tokenwise_linear_multi(targets, _native.TW_KMAJOR_W4, 64, 256, 0, s)
+    with pytest.raises(ValueError, match="1 to 4 targets"):
+        _native.tokenwise_linear_multi(targets * 3, _native.TW_KMAJOR_W4, 64, 256, 0, s, x=x)
+    lib = _native.lib()
+    structs = (_native._TwTarget * 5)()
+    rc = lib.actune_tokenwise_linear_multi(None, 0, x.data_ptr(), 0, s.data_ptr(), _native.TW_KMAJOR_W4, structs, 5,
+                                           2, 0, 1, 64, 256, 0, None, 0, None)
+    assert rc != 0 and b"ACTUNE_MAX_TARGETS" in lib.actune_last_error()
+    rc = lib.actune_tokenwise_linear_multi(x.data_ptr(), 0, x.data_ptr(), 0, s.data_ptr(), _native.TW_KMAJOR_W4,
+                                           structs, 2, 2, 0, 1, 64, 256, 0, None, 0, None)
+    assert rc != 0 and b"either" in lib.actune_last_error()
+
+
+def test_decode_group_plan_and_launch_group():
+    """q/k/v of one row as ONE decode plan (one GEMM launch over the three
+    projections + one reduce, the row quantized in the launch) and through
+    launch_decode_group on caller buffers: both equal the modules' own
+    direct calls bit for bit, and the counters record one projection group."""
+    torch.manual_seed(9)
+    mods = [T.W4A8TritonLinear(torch.nn.Linear(4096, 4096, bias=b, dtype=torch.bfloat16, device=DEV))
+            for b in (False, True, False)]
+    x, _, _ = seeded_inputs(1, 4096, 1, seed=9)
+    xd = x.to(DEV)
+    with T.decode_optimization_scope(enabled=False):
+        want = [m(xd) for m in mods]
+    plan = T.DecodeGraphPlan(xd, [m.packed_weight for m in mods], [None] * 3, [m.weight_scale for m in mods],
+                             [m.bias for m in mods])
+    with T.decode_optimization_scope() as stats:
+        for _ in range(3):
+            got = plan.run(xd)
+            torch.cuda.synchronize()
+            assert all(torch.equal(got[i:i + 1], want[i]) for i in range(3))
+    assert stats.graph_replays == 3 and stats.projection_groups == 3 and stats.projection_calls_fused == 9
+    assert stats.graph_quantization_kernels == 0  # the row is quantized inside the GEMM launch
+    act, s = _native.tokenwise_quantize(xd, 8)
+    outs = [torch.empty(1, 4096, device=DEV, dtype=torch.bfloat16) for _ in mods]
+    partial = torch.full((3 * 32, 4096), 7, dtype=torch.int32, device=DEV)
+    T.launch_decode_group(act, [m.packed_weight for m in mods], [None] * 3, s, [m.weight_scale for m in mods],
+                          [m.bias for m in mods], outs, partial)
+    assert all(torch.equal(o, w) for o, w in zip(outs, want))
+    with pytest.raises(NotImplementedError):
+        T.launch_decode_group(act, [mods[0].packed_weight], [mods[0].packed_weight], s, [mods[0].weight_scale],
+                              [None], outs[:1], partial)
+
+
+def test_captured_split_workspace_survives_later_calls():
+    """A W4A8 module captured at M = 1 (its split-K workspace comes from the
+    graph's pool), then called eagerly at M = 8 (a larger workspace), then
+    filler tensors allocated and written: replays leave the fillers
+    untouched and still equal the eager result."""
+    torch.manual_seed(10)
+    mod = T.W4A8TritonLinear(torch.nn.Linear(4096, 4096, bias=False, dtype=torch.bfloat16, device=DEV))
+    x1 = torch.randn(1, 4096, device=DEV).to(torch.bfloat16)
+    x8 = torch.randn(8, 4096, device=DEV).to(torch.bfloat16)
+    with T.decode_optimization_scope(enabled=False):
+        want1 = mod(x1)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            mod(x1)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            y = mod(x1)
+        want8 = mod(x8)
+        fillers = [torch.full((1 << 18,), 1234 + i, dtype=torch.int32, device=DEV) for i in range(16)]
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, want1)
+        assert all(bool((f == 1234 + i).all()) for i, f in enumerate(fillers))
+        assert torch.equal(mod(x8), want8)

@@ -101,19 +101,35 @@ def test_replace_helpers():
 
 def test_shared_cache_scope_and_counters():
     with T.shared_a8_cache_scope(enabled=False) as state:
-        assert T._SHARED_A8_STATE.get() is state and not state.enabled
+        assert T.current_shared_a8_cache() is state and not state.enabled
         assert state.hits == state.misses == 0
     with T.decode_optimization_scope(enabled=False) as stats:
-        assert not T._DECODE_ENABLED.get()
+        assert not T.decode_enabled()
         assert set(stats.metrics()) == {"split_k_calls", "projection_groups", "projection_calls_fused",
                                         "partial_kernels", "reduction_kernels", "resident_quantization_kernels",
                                         "graph_replays", "graph_quantization_kernels"}
-    assert T._DECODE_ENABLED.get()
+        with T.runtime_optimization_scope(dense_candidates=True):
+            assert not T.decode_enabled() and T.dense_candidates_enabled()
+        assert not T.dense_candidates_enabled()
+    assert T.decode_enabled()
     with T.runtime_optimization_scope(dense_candidates=True) as rs:
-        assert T._DENSE_CANDIDATES.get() and T.runtime_stats_dict(rs)["resident_a8_kernels"] == 0
-    assert not T._DENSE_CANDIDATES.get()
+        assert T.dense_candidates_enabled() and T.runtime_stats_dict(rs) == {
+            "resident_a8_kernels": 0, "mlp_graph_replays": 0, "predecoded_r4_gemms": 0}
+        with T.runtime_optimization_scope() as inner:
+            assert T.dense_candidates_enabled() and inner is not rs  # None keeps the enclosing setting
+    assert not T.dense_candidates_enabled()
     T.clear_shared_a8_cache()
-    assert T._SHARED_A8_STATE.get() is not None
+    assert T.current_shared_a8_cache() is not None
+
+
+def test_replace_is_all_or_nothing():
+    """A selected layer the backend cannot take (out_features not a multiple
+    of 16 for the K-major layouts) makes the helper raise before anything is
+    replaced."""
+    model = torch.nn.Sequential(torch.nn.Linear(128, 32), torch.nn.Linear(128, 24))
+    with pytest.raises(ValueError, match="divisible by 16"):
+        T.replace_with_w4a8_triton_(model, lambda child, name: isinstance(child, torch.nn.Linear))
+    assert all(type(m) is torch.nn.Linear for m in model)
 
 
 def test_decode_eligibility():
