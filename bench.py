@@ -420,6 +420,77 @@ def bench_gemma(torch, _native, steps, warmup):
     return out
 
 
+GEMMA_BLOCK = {"q": (2048, 2048), "k": (256, 2048), "v": (256, 2048), "o": (2048, 2048),
+               "gate": (16384, 2048), "up": (16384, 2048), "down": (2048, 16384)}
+# C4's bank: fixed versions and the two binary switchable matrices (q, gate),
+# W4A4 <-> W4A8; the W4A2 layers keep the [M, 2048] group at 4 activation bits
+GEMMA_FIXED = {"k": "w4a2", "v": "w4a2", "o": "w4a2", "up": "w4a2", "down": "w4a4"}
+GEMMA_SWITCH = {"q00": ("w4a4", "w4a4"), "q01": ("w4a4", "w4a8"), "q11": ("w4a8", "w4a8"), "q10": ("w4a8", "w4a4")}
+
+
+def bench_gemma_bank(torch, steps, warmup):
+    """C4's bank: one Gemma-2B-shaped block (q / o 2048x2048, k / v
+    256x2048, gate / up 16384x2048, down 2048x16384, random init) installed
+    with install_bank as a W4A4 SharedBank whose two binary switchable
+    matrices (q and gate) run W4A8 in q01 / q11 / q10, balanced by W4A2
+    k / v / o / up (the bank rules of precision.py:54-62). Each
+    configuration's block forward (7 linears and the block's elementwise ops)
+    is one GraphReplay graph; us per block at M = 256 and M = 1."""
+    from actune_amd.graph import GraphReplay
+    from actune_amd.layers import install_bank
+    from actune_amd.precision import CONFIGURATIONS, SharedBank, precision_profile
+    torch.manual_seed(8)
+
+    class Block(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            for name, (n, k) in GEMMA_BLOCK.items():
+                setattr(self, name, torch.nn.Linear(k, n, bias=False, dtype=torch.bfloat16, device="cuda"))
+
+        def forward(self, x):
+            q, _k, _v = self.q(x), self.k(x), self.v(x)
+            h = x + self.o(q)
+            return h + self.down(torch.nn.functional.silu(self.gate(h)) * self.up(h))
+
+    configs = {q: dict(GEMMA_FIXED, q=qm, gate=gm) for q, (qm, gm) in GEMMA_SWITCH.items()}
+    modes = [f"w{w}a{a}" for w in (2, 4, 8) for a in (2, 4, 8)]
+    sizes = {name: {md: n * k * int(md[1]) // 8 + 4 * n for md in modes} for name, (n, k) in GEMMA_BLOCK.items()}
+    out = {}
+    for m in (256, 1):
+        bank = SharedBank(configurations=configs, shapes={n: list(s_) for n, s_ in GEMMA_BLOCK.items()},
+                          activation_elements={n: m * s_[1] for n, s_ in GEMMA_BLOCK.items()},
+                          shape_groups=[["q", "k", "v", "o", "gate", "up"], ["down"]], version_bytes=sizes,
+                          budget="w4a4", storage_limit=1 << 30)
+        model = Block()
+        clips = {n: {md: None for md in {c[n] for c in configs.values()}} for n in GEMMA_BLOCK}
+        runtime = install_bank(model, bank, clips)
+        replay = GraphReplay(model, runtime.modules, shared_a8=True)
+        replay.enabled = True
+        x = torch.randn(m, 2048, device="cuda").to(torch.bfloat16)
+        row = {}
+        for q in CONFIGURATIONS:
+            with precision_profile(q):
+                for _ in range(warmup):
+                    replay(x)
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(steps):
+                    replay(x)
+                e1.record()
+                torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / steps
+            wbytes = sum(sizes[n][configs[q][n]] for n in GEMMA_BLOCK)
+            row[q] = dict(us_per_block=round(us, 2), weight_GBps=round(wbytes / us / 1e3, 1),
+                          TOPS=round(sum(2 * m * n * k for n, k in GEMMA_BLOCK.values()) / us / 1e6, 1),
+                          versions={n: configs[q][n] for n in ("q", "gate")})
+        out[f"M={m}"] = row
+        del model, runtime, replay
+    out["note"] = ("host-timed replays (events around the replay loop, one graph per configuration); "
+                   "k/v/o/up W4A2 and down W4A4 fixed, q and gate switch W4A4 <-> W4A8")
+    return out
+
+
 def bench_ceilings(torch):
     """Limits measured on this GPU that bound the two hot kernels:
     - graph_launch_floor_us: per-launch time of a hipGraph of tiny fill
@@ -581,8 +652,9 @@ def bench_expert(torch, steps):
     versions are all resident in HBM. One denoise step runs the 18 blocks on
     a 50-token chunk; 10 steps follow a seeded q00/q01/q11/q10 schedule, each
     step one GraphReplay replay of the active configuration's graph; inside
-    it linears that read the same x at the same activation width share one
-    quantizer launch."""
+    it linears that read the same tensor at the same activation width share
+    one quantizer launch (q/k/v on the block input, gate/up on the
+    post-attention residual)."""
     from actune_amd.graph import GraphReplay
     from actune_amd.layers import install_bank
     from actune_amd.precision import CONFIGURATIONS, SharedBank, precision_profile
@@ -596,10 +668,12 @@ def bench_expert(torch, steps):
 
         def forward(self, x):
             # k and v run (they are launched in the graph) but attention is
-            # not modelled: only the linears and the block's residual path
+            # not modelled: only the linears and the block's residual path;
+            # the MLP reads the post-attention residual h, as a real block's
+            # does, so only q/k/v (on x) and gate/up (on h) share inputs
             q, _k, _v = self.q(x), self.k(x), self.v(x)
             h = x + self.o(q * 0.5)
-            return h + self.down(torch.nn.functional.silu(self.gate(x)) * self.up(x))
+            return h + self.down(torch.nn.functional.silu(self.gate(h)) * self.up(h))
 
     class Expert(torch.nn.Module):
         def __init__(self):
@@ -806,6 +880,7 @@ def main():
     if not args.no_extra:
         line["detail"]["C3_prefill_M512"] = bench_prefill(torch, _native, 10, 3)
         line["detail"]["C4_gemma_W4A4"] = bench_gemma(torch, _native, 20, 5)
+        line["detail"]["C4_gemma_W4A4"]["bank"] = bench_gemma_bank(torch, 20, 3)
         line["detail"]["C5_expert_switching"] = bench_expert(torch, 20)
         line["detail"]["tokenwise_family"] = bench_tokenwise(torch, _native, 10, 3)
         line["detail"]["ceilings"] = bench_ceilings(torch)

@@ -499,3 +499,81 @@ def test_reuse_mlp_temporary_with_grouped_projections():
 def _run_profile(module, x, q):
     with precision_profile(q):
         return module(x).clone()
+
+
+# ---------------------------------------------------------------- C4: Gemma-2B-shaped W4A4 bank
+GEMMA = {"q": (2048, 2048), "k": (256, 2048), "v": (256, 2048), "o": (2048, 2048),
+         "gate": (16384, 2048), "up": (16384, 2048), "down": (2048, 16384)}
+# fixed versions, and the two binary switchable matrices (q, gate) that move
+# between W4A4 and W4A8; the A2 layers of the [M, 2048] shape group keep its
+# element-weighted activation bits at 4 when both run at A8
+GEMMA_FIXED = {"k": "w4a2", "v": "w4a2", "o": "w4a2", "up": "w4a2", "down": "w4a4"}
+GEMMA_SWITCH = {"q00": ("w4a4", "w4a4"), "q01": ("w4a4", "w4a8"), "q11": ("w4a8", "w4a8"),
+                "q10": ("w4a8", "w4a4")}
+
+
+class GemmaBlock(torch.nn.Module):
+    def __init__(self, seed=0):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        for name, (n, k) in GEMMA.items():
+            lin = torch.nn.Linear(k, n, bias=False, dtype=torch.bfloat16)
+            with torch.no_grad():
+                lin.weight.copy_((torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16))
+            setattr(self, name, lin.to(DEV))
+
+    def forward(self, x):
+        q, k, v = self.q(x), self.k(x), self.v(x)
+        h = x + self.o(q)
+        return h + self.down(torch.nn.functional.silu(self.gate(h)) * self.up(h)), k, v
+
+
+def gemma_bank():
+    configs = {q: dict(GEMMA_FIXED, q=qm, gate=gm) for q, (qm, gm) in GEMMA_SWITCH.items()}
+    modes = [f"w{w}a{a}" for w in (2, 4, 8) for a in (2, 4, 8)]
+    sizes = {name: {m: n * k * int(m[1]) // 8 + 4 * n for m in modes} for name, (n, k) in GEMMA.items()}
+    return SharedBank(configurations=configs, shapes={n: list(s) for n, s in GEMMA.items()},
+                      activation_elements={n: 256 * s[1] for n, s in GEMMA.items()},
+                      shape_groups=[["q", "k", "v", "o", "gate", "up"], ["down"]], version_bytes=sizes,
+                      budget="w4a4", storage_limit=1 << 30)
+
+
+@pytest.mark.parametrize("m", [256, 1])
+def test_gemma_2b_w4a4_bank_against_oracle(m):
+    """C4: a Gemma-2B-shaped block installed as a W4A4 shared bank whose two
+    binary switchable matrices (q, gate) run W4A8 in three of the four
+    configurations (balanced by A2 layers, precision.py:54-62). Under each
+    configuration every linear equals the oracle on 64 sampled columns, the
+    request passes the bank's audit, and a hipGraph replay equals eager."""
+    model = GemmaBlock(4)
+    bank = gemma_bank().validate()
+    clips = {n: {md: None for md in {c[n] for c in bank.configurations.values()}} for n in bank.shapes}
+    runtime = install_bank(model, bank, clips)
+    x = torch.randn(m, 2048, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    xd = x.to(DEV)
+    rng = np.random.default_rng(m)
+    replay = GraphReplay(model, runtime.modules)
+    replay.enabled = True
+    for q in CONFIGURATIONS:
+        runtime.before()
+        with precision_profile(q):
+            h_eager = model(xd)
+            for name, (n, k) in GEMMA.items():
+                layer = getattr(model, name)
+                backend = layer.active_backend()
+                assert f"w{backend.w}a{backend.a}" == bank.configurations[q][name]
+                inp = x if k == 2048 else torch.randn(m, k, generator=torch.Generator().manual_seed(n)).to(
+                    torch.bfloat16)
+                out = layer(inp.to(DEV))
+                cols = np.sort(rng.choice(n, size=min(64, n), replace=False))
+                wc = O.unpack_rows(backend.packed_weight[torch.from_numpy(cols).to(DEV)].cpu().numpy(), backend.w, k)
+                _, a_scales, a_codes = oracle_activation(inp, backend.a)
+                want = O.linear(a_codes, a_scales, wc, backend.weight_scale.cpu().numpy()[cols], None,
+                                bounds=canonical_bounds(k // 64))
+                np.testing.assert_array_equal(bits(out)[:, cols], O.round_out(want, "bf16"), err_msg=f"{q} {name}")
+            for _ in range(2):
+                h_graph = replay(xd)
+                torch.cuda.synchronize()
+                assert all(torch.equal(a, b) for a, b in zip(h_eager, h_graph)), q
+        metrics = bank.check_request(q, {n: m * GEMMA[n][1] for n in GEMMA})
+        assert metrics["weight_bits"] == 4 and max(metrics["group_activation_bits"]) <= 4

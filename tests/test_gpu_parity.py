@@ -165,6 +165,11 @@ def test_grouped_forward_matches_two_step_path():
     (1, 4096, 4096, 4, 8), (8, 11008, 4096, 4, 8), (1, 4096, 11008, 4, 8),
     (512, 4096, 4096, 8, 8), (512, 11008, 4096, 4, 8), (256, 2048, 2048, 4, 4),
     (50, 4096, 1024, 2, 4), (1, 256, 2048, 4, 4), (256, 2048, 16384, 4, 4),
+    # C4 (Gemma-2B) remainder: gate/up 16384x2048 at M = 256 and 1, q at M = 1,
+    # kv at M = 256, down at M = 1, and the bank's W4A8 / W4A2 versions
+    (256, 16384, 2048, 4, 4), (1, 16384, 2048, 4, 4), (1, 2048, 2048, 4, 4), (256, 256, 2048, 4, 4),
+    (1, 2048, 16384, 4, 4), (256, 16384, 2048, 4, 8), (1, 16384, 2048, 4, 8), (256, 2048, 2048, 4, 8),
+    (256, 256, 2048, 4, 2), (1, 256, 2048, 4, 2),
 ])
 def test_full_size_sampled_parity(m, n, k, W, A):
     """BASELINE shapes: every output row against the oracle on 64 sampled
@@ -269,6 +274,31 @@ def test_multi_target_equals_separate_calls(m, W, A):
     outs = _native.grouped_forward_multi(xd, targets, W, A)
     for (w_dev, ws_dev, bd, _), out in zip(targets, outs):
         assert torch.equal(out, _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A))
+
+
+@pytest.mark.parametrize("m", [1, 8])
+@pytest.mark.parametrize("n,k,count", [(4096, 4096, 3), (11008, 4096, 2)])
+def test_full_size_sibling_launches_against_oracle(m, n, k, count):
+    """The sibling launches the C2 benchmark times (q/k/v 3 x 4096x4096 and
+    gate/up 2 x 11008x4096, W4A8, default config, M = 1 and 8): each target
+    against the oracle on 64 sampled columns, bit-exact in the canonical
+    order, and equal to its own single-target forward."""
+    W, A = 4, 8
+    x, _, _ = seeded_inputs(m, k, 1, seed=n + m)
+    xd = x.to(DEV)
+    _, a_scales, a_codes = oracle_activation(x, A)
+    targets, oracle_side = [], []
+    for j in range(count):
+        _, w, _ = seeded_inputs(1, k, n, seed=7000 + 10 * j + m)
+        codes, scale, w_dev, ws_dev = _packed_weight(w, W, A)
+        targets.append((w_dev, ws_dev, None, None))
+        oracle_side.append((codes, scale))
+    outs = _native.grouped_forward_multi(xd, targets, W, A)
+    cols = np.sort(np.random.default_rng(n + m).choice(n, size=64, replace=False))
+    for (w_dev, ws_dev, _, _), (codes, scale), out in zip(targets, oracle_side, outs):
+        want = O.linear(a_codes, a_scales, codes, scale, None, bounds=canonical_bounds(k // 64), cols=cols)
+        np.testing.assert_array_equal(bits(out)[:, cols], O.round_out(want, "bf16"))
+        assert torch.equal(out, _native.grouped_forward(xd, w_dev, ws_dev, None, W, A))
 
 
 @pytest.mark.parametrize("W,A", PAIRS)
