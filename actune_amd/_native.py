@@ -167,6 +167,15 @@ def _check_flat(flat):
     _dtype_code(flat)
 
 
+def _aligned16(t):
+    """t itself when its data is 16-byte aligned (the kernels read rows with
+    16-byte loads), else an aligned copy: a contiguous view at an odd offset
+    (x[:, 1:].reshape(...) style) computes as the reference does."""
+    if t is None or t.data_ptr() % 16 == 0:
+        return t
+    return t.clone()
+
+
 def version() -> str:
     return lib().actune_version().decode()
 
@@ -225,6 +234,7 @@ def quantize_groups(x: torch.Tensor, a: int, input_scale: torch.Tensor | None = 
     _check_flat(x)
     m, k = x.shape
     _check_input_scale(input_scale, x)
+    x, input_scale = _aligned16(x), _aligned16(input_scale)
     packed, scales = _act_buffers(packed, scales, m, k, a, x.device)
     _check(lib().actune_quantize_groups(_ptr(x), _dtype_code(x), _ptr(input_scale), m, k, a,
                                         _ptr(packed), _ptr(scales), _stream(x.device)))
@@ -291,6 +301,7 @@ def grouped_forward(flat, w, ws, bias, W, A, input_scale=None, config=CONFIG_AUT
     m, k = flat.shape
     n = _check_weights(w, ws, bias, k, W)
     _check_input_scale(input_scale, flat)
+    flat, input_scale = _aligned16(flat), _aligned16(input_scale)
     packed, scales = _act_buffers(packed, scales, m, k, A, flat.device)
     if out is None:
         out = torch.empty((m, n), device=flat.device, dtype=flat.dtype)
@@ -314,6 +325,7 @@ def grouped_forward_multi(flat, targets, W, A, input_scale=None, config=CONFIG_A
     _check_flat(flat)
     m, k = flat.shape
     _check_input_scale(input_scale, flat)
+    flat, input_scale = _aligned16(flat), _aligned16(input_scale)
     biases = [t[2] for t in targets]
     if len({(b.dtype if b is not None else None) for b in biases}) != 1:
         raise ValueError("all targets must share one bias dtype (or none)")
@@ -371,6 +383,7 @@ def tokenwise_quantize(x, bits, codes=None, scales=None):
     _check_flat(x)
     if bits not in (8, 4):
         raise ValueError("tokenwise activations are A8 or A4")
+    x = _aligned16(x)
     m, k = x.shape
     if codes is None:
         codes = torch.empty((m, k) if bits == 8 else (m, k // 2), device=x.device,
@@ -415,6 +428,7 @@ def tokenwise_linear_x(x, as_out, w, w_layout, ws, bias, n, k, epilogue, out, wo
     if not (x.is_contiguous() and w.is_contiguous() and ws.is_contiguous()
             and (bias is None or bias.is_contiguous())):
         raise RuntimeError("contiguous operands required")
+    x = _aligned16(x)
     if as_out.dtype != torch.float32 or ws.dtype != torch.float32:
         raise RuntimeError("float scales/bias required")
     if as_out.numel() != m or not as_out.is_contiguous() or ws.numel() != n or (bias is not None and bias.numel() != n):
@@ -486,6 +500,7 @@ def tokenwise_linear_multi(targets, w_layout, n, k, epilogue, scales, *, codes=N
         if x.dim() != 2 or not 1 <= x.shape[0] <= 8 or x.shape[1] != k or not x.is_contiguous():
             raise RuntimeError("fused quantization takes contiguous x of shape [M, K] with M <= 8")
         _dtype_code(x)
+        x = act = _aligned16(x)
     else:
         abytes = k if a_layout == TW_ACT_A8 else k // 2
         if codes.dim() != 2 or codes.shape[1] != abytes or codes.element_size() != 1 or not codes.is_contiguous():
@@ -518,3 +533,4 @@ def tokenwise_linear_multi(targets, w_layout, n, k, epilogue, scales, *, codes=N
         len(targets), _bias_code(bias0), _dtype_code(targets[0][3]), m, n, k, epilogue,
         _ptr(workspace) if need else None, need, _stream(act.device)))
     return [t[3] for t in targets]
+

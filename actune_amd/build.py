@@ -47,12 +47,25 @@ def flags() -> list[str]:
     ]
 
 
+def _includes(path: Path, seen: set) -> None:
+    """Adds path and every local header it includes (transitively) to seen."""
+    if path in seen or not path.exists():
+        return
+    seen.add(path)
+    for line in path.read_text().splitlines():
+        line = line.strip()
+        if line.startswith("#include \""):
+            _includes((path.parent / line.split('"')[1]).resolve(), seen)
+
+
 def _stale(src: str, out: Path) -> bool:
-    """True when `out` is missing or older than the source or any header."""
+    """True when `out` is missing or older than the source, a header it
+    includes, or this build script."""
     if not out.exists():
         return True
-    deps = [CSRC / src, *CSRC.glob("*.hpp"), PKG.parent / "include" / "actune_hip.h", Path(__file__)]
-    return any(d.exists() and d.stat().st_mtime > out.stat().st_mtime for d in deps)
+    deps = {Path(__file__)}
+    _includes((CSRC / src).resolve(), deps)
+    return any(d.stat().st_mtime > out.stat().st_mtime for d in deps)
 
 
 def _compile(src: str, incremental: bool = False) -> Path:

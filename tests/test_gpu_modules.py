@@ -134,6 +134,31 @@ def test_install_bank_on_cuda_model_uses_gpu_codes():
             np.testing.assert_array_equal(backend.weight_scale.cpu().numpy(), s, err_msg=mode)
 
 
+def test_offset_views_compute_like_aligned_inputs():
+    """A contiguous view at a 2-byte offset (x[:, 1:] of a [1, K + 1]
+    tensor) is not 16-byte aligned: the group-64 and tokenwise modules copy
+    it and compute what they compute for the same values aligned, as the
+    reference's forward (grouped.py:129, .contiguous() keeps the view)
+    computes any contiguous input."""
+    from actune_amd.kernels import tokenwise as T
+    k, n = 512, 64
+    lin = _linear(k, n, False, seed=77)
+    base = torch.randn(1, k + 1, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(DEV)
+    view = base[:, 1:]
+    assert view.is_contiguous() and view.data_ptr() % 16 != 0
+    aligned = view.clone()
+    for W, A in ((4, 8), (2, 4), (8, 2)):
+        mod = GroupedLinear(lin, W, A, None).to(DEV)
+        assert torch.equal(mod(view), mod(aligned))
+    scale = torch.linspace(0.5, 2.0, k + 1).to(torch.bfloat16).to(DEV)[1:]
+    r = ResidentLinear(lin, {q: "w4a8" for q in CONFIGURATIONS}, {"w4a8": None}, scale.cpu().clone()).to(DEV)
+    assert torch.equal(r(view), r(aligned))
+    tw = T.W4A8TritonLinear(lin.to(DEV))
+    with T.decode_optimization_scope(enabled=False):
+        assert torch.equal(tw(view), tw(aligned))
+    assert torch.equal(tw(view), tw(aligned))  # the decode graph plan copies the row in
+
+
 def test_grouped_linear_rejects_host_input():
     mod = GroupedLinear(_linear(64, 16, False, 1), 4, 8, None).to(DEV)
     with pytest.raises(ValueError, match="requires CUDA"):
