@@ -34,7 +34,7 @@ class _Target(ctypes.Structure):
 
 class _TwTarget(ctypes.Structure):
     """actune_tw_target"""
-    _fields_ = [("w", _P), ("w_scale", _P), ("bias", _P), ("out", _P)]
+    _fields_ = [("w", _P), ("r", _P), ("w_scale", _P), ("bias", _P), ("out", _P)]
 
 
 def lib():
@@ -371,7 +371,7 @@ def extension() -> Extension:
 
 
 # ---------------------------------------------------------------- tokenwise family
-TW_KMAJOR_W8, TW_KMAJOR_W4, TW_KMAJOR_W2, TW_ROWS_S4, TW_ROWS_S2 = 0, 1, 2, 3, 4
+TW_KMAJOR_W8, TW_KMAJOR_W4, TW_KMAJOR_W2, TW_ROWS_S4, TW_ROWS_S2, TW_KMAJOR_W4R4 = 0, 1, 2, 3, 4, 5
 TW_ACT_A8, TW_ACT_A4 = 0, 1
 TW_EPI_A8, TW_EPI_A4 = 0, 1
 
@@ -433,7 +433,8 @@ def tokenwise_linear_x(x, as_out, w, w_layout, ws, bias, n, k, epilogue, out, wo
         raise RuntimeError("float scales/bias required")
     if as_out.numel() != m or not as_out.is_contiguous() or ws.numel() != n or (bias is not None and bias.numel() != n):
         raise RuntimeError("scale shape mismatch")
-    wbytes = {TW_KMAJOR_W8: k * n, TW_KMAJOR_W4: k // 2 * n, TW_KMAJOR_W2: k // 4 * n}.get(w_layout)
+    wbytes = {TW_KMAJOR_W8: k * n, TW_KMAJOR_W4: k // 2 * n, TW_KMAJOR_W2: k // 4 * n,
+              TW_KMAJOR_W4R4: k // 2 * n}.get(w_layout)
     if wbytes is None:
         raise RuntimeError("fused quantization takes the K-major (A8) weight layouts")
     if w.numel() != wbytes or w.element_size() != 1:
@@ -466,7 +467,7 @@ def tokenwise_linear(a, a_layout, as_, w, w_layout, ws, bias, n, k, epilogue, ou
     if a.dim() != 2 or a.shape[1] != abytes or a.element_size() != 1:
         raise RuntimeError("packed activation shape mismatch")
     wbytes = {TW_KMAJOR_W8: k * n, TW_KMAJOR_W4: k // 2 * n, TW_KMAJOR_W2: k // 4 * n,
-              TW_ROWS_S4: n * k // 2, TW_ROWS_S2: n * k // 4}[w_layout]
+              TW_ROWS_S4: n * k // 2, TW_ROWS_S2: n * k // 4, TW_KMAJOR_W4R4: k // 2 * n}[w_layout]
     if w.numel() != wbytes or w.element_size() != 1:
         raise RuntimeError("packed weight shape mismatch")
     _check_buffer(out, "out", (m, n), out.dtype, a.device)
@@ -480,21 +481,32 @@ def tokenwise_linear(a, a_layout, as_, w, w_layout, ws, bias, n, k, epilogue, ou
 
 
 def tokenwise_linear_multi(targets, w_layout, n, k, epilogue, scales, *, codes=None, a_layout=TW_ACT_A8, x=None,
-                           workspace=None):
+                           workspace=None, residuals=None):
     """1 to MAX_TARGETS sibling projections on the same rows in one GEMM
     launch (and one reduce when K is split): actune_tokenwise_linear_multi.
     targets: [(w, ws, bias, out)] sharing n, k and w_layout, out [M, N]
     preallocated; each bias may be None, those present share one dtype.
     Pass either codes (in a_layout; scales [M] read) or x (rows [M, K]
     quantized to A8 in the launch; scales [M] written).
+    residuals: with TW_KMAJOR_W4R4 only, one entry per target, each a u8
+    [K/2, N] residual in the KMAJOR_W4 packing or None (that target reads
+    r4 = 0, its result equals TW_KMAJOR_W4's).
     workspace: u8 tensor of at least len(targets) x tokenwise_workspace_bytes()
     bytes (None when that is 0). Each output equals the single-target call."""
     if (codes is None) == (x is None):
         raise ValueError("pass either codes or x")
     if not 1 <= len(targets) <= MAX_TARGETS:
         raise ValueError(f"1 to {MAX_TARGETS} targets")
+    if w_layout == TW_KMAJOR_W4R4:
+        residuals = [None] * len(targets) if residuals is None else list(residuals)
+        if len(residuals) != len(targets):
+            raise ValueError("one residual (or None) per target")
+    elif residuals is not None and any(r is not None for r in residuals):
+        raise ValueError("residuals go with the TW_KMAJOR_W4R4 layout only")
+    else:
+        residuals = [None] * len(targets)
     act = codes if codes is not None else x
-    _require_cuda(act, scales, workspace, *[t for tgt in targets for t in tgt])
+    _require_cuda(act, scales, workspace, *[t for tgt in targets for t in tgt], *residuals)
     if x is not None:
         a_layout = TW_ACT_A8
         if x.dim() != 2 or not 1 <= x.shape[0] <= 8 or x.shape[1] != k or not x.is_contiguous():
@@ -509,12 +521,16 @@ def tokenwise_linear_multi(targets, w_layout, n, k, epilogue, scales, *, codes=N
     if scales.dtype != torch.float32 or scales.numel() != m or not scales.is_contiguous():
         raise RuntimeError("scale shape mismatch")
     wbytes = {TW_KMAJOR_W8: k * n, TW_KMAJOR_W4: k // 2 * n, TW_KMAJOR_W2: k // 4 * n,
-              TW_ROWS_S4: n * k // 2, TW_ROWS_S2: n * k // 4}[w_layout]
+              TW_ROWS_S4: n * k // 2, TW_ROWS_S2: n * k // 4, TW_KMAJOR_W4R4: k // 2 * n}[w_layout]
     out_dtype = targets[0][3].dtype
     present = [t[2] for t in targets if t[2] is not None]
     bias0 = present[0] if present else None
     structs = (_TwTarget * len(targets))()
-    for i, (w, ws, bias, out) in enumerate(targets):
+    for r in residuals:
+        if r is not None and (not r.is_contiguous() or r.numel() != wbytes or r.element_size() != 1):
+            raise RuntimeError("packed residual shape mismatch (contiguous u8 [K/2, N] required)")
+    residuals = [_aligned16(r) for r in residuals]  # held until the launch is issued
+    for i, ((w, ws, bias, out), r) in enumerate(zip(targets, residuals)):
         if not (w.is_contiguous() and ws.is_contiguous() and (bias is None or bias.is_contiguous())):
             raise RuntimeError("contiguous operands required")
         if w.numel() != wbytes or w.element_size() != 1:
@@ -524,7 +540,8 @@ def tokenwise_linear_multi(targets, w_layout, n, k, epilogue, scales, *, codes=N
         if bias is not None and bias.dtype != bias0.dtype:
             raise RuntimeError("the sibling biases present must share one dtype")
         _check_buffer(out, "out", (m, n), out_dtype, act.device)
-        structs[i] = _TwTarget(w.data_ptr(), ws.data_ptr(), None if bias is None else bias.data_ptr(), out.data_ptr())
+        structs[i] = _TwTarget(w.data_ptr(), None if r is None else r.data_ptr(), ws.data_ptr(),
+                               None if bias is None else bias.data_ptr(), out.data_ptr())
     need = len(targets) * tokenwise_workspace_bytes(m, n, k, w_layout, a_layout)
     if need and (workspace is None or workspace.numel() < need or workspace.dtype != torch.uint8):
         raise RuntimeError(f"workspace of at least {need} bytes required")

@@ -87,6 +87,14 @@ template <> struct WTraits<ACTUNE_TW_KMAJOR_W2> {
   static constexpr int rows(int) { return 32; }
   static constexpr int row_bytes(int tn) { return tn; }
 };
+// nibble-pair q4 rows (staged rows 0-31) and the residual r4 rows of the
+// same K (staged rows 32-63); codes formed as int8 16 q4 + r4
+template <> struct WTraits<ACTUNE_TW_KMAJOR_W4R4> {
+  static constexpr int U = 1, TW = 0;
+  static constexpr bool KM = true;
+  static constexpr int rows(int) { return 64; }
+  static constexpr int row_bytes(int tn) { return tn; }
+};
 template <> struct WTraits<ACTUNE_TW_ROWS_S4> {
   static constexpr int U = 1, TW = 4;
   static constexpr bool KM = false;
@@ -102,8 +110,11 @@ template <> struct WTraits<ACTUNE_TW_ROWS_S2> {
 
 // Padded LDS row strides: the transposed reads of 8 weight rows and the
 // 16-row activation reads each touch distinct banks.
+constexpr bool kmajor(int wl) { return wl <= ACTUNE_TW_KMAJOR_W2 || wl == ACTUNE_TW_KMAJOR_W4R4; }
+// nibble-pair layouts: a buffer row holds codes j and j + K/2
+constexpr bool nibble_pairs(int wl) { return wl == ACTUNE_TW_KMAJOR_W4 || wl == ACTUNE_TW_KMAJOR_W4R4; }
 constexpr int w_stride(int wl, int tn) {
-  return wl <= ACTUNE_TW_KMAJOR_W2 ? tn + 16 : (wl == ACTUNE_TW_ROWS_S4 ? 40 : 20);
+  return kmajor(wl) ? tn + 16 : (wl == ACTUNE_TW_ROWS_S4 ? 40 : 20);
 }
 // activation bytes per staged row and K-step: int8 codes 64 per MFMA (the
 // nibble-pair layout stages k = j.. and K/2 + j.. as two 32-byte pieces, the
@@ -115,6 +126,7 @@ constexpr int a_stride(int wl, int al) { return al == ACTUNE_TW_ACT_A4 ? 40 : a_
 // rows, K, N and layouts); target 0 is also held in TwArgs' own fields.
 struct TwTarget {
   const uint8_t* w;
+  const uint8_t* r;
   const float* ws;
   const void* bias;
   void* out;
@@ -129,6 +141,8 @@ struct TwArgs {
   const void* bias;     // [N] or nullptr
   void* out;            // [M, N]
   int32_t* partial;     // [T, S, M, N] int32 raw (shifted) partial sums (S > 1)
+  const uint8_t* r;     // KMAJOR_W4R4: residual codes (nullptr: r4 = 0)
+  float ws_mul;         // 1, or 1/16 for the nested 16 q4 + r4 codes (exact)
   int M, N, K, bias_dt, out_dt, splits, steps;
   int targets;          // T: grid z = S x T (GEMM), T (reduce)
   TwTarget t[ACTUNE_MAX_TARGETS];
@@ -140,6 +154,7 @@ __device__ __forceinline__ TwArgs for_target(const TwArgs& in, int i) {
   TwArgs a = in;
   if (i > 0) {
     a.w = in.t[i].w;
+    a.r = in.t[i].r;
     a.ws = in.t[i].ws;
     a.bias = in.t[i].bias;
     a.out = in.t[i].out;
@@ -153,7 +168,7 @@ __device__ __forceinline__ TwArgs for_target(const TwArgs& in, int i) {
 template <int EPI>
 __device__ __forceinline__ void store_result(const TwArgs& a, int m, int n, int32_t acc) {
   const float x = (float)acc;
-  const float as = a.as[m], ws = a.ws[n];
+  const float as = a.as[m], ws = a.ws[n] * a.ws_mul;
   float y;
   if constexpr (EPI == ACTUNE_TW_EPI_A8) {
     const float t = x * as;
@@ -202,6 +217,17 @@ __device__ __forceinline__ void finish_tile(const TwArgs& args, const v4i (&acc)
         if (m < M) store_result<EPI>(args, m, n, acc[mt][nt][i] >> SHIFT);
       }
   }
+}
+
+// Bytes of 16 q4 + r4 as int8, wrapped to 8 bits (decode_w4a8_triton.py:61-66
+// forms the same value in int16 and casts it to int8), for the four nibble
+// pairs in the low nibbles of q and r: the high nibble is q4 - [r4 < 0]
+// (mod 16), the low nibble is r4's own. No carry crosses a byte (each sum is
+// at most 30).
+__device__ __forceinline__ uint32_t nested_r4(uint32_t q, uint32_t r) {
+  const uint32_t qn = q & 0x0F0F0F0Fu, rn = r & 0x0F0F0F0Fu;
+  const uint32_t neg = (rn >> 3) & 0x01010101u;
+  return (((qn + neg * 15u) & 0x0F0F0F0Fu) << 4) | rn;
 }
 
 __device__ __forceinline__ v2u tr8(const uint8_t* p) {
@@ -277,12 +303,16 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args_in) {
   // buffer resources: reads past the end return zeros
   uint32_t wbytes;
   if constexpr (WL == ACTUNE_TW_KMAJOR_W8) wbytes = (uint32_t)K * N;
-  else if constexpr (WL == ACTUNE_TW_KMAJOR_W4) wbytes = (uint32_t)(K / 2) * N;
+  else if constexpr (nibble_pairs(WL)) wbytes = (uint32_t)(K / 2) * N;
   else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) wbytes = (uint32_t)(K / 4) * N;
   else if constexpr (WL == ACTUNE_TW_ROWS_S4) wbytes = (uint32_t)N * (K / 2);
   else wbytes = (uint32_t)N * (K / 4);
   const uint32_t arow = AL == ACTUNE_TW_ACT_A4 ? (uint32_t)K / 2 : (uint32_t)K;
   const Rsrc wr = make_rsrc(args.w, wbytes);
+  // the residual rows of W4R4 (a target without one reads zeros)
+  const Rsrc rr = make_rsrc(args.r, args.r ? wbytes : 0u);
+  constexpr bool R4 = WL == ACTUNE_TW_KMAJOR_W4R4;
+  static_assert(!R4 || WCH == 2 * kThreads, "W4R4: load batch 0 holds the q4 rows, batch 1 the r4 rows");
   const Rsrc ar = FX ? make_rsrc(args.x, (uint32_t)M * K * XSZ) : make_rsrc(args.a, (uint32_t)M * arow);
 
   // Per-thread base offsets of its weight / activation chunks (step 0) and
@@ -296,28 +326,29 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args_in) {
     bool live = c < WCH;
     if constexpr (T::KM) {
       live = live && n0 + 16 * cb < N;
-      wbase[i] = live ? (uint32_t)row * (uint32_t)N + (uint32_t)(n0 + 16 * cb) : kOff;
+      // W4R4: staged rows 32-63 are rows 0-31 of the residual buffer
+      wbase[i] = live ? (uint32_t)(R4 ? row % 32 : row) * (uint32_t)N + (uint32_t)(n0 + 16 * cb) : kOff;
     } else {
       live = live && n0 + row < N;
       wbase[i] = live ? (uint32_t)(n0 + row) * (uint32_t)(WL == ACTUNE_TW_ROWS_S4 ? K / 2 : K / 4) + (uint32_t)(16 * cb)
                       : kOff;
     }
   }
-  const uint32_t wstep = T::KM ? (uint32_t)WROWS * (uint32_t)N : (uint32_t)WRB;
+  const uint32_t wstep = T::KM ? (uint32_t)(R4 ? WROWS / 2 : WROWS) * (uint32_t)N : (uint32_t)WRB;
 #pragma unroll
   for (int i = 0; i < NAC; ++i) {
     const int c = tid + i * kThreads, row = c / (ARB / 16), cb = c % (ARB / 16);
     const bool live = c < ACH && m0 + row < M;
     uint32_t k;
     if constexpr (AL == ACTUNE_TW_ACT_A4) k = 16 * cb;                                   // packed row bytes
-    else if constexpr (WL == ACTUNE_TW_KMAJOR_W4) k = (uint32_t)(cb >> 1) * (K / 2) + 16 * (cb & 1);
+    else if constexpr (nibble_pairs(WL)) k = (uint32_t)(cb >> 1) * (K / 2) + 16 * (cb & 1);
     else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) k = (uint32_t)(cb >> 1) * (K / 4) + 16 * (cb & 1);
     else k = 16 * cb;
     // fused: byte offset of element k of the row (row 0 only)
     if constexpr (FX) abase[i] = live && row == 0 ? k * XSZ : kOff;
     else abase[i] = live ? (uint32_t)(m0 + row) * arow + k : kOff;
   }
-  constexpr uint32_t astep = (AL == ACTUNE_TW_ACT_A4 || WL == ACTUNE_TW_KMAJOR_W4 || WL == ACTUNE_TW_KMAJOR_W2) ? 32 : 64;
+  constexpr uint32_t astep = (AL == ACTUNE_TW_ACT_A4 || nibble_pairs(WL) || WL == ACTUNE_TW_KMAJOR_W2) ? 32 : 64;
 
   // loads of step g; a step outside [g0, g1) is switched off through the
   // scalar offset (reads zeros)
@@ -325,7 +356,8 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args_in) {
     const uint32_t soff = g < g1 ? 0u : kOff;
 #pragma unroll
     for (int i = 0; i < NWC; ++i)
-      wreg[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, wbase[i] == kOff ? kOff : wbase[i] + (uint32_t)g * wstep, soff, 0);
+      wreg[i] = __builtin_amdgcn_raw_buffer_load_b128(R4 && i >= NWC / 2 ? rr : wr,
+                                                      wbase[i] == kOff ? kOff : wbase[i] + (uint32_t)g * wstep, soff, 0);
 #pragma unroll
     for (int i = 0; i < NAC; ++i)
       areg[i] = __builtin_amdgcn_raw_buffer_load_b128(ar, abase[i] == kOff ? kOff : abase[i] + (uint32_t)g * astep, soff, 0);
@@ -377,6 +409,11 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args_in) {
           const v2u b = tr8(wt + (8 * kb + tr_row) * WSTR + cn + 8 * tr_half);
           bf[nt][0] = (b[0] << 4) & 0xF0F0F0F0u; bf[nt][1] = (b[1] << 4) & 0xF0F0F0F0u;
           bf[nt][2] = b[0] & 0xF0F0F0F0u;        bf[nt][3] = b[1] & 0xF0F0F0F0u;
+        } else if constexpr (R4) {
+          const v2u q = tr8(wt + (8 * kb + tr_row) * WSTR + cn + 8 * tr_half);
+          const v2u r = tr8(wt + (32 + 8 * kb + tr_row) * WSTR + cn + 8 * tr_half);
+          bf[nt][0] = nested_r4(q[0], r[0]); bf[nt][1] = nested_r4(q[1], r[1]);
+          bf[nt][2] = nested_r4(q[0] >> 4, r[0] >> 4); bf[nt][3] = nested_r4(q[1] >> 4, r[1] >> 4);
         } else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) {
           const v2u b = tr8(wt + (8 * kb + tr_row) * WSTR + cn + 8 * tr_half);
           // fields 2u (k = j + 2u K/4) and 2u + 1 (k = j + (2u+1) K/4)
@@ -404,7 +441,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args_in) {
           unpack_slot<4>(pp, af);
           if constexpr (WL == ACTUNE_TW_ROWS_S2) reorder_slot<4, 2>(af);
           else if constexpr (T::KM) reorder_slot<4, 8>(af);
-        } else if constexpr (WL == ACTUNE_TW_KMAJOR_W4 || WL == ACTUNE_TW_KMAJOR_W2) {
+        } else if constexpr (nibble_pairs(WL) || WL == ACTUNE_TW_KMAJOR_W2) {
           const v2u lo = *reinterpret_cast<const v2u*>(arow_l + 64 * u + 8 * kb);
           const v2u hi = *reinterpret_cast<const v2u*>(arow_l + 64 * u + 32 + 8 * kb);
           af[0] = lo[0]; af[1] = lo[1]; af[2] = hi[0]; af[3] = hi[1];
@@ -443,7 +480,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args_in) {
     static_assert(EPT == 1 || EPT == 2 || EPT == 4, "fused slice: 1, 2 or 4 elements per thread");
     const int fi = tid * EPT / ARB, fb = tid * EPT % ARB, fc = fb / 16;
     uint32_t kx;
-    if constexpr (WL == ACTUNE_TW_KMAJOR_W4) kx = (uint32_t)(fc >> 1) * (K / 2) + 16 * (fc & 1);
+    if constexpr (nibble_pairs(WL)) kx = (uint32_t)(fc >> 1) * (K / 2) + 16 * (fc & 1);
     else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) kx = (uint32_t)(fc >> 1) * (K / 4) + 16 * (fc & 1);
     else kx = 16 * fc;
     kx += (uint32_t)(fb % 16) + (uint32_t)(g0 + fi) * astep;
@@ -467,7 +504,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args_in) {
 #pragma unroll
       for (int c = 0; c < NWC; ++c)
         wreg[i][c] = __builtin_amdgcn_raw_buffer_load_b128(
-            wr, wbase[c] == kOff ? kOff : wbase[c] + (uint32_t)(g0 + i) * wstep, soff, 0);
+            R4 && c >= NWC / 2 ? rr : wr, wbase[c] == kOff ? kOff : wbase[c] + (uint32_t)(g0 + i) * wstep, soff, 0);
     }
     float amax = 0.0f;
 #pragma unroll
@@ -530,7 +567,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args_in) {
     static_assert(EPT == 1 || EPT == 2 || EPT == 4, "fused slice: 1, 2 or 4 elements per thread");
     const int fi = tid * EPT / ARB, fb = tid * EPT % ARB, fc = fb / 16;
     uint32_t kx;
-    if constexpr (WL == ACTUNE_TW_KMAJOR_W4) kx = (uint32_t)(fc >> 1) * (K / 2) + 16 * (fc & 1);
+    if constexpr (nibble_pairs(WL)) kx = (uint32_t)(fc >> 1) * (K / 2) + 16 * (fc & 1);
     else if constexpr (WL == ACTUNE_TW_KMAJOR_W2) kx = (uint32_t)(fc >> 1) * (K / 4) + 16 * (fc & 1);
     else kx = 16 * fc;
     kx += (uint32_t)(fb % 16) + (uint32_t)(g0 + fi) * astep;
@@ -572,7 +609,7 @@ __global__ __launch_bounds__(kThreads) void tw_gemm(const TwArgs args_in) {
 #pragma unroll
       for (int c = 0; c < NWC; ++c)
         wreg[i][c] = __builtin_amdgcn_raw_buffer_load_b128(
-            wr, wbase[c] == kOff ? kOff : wbase[c] + (uint32_t)(g0 + i) * wstep, soff, 0);
+            R4 && c >= NWC / 2 ? rr : wr, wbase[c] == kOff ? kOff : wbase[c] + (uint32_t)(g0 + i) * wstep, soff, 0);
     }
     float amax = 0.0f;
 #pragma unroll
@@ -1071,7 +1108,7 @@ int kps_of(int wl) { return wl == ACTUNE_TW_KMAJOR_W2 ? 128 : 64; }
 int64_t steps_of(int64_t K, int wl) { return (K + kps_of(wl) - 1) / kps_of(wl); }
 // K-steps a small-M workgroup loads at entry: the int8 K-major tile is twice
 // the others, so it keeps half as many steps to stay inside the LDS
-int small_ns(int wl) { return wl == ACTUNE_TW_KMAJOR_W8 ? 4 : 8; }
+int small_ns(int wl) { return wl == ACTUNE_TW_KMAJOR_W8 || wl == ACTUNE_TW_KMAJOR_W4R4 ? 4 : 8; }
 int64_t tiles_of(int64_t M, int64_t N, const Geometry& g) {
   return ((N + g.tn() - 1) / g.tn()) * ((M + g.tm() - 1) / g.tm());
 }
@@ -1087,7 +1124,7 @@ int64_t tiles_of(int64_t M, int64_t N, const Geometry& g) {
 // / S2 (W4A8 4096x11008: 57.7 -> 51.2 us, W4A4 4096x4096: 30.4 -> 20.3 us).
 Geometry pick_geometry(int64_t M, int64_t N, int wl) {
   if (M <= 32) return Geometry{1, 1, 2, small_ns(wl), 0, 0};
-  const bool km = wl <= ACTUNE_TW_KMAJOR_W2;
+  const bool km = kmajor(wl);
   const Geometry big{2, 2, 4, 0, km ? 1 : 2, 3};
   if (tiles_of(M, N, big) >= 512) return big;
   return km ? Geometry{2, 2, 4, 0, 2, 4} : Geometry{2, 2, 2, 0, 2, 4};
@@ -1174,17 +1211,21 @@ void launch_ring_t(const TwArgs& a, hipStream_t st) {
 template <int WL, int AL, int EPI>
 void launch_gemm_g(const TwArgs& a, const Geometry& g, hipStream_t st) {
   constexpr bool KM = WTraits<WL>::KM;
-  if (g.wm == 1) launch_gemm_t<WL, AL, EPI, 1, 1, 2, (WL == ACTUNE_TW_KMAJOR_W8 ? 4 : 8)>(a, st);
-  else if (g.d == 3) launch_ring_t<WL, AL, EPI, 2, 2, 4, KM ? 1 : 2, 3>(a, st);
-  else if constexpr (KM) launch_ring_t<WL, AL, EPI, 2, 2, 4, 2, 4>(a, st);
-  else launch_ring_t<WL, AL, EPI, 2, 2, 2, 2, 4>(a, st);
+  if constexpr (WL == ACTUNE_TW_KMAJOR_W4R4) {  // small M only (the entry point checks M <= 32)
+    launch_gemm_t<WL, AL, EPI, 1, 1, 2, 4>(a, st);
+  } else {
+    if (g.wm == 1) launch_gemm_t<WL, AL, EPI, 1, 1, 2, (WL == ACTUNE_TW_KMAJOR_W8 ? 4 : 8)>(a, st);
+    else if (g.d == 3) launch_ring_t<WL, AL, EPI, 2, 2, 4, KM ? 1 : 2, 3>(a, st);
+    else if constexpr (KM) launch_ring_t<WL, AL, EPI, 2, 2, 4, 2, 4>(a, st);
+    else launch_ring_t<WL, AL, EPI, 2, 2, 2, 2, 4>(a, st);
+  }
 }
 
 // A8 rows quantized inside the GEMM launch (small-M geometry, 16 x 128 tiles):
 // one row, or two to eight rows of 16-bit x
 template <int WL, int EPI, int XDT>
 void launch_fused_t(const TwArgs& a, hipStream_t st) {
-  constexpr int NB = WL == ACTUNE_TW_KMAJOR_W8 ? 4 : 8;
+  constexpr int NB = WL == ACTUNE_TW_KMAJOR_W8 || WL == ACTUNE_TW_KMAJOR_W4R4 ? 4 : 8;
   if constexpr (XDT == kF32) {
     launch_gemm_t<WL, ACTUNE_TW_ACT_A8, EPI, 1, 1, 2, NB, XDT>(a, st);
   } else {
@@ -1204,12 +1245,13 @@ void launch_fused(int wl, int epi, int xdt, const TwArgs& a, hipStream_t st) {
   TWF(ACTUNE_TW_KMAJOR_W8, ACTUNE_TW_EPI_A8) TWF(ACTUNE_TW_KMAJOR_W8, ACTUNE_TW_EPI_A4)
   TWF(ACTUNE_TW_KMAJOR_W4, ACTUNE_TW_EPI_A8) TWF(ACTUNE_TW_KMAJOR_W4, ACTUNE_TW_EPI_A4)
   TWF(ACTUNE_TW_KMAJOR_W2, ACTUNE_TW_EPI_A8) TWF(ACTUNE_TW_KMAJOR_W2, ACTUNE_TW_EPI_A4)
+  TWF(ACTUNE_TW_KMAJOR_W4R4, ACTUNE_TW_EPI_A8) TWF(ACTUNE_TW_KMAJOR_W4R4, ACTUNE_TW_EPI_A4)
 #undef TWF
 }
 
 // the six (weight layout, activation layout) pairs of the reference family
 bool pair_ok(int wl, int al) {
-  if (al == ACTUNE_TW_ACT_A8) return wl <= ACTUNE_TW_KMAJOR_W2;
+  if (al == ACTUNE_TW_ACT_A8) return kmajor(wl);
   if (al == ACTUNE_TW_ACT_A4) return wl == ACTUNE_TW_KMAJOR_W8 || wl == ACTUNE_TW_ROWS_S4 || wl == ACTUNE_TW_ROWS_S2;
   return false;
 }
@@ -1224,6 +1266,7 @@ void launch_gemm(int wl, int al, int epi, const TwArgs& a, const Geometry& g, hi
   TW_CASE(ACTUNE_TW_KMAJOR_W8, ACTUNE_TW_ACT_A8)
   TW_CASE(ACTUNE_TW_KMAJOR_W4, ACTUNE_TW_ACT_A8)
   TW_CASE(ACTUNE_TW_KMAJOR_W2, ACTUNE_TW_ACT_A8)
+  TW_CASE(ACTUNE_TW_KMAJOR_W4R4, ACTUNE_TW_ACT_A8)
   TW_CASE(ACTUNE_TW_KMAJOR_W8, ACTUNE_TW_ACT_A4)
   TW_CASE(ACTUNE_TW_ROWS_S4, ACTUNE_TW_ACT_A4)
   TW_CASE(ACTUNE_TW_ROWS_S2, ACTUNE_TW_ACT_A4)
@@ -1241,13 +1284,14 @@ thread_local char g_tw_msg[128];
 int check_tw_shape(int64_t M, int64_t N, int64_t K, int wl, int al) {
   if (!pair_ok(wl, al)) return fail("unsupported tokenwise weight/activation layout pair");
   if (M < 0 || N <= 0 || K <= 0) return fail("invalid dimensions");
+  if (wl == ACTUNE_TW_KMAJOR_W4R4 && M > 32) return fail("the W4R4 layout takes up to 32 rows");
   if (K >= (1 << 17)) return fail("K must stay below 131072 (exact int32 accumulation)");
-  const int kq = wl == ACTUNE_TW_KMAJOR_W4 ? 32 : (wl == ACTUNE_TW_KMAJOR_W2 ? 128 : 64);
+  const int kq = nibble_pairs(wl) ? 32 : (wl == ACTUNE_TW_KMAJOR_W2 ? 128 : 64);
   if (K % kq) {
     snprintf(g_tw_msg, sizeof g_tw_msg, "in_features must be divisible by %d for this layout", kq);
     return fail(g_tw_msg);
   }
-  if (wl <= ACTUNE_TW_KMAJOR_W2 && N % 16) return fail("K-major weight layouts need out_features divisible by 16");
+  if (kmajor(wl) && N % 16) return fail("K-major weight layouts need out_features divisible by 16");
   if (N > INT_MAX / 2 || M > INT_MAX / 2 || M * K >= ((int64_t)1 << 31) || N * K >= ((int64_t)1 << 31) ||
       M * N * 4 >= ((int64_t)1 << 31))
     return fail("operand too large (each buffer must stay below 2 GiB)");
@@ -1333,6 +1377,8 @@ int prepare_linear(TwArgs& args, const void* act, int a_layout, const float* a_s
   args.splits = S;
   args.steps = (int)steps_of(K, w_layout);
   args.targets = 1;
+  args.r = nullptr;
+  args.ws_mul = w_layout == ACTUNE_TW_KMAJOR_W4R4 ? 0.0625f : 1.0f;
   if (S > 1) {
     const int64_t need = (int64_t)S * M * N * 4;
     if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 16))
@@ -1346,7 +1392,7 @@ int prepare_linear(TwArgs& args, const void* act, int a_layout, const float* a_s
 // Checks of a launch that quantizes the rows x itself.
 int check_fused(int x_dtype, int w_layout, int64_t M, int64_t K) {
   if (x_dtype != kBF16 && x_dtype != kF16 && x_dtype != kF32) return fail("unsupported activation dtype");
-  if (w_layout > ACTUNE_TW_KMAJOR_W2) return fail("fused quantization takes the K-major (A8) weight layouts");
+  if (!kmajor(w_layout)) return fail("fused quantization takes the K-major (A8) weight layouts");
   if (M < 1 || M > kTwFusedMaxRows) return fail("fused quantization takes 1 to 8 rows");
   if (M > 1 && x_dtype == kF32) return fail("fused quantization of more than one row takes bf16 or f16 x");
   if (K > tw_fused_max_k(M)) {
@@ -1376,6 +1422,7 @@ int actune_tokenwise_linear(const void* a, int a_layout, const float* a_scales, 
                             int64_t M, int64_t N, int64_t K, int epilogue, void* workspace,
                             int64_t workspace_bytes, void* stream) {
   set_last_error("");
+  if (w_layout == ACTUNE_TW_KMAJOR_W4R4) return fail("the W4R4 layout takes a residual: use actune_tokenwise_linear_multi");
   TwArgs args;
   const int rc = prepare_linear(args, a, a_layout, a_scales, w, w_layout, w_scale, bias, bias_dtype, out, out_dtype,
                                 M, N, K, epilogue, workspace, workspace_bytes);
@@ -1390,6 +1437,7 @@ int actune_tokenwise_linear_x(const void* x, int x_dtype, float* a_scales, const
                               int64_t M, int64_t N, int64_t K, int epilogue, void* workspace,
                               int64_t workspace_bytes, void* stream) {
   set_last_error("");
+  if (w_layout == ACTUNE_TW_KMAJOR_W4R4) return fail("the W4R4 layout takes a residual: use actune_tokenwise_linear_multi");
   const int rc = check_fused(x_dtype, w_layout, M, K);
   if (rc) return rc;
   TwArgs args;
@@ -1409,6 +1457,9 @@ int actune_tokenwise_linear_multi(const void* a, int a_layout, const void* x, in
   if ((a == nullptr) == (x == nullptr)) return fail("pass either activation codes or activation rows");
   if (ntargets < 1 || ntargets > ACTUNE_MAX_TARGETS) return fail("1 to ACTUNE_MAX_TARGETS targets");
   if (!targets) return fail("null pointer");
+  if (w_layout == ACTUNE_TW_KMAJOR_W4R4)
+    for (int i = 0; i < ntargets; ++i)
+      if ((uintptr_t)targets[i].r % 16) return fail("misaligned residual (packed data needs 16 B)");
   if (x) {
     const int rc = check_fused(x_dtype, w_layout, M, K);
     if (rc) return rc;
@@ -1429,9 +1480,12 @@ int actune_tokenwise_linear_multi(const void* a, int a_layout, const void* x, in
   if (per && (int64_t)ntargets * per > workspace_bytes)
     return fail("workspace missing, misaligned or smaller than ntargets x actune_tokenwise_workspace_bytes()");
   args.targets = ntargets;
+  const bool r4 = w_layout == ACTUNE_TW_KMAJOR_W4R4;
   for (int i = 0; i < ntargets; ++i)
-    args.t[i] = TwTarget{static_cast<const uint8_t*>(targets[i].w), targets[i].w_scale, targets[i].bias,
-                         targets[i].out};
+    args.t[i] = TwTarget{static_cast<const uint8_t*>(targets[i].w),
+                         r4 ? static_cast<const uint8_t*>(targets[i].r) : nullptr, targets[i].w_scale,
+                         targets[i].bias, targets[i].out};
+  args.r = args.t[0].r;
   hipStream_t st = (hipStream_t)stream;
   if (x) {
     args.x = x;

@@ -635,9 +635,13 @@ _FUSED_MAX_K = 16384
 _PLANS_PER_MODULE = 4
 
 
-def _no_residual(residuals):
-    if any(r is not None for r in residuals):
-        raise NotImplementedError("the signed-R4 residual decode layout is not part of this backend")
+def _decode_layout(residuals):
+    """KMAJOR_W4, or KMAJOR_W4R4 when any projection carries a signed R4
+    residual (decode_w4a8_triton.py:61-66): its weight code is the int8
+    16 q4 + r4 and its epilogue scale ws / 16; a projection without a
+    residual in the same launch computes as plain W4 (the reference's mixed
+    W4/R4 group, :205-211)."""
+    return _native.TW_KMAJOR_W4R4 if any(r is not None for r in residuals) else _native.TW_KMAJOR_W4
 
 
 def _w4_shape(packed):
@@ -645,11 +649,11 @@ def _w4_shape(packed):
     return packed.shape[1], packed.shape[0] * 2
 
 
-def _count_split_decode(groups, n, k):
+def _count_split_decode(groups, n, k, layout=_native.TW_KMAJOR_W4):
     """DecodeStats of one decode of `groups` sibling projections on one row:
     the GEMM launch (a partial kernel) and, when the library splits K for
     this shape, the integer reduce."""
-    split = _native.tokenwise_workspace_bytes(1, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8) > 0
+    split = _native.tokenwise_workspace_bytes(1, n, k, layout, _native.TW_ACT_A8) > 0
     kind = dict(split_k_calls=1) if groups == 1 else dict(projection_groups=1, projection_calls_fused=groups)
     _count(1, partial_kernels=1, reduction_kernels=int(split), **kind)
 
@@ -667,21 +671,23 @@ def _caller_workspace(partial, need):
 
 def launch_decode_group(activation, weights, residuals, activation_scale, scales, biases, outputs, partial, *,
                         splits=None, bn=None):
-    """Decode of 1 to 4 sibling projections (K-major W4 weights) sharing one
+    """Decode of 1 to 4 sibling projections (K-major W4 weights, each with
+    an optional signed R4 residual of the same packing) sharing one
     quantized row, into caller-owned buffers: ONE GEMM launch over every
     projection's column tiles and K splits, then one integer reduce for all
     of them (decode_w4a8_triton.py:150-239 launches the same pair).
     ``splits`` and ``bn`` are accepted for call compatibility: the library
     sizes the split per shape, and results do not depend on it. ``partial``:
     at least len(weights) x actune_tokenwise_workspace_bytes() bytes."""
-    _no_residual(residuals)
+    layout = _decode_layout(residuals)
     n, k = _w4_shape(weights[0])
     m = activation.numel() // k
-    need = len(weights) * _native.tokenwise_workspace_bytes(m, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8)
+    need = len(weights) * _native.tokenwise_workspace_bytes(m, n, k, layout, _native.TW_ACT_A8)
     targets = [(w, s, b, o.view(m, n)) for w, s, b, o in zip(weights, scales, biases, outputs)]
-    return _native.tokenwise_linear_multi(targets, _native.TW_KMAJOR_W4, n, k, _native.TW_EPI_A8,
+    return _native.tokenwise_linear_multi(targets, layout, n, k, _native.TW_EPI_A8,
                                           activation_scale.reshape(-1), codes=activation.reshape(m, k),
-                                          workspace=_caller_workspace(partial, need))
+                                          workspace=_caller_workspace(partial, need),
+                                          residuals=residuals if layout == _native.TW_KMAJOR_W4R4 else None)
 
 
 def launch_decode(activation, packed, residual, activation_scale, weight_scale, bias, output, partial, *,
@@ -695,15 +701,21 @@ def launch_decode(activation, packed, residual, activation_scale, weight_scale, 
 
 def decode_linear(activation, packed, residual, activation_scale, weight_scale, bias, output):
     """One split-K decode into `output` with a per-call workspace
-    (decode_w4a8_triton.py:312-323)."""
-    _no_residual((residual,))
+    (decode_w4a8_triton.py:312-323); a signed R4 residual goes through the
+    multi-target entry point, the one that takes it."""
+    layout = _decode_layout((residual,))
     n, k = _w4_shape(packed)
     m = activation.numel() // k
-    _native.tokenwise_linear(activation.reshape(m, k), _native.TW_ACT_A8, activation_scale.reshape(-1), packed,
-                             _native.TW_KMAJOR_W4, weight_scale, bias, n, k, _native.TW_EPI_A8, output.view(m, n),
-                             workspace=_split_workspace(m, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8,
-                                                        activation.device))
-    _count_split_decode(1, n, k)
+    work = _split_workspace(m, n, k, layout, _native.TW_ACT_A8, activation.device)
+    if residual is None:
+        _native.tokenwise_linear(activation.reshape(m, k), _native.TW_ACT_A8, activation_scale.reshape(-1), packed,
+                                 layout, weight_scale, bias, n, k, _native.TW_EPI_A8, output.view(m, n),
+                                 workspace=work)
+    else:
+        _native.tokenwise_linear_multi([(packed, weight_scale, bias, output.view(m, n))], layout, n, k,
+                                       _native.TW_EPI_A8, activation_scale.reshape(-1),
+                                       codes=activation.reshape(m, k), workspace=work, residuals=(residual,))
+    _count_split_decode(1, n, k, layout)
 
 
 def _record(issue, device):
@@ -723,8 +735,9 @@ def _record(issue, device):
 
 
 class DecodeGraphPlan:
-    """A captured decode of 1 to 4 sibling projections of one row. The
-    contract is the reference's (decode_w4a8_triton.py:326-425): each run
+    """A captured decode of 1 to 4 sibling projections of one row (K-major
+    W4, each with an optional signed R4 residual). The contract is the
+    reference's (decode_w4a8_triton.py:326-425): each run
     copies the row into the plan's staging buffer, replays, and returns the
     outputs [projections, N] as a fresh tensor, so callers never hold
     graph-owned memory. The graph holds two launches: the GEMM over every
@@ -734,21 +747,20 @@ class DecodeGraphPlan:
     staging buffers."""
 
     def __init__(self, value, weights, residuals, scales, biases):
-        _no_residual(residuals)
         if not 1 <= len(weights) <= _native.MAX_TARGETS:
             raise ValueError(f"a decode plan takes 1 to {_native.MAX_TARGETS} projections")
         self.weights, self.residuals = tuple(weights), tuple(residuals)
         self.scales, self.biases = tuple(scales), tuple(biases)
         self.n, self.k = _w4_shape(self.weights[0])
         self.groups = len(self.weights)
+        self.layout = _decode_layout(self.residuals)
         dev = value.device
         self.quantize_in_gemm = self.k <= _FUSED_MAX_K
         self.input = torch.empty((1, self.k), device=dev, dtype=value.dtype)
         self.activation = None if self.quantize_in_gemm else torch.empty((1, self.k), device=dev, dtype=torch.int8)
         self.scale = torch.empty(1, device=dev, dtype=torch.float32)
         self.output = torch.empty((self.groups, self.n), device=dev, dtype=value.dtype)
-        need = self.groups * _native.tokenwise_workspace_bytes(1, self.n, self.k, _native.TW_KMAJOR_W4,
-                                                               _native.TW_ACT_A8)
+        need = self.groups * _native.tokenwise_workspace_bytes(1, self.n, self.k, self.layout, _native.TW_ACT_A8)
         self.partial = torch.empty(need, device=dev, dtype=torch.uint8) if need else None
         self.lock = threading.Lock()
         self.input.copy_(value.reshape(1, self.k))
@@ -757,13 +769,14 @@ class DecodeGraphPlan:
     def _issue(self):
         targets = [(w, s, b, self.output[i:i + 1])
                    for i, (w, s, b) in enumerate(zip(self.weights, self.scales, self.biases))]
+        residuals = self.residuals if self.layout == _native.TW_KMAJOR_W4R4 else None
         if self.quantize_in_gemm:
-            _native.tokenwise_linear_multi(targets, _native.TW_KMAJOR_W4, self.n, self.k, _native.TW_EPI_A8,
-                                           self.scale, x=self.input, workspace=self.partial)
+            _native.tokenwise_linear_multi(targets, self.layout, self.n, self.k, _native.TW_EPI_A8, self.scale,
+                                           x=self.input, workspace=self.partial, residuals=residuals)
         else:
             _native.tokenwise_quantize(self.input, 8, self.activation, self.scale)
-            _native.tokenwise_linear_multi(targets, _native.TW_KMAJOR_W4, self.n, self.k, _native.TW_EPI_A8,
-                                           self.scale, codes=self.activation, workspace=self.partial)
+            _native.tokenwise_linear_multi(targets, self.layout, self.n, self.k, _native.TW_EPI_A8, self.scale,
+                                           codes=self.activation, workspace=self.partial, residuals=residuals)
 
     @property
     def workspace_bytes(self):
@@ -778,7 +791,7 @@ class DecodeGraphPlan:
             result = self.output.clone()
         separate = int(not self.quantize_in_gemm)
         _count(1, graph_replays=1, graph_quantization_kernels=separate, resident_quantization_kernels=separate)
-        _count_split_decode(self.groups, self.n, self.k)
+        _count_split_decode(self.groups, self.n, self.k, self.layout)
         return result
 
 

@@ -172,9 +172,17 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A);
  *   ACTUNE_TW_KMAJOR_W2  u8 [K/4, N], byte j = codes j + f K/4 at bits 2f (w2a8_triton.py:149-159)
  *   ACTUNE_TW_ROWS_S4    u8 [N, K/2], consecutive nibbles               (wxa4_native.py:206-211)
  *   ACTUNE_TW_ROWS_S2    u8 [N, K/4], consecutive 2-bit fields          (wxa4_native.py:212-219)
+ *   ACTUNE_TW_KMAJOR_W4R4  two KMAJOR_W4 buffers, q4 codes and the signed
+ *                        R4 residual r4; the weight code is the int8
+ *                        16 q4 + r4, wrapped to 8 bits as the reference
+ *                        forms it (decode_w4a8_triton.py:61-66), and the
+ *                        A8 epilogue uses ws[n] / 16 (:103-104). Through
+ *                        actune_tokenwise_linear_multi only, M <= 32; a
+ *                        target with no residual reads r4 = 0 (its result
+ *                        equals KMAJOR_W4's).
  * Activations: ACTUNE_TW_ACT_A8 int8 codes [M, K]; ACTUNE_TW_ACT_A4 packed
- * [M, K/2] (low nibble = even k). Supported pairs: the three K-major
- * layouts with A8, and KMAJOR_W8 / ROWS_S4 / ROWS_S2 with A4.
+ * [M, K/2] (low nibble = even k). Supported pairs: the K-major layouts with
+ * A8, and KMAJOR_W8 / ROWS_S4 / ROWS_S2 with A4.
  * Epilogues (fp32, then rounded to out_dtype):
  *   ACTUNE_TW_EPI_A8  t = f32(acc) * as[m]; y = bias ? fmaf(t, ws[n], bias[n]) : t * ws[n]
  *                     (w4a8_triton.py:105-113, decode_w4a8_triton.py:102-110)
@@ -183,7 +191,7 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A);
  */
 enum {
   ACTUNE_TW_KMAJOR_W8 = 0, ACTUNE_TW_KMAJOR_W4 = 1, ACTUNE_TW_KMAJOR_W2 = 2,
-  ACTUNE_TW_ROWS_S4 = 3, ACTUNE_TW_ROWS_S2 = 4
+  ACTUNE_TW_ROWS_S4 = 3, ACTUNE_TW_ROWS_S2 = 4, ACTUNE_TW_KMAJOR_W4R4 = 5
 };
 enum { ACTUNE_TW_ACT_A8 = 0, ACTUNE_TW_ACT_A4 = 1 };
 enum { ACTUNE_TW_EPI_A8 = 0, ACTUNE_TW_EPI_A4 = 1 };
@@ -249,6 +257,7 @@ int actune_tokenwise_linear_x(const void* x, int x_dtype, float* a_scales, const
 /* One projection of a multi-target tokenwise call. */
 typedef struct actune_tw_target {
   const void* w;          /* weights [.., N] in the call's layout */
+  const void* r;          /* ACTUNE_TW_KMAJOR_W4R4: residual codes [K/2, N], or NULL; else unused */
   const float* w_scale;   /* [N] */
   const void* bias;       /* [N] in the call's bias dtype, or NULL */
   void* out;              /* [M, N] in out_dtype */

@@ -18,10 +18,15 @@ the reference lines (zanehpn/Actune) it restates:
 * ``group_epilogue``   kernels/grouped.py:90-94, grouped_native.cu:75, 85.
 * ``activation_dequant`` / ``reference_float_linear``  calibration.py:7-16 and
   tests/test_kernels.py:42-44 (the reference's float dequant-then-matmul).
+* ``tw_*`` / ``pack_kmajor`` / ``unpack_kmajor``  the tokenwise family
+  (w4a8_triton.py, w8a8_triton.py, w2a8_triton.py, wxa4_native.py).
+* ``nested_r4_codes``  decode_w4a8_triton.py:61-66 (signed-R4 residual codes).
 
-Pinning: every function is checked in ``tests/test_oracle.py`` against known
-answers fixed by the mathematics (exactly representable ties, hand-derived
-codes and bytes, brute-force integer dots, exact-rational FMA cases).
+Pinning: every function is checked against known answers fixed by the
+mathematics (exactly representable ties, hand-derived codes and bytes,
+brute-force integer dots, exact-rational FMA cases): the group-64 functions
+in ``tests/test_oracle.py``, the tokenwise ones in
+``tests/test_oracle_tokenwise.py``.
 """
 from __future__ import annotations
 
@@ -324,6 +329,20 @@ def pack_kmajor(codes, bits):
     for f in fields:
         packed |= f
     return np.ascontiguousarray(packed.astype(np.uint8).T)
+
+
+def nested_r4_codes(q4, r4):
+    """The W4R4 decode's int8 weight codes from signed q4 and r4 codes (each
+    int8 in [-8, 7], any shape): 16 q4 + r4 formed in int16 and narrowed to
+    8 bits by two's-complement wrap (decode_w4a8_triton.py:61-66), so the
+    pair (-8, r < 0) wraps to 128 + r. The matching epilogue is mode 0 with
+    the weight scale divided by 16 (:103-104)."""
+    q = _c(q4, np.int8).astype(np.int16)
+    r = _c(r4, np.int8).astype(np.int16)
+    if q.shape != r.shape or q.min(initial=0) < -8 or q.max(initial=0) > 7 or r.min(initial=0) < -8 \
+            or r.max(initial=0) > 7:
+        raise ValueError("q4 and r4 are signed 4-bit codes of one shape")
+    return (q * 16 + r).astype(np.uint16).astype(np.uint8).view(np.int8)
 
 
 def unpack_kmajor(packed, bits, K):

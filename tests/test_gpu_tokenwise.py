@@ -499,9 +499,6 @@ def test_decode_group_plan_and_launch_group():
     T.launch_decode_group(act, [m.packed_weight for m in mods], [None] * 3, s, [m.weight_scale for m in mods],
                           [m.bias for m in mods], outs, partial)
     assert all(torch.equal(o, w) for o, w in zip(outs, want))
-    with pytest.raises(NotImplementedError):
-        T.launch_decode_group(act, [mods[0].packed_weight], [mods[0].packed_weight], s, [mods[0].weight_scale],
-                              [None], outs[:1], partial)
 
 
 def test_captured_split_workspace_survives_later_calls():
@@ -531,3 +528,146 @@ def test_captured_split_workspace_survives_later_calls():
             assert torch.equal(y, want1)
         assert all(bool((f == 1234 + i).all()) for i, f in enumerate(fillers))
         assert torch.equal(mod(x8), want8)
+
+
+# ---------------------------------------------------------------- signed-R4 residual decode
+def _r4_targets(n, k, count, seed, m=1, with_residual=(True,), bias_dtype=torch.bfloat16):
+    """count W4R4 projections: random q4 / r4 codes (about 1 in 32 pairs
+    wraps), residual present per with_residual (cycled), a bias on every
+    other projection; the oracle's expected codes and epilogue scale."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        q = rng.integers(-8, 8, (n, k)).astype(np.int8)
+        has = with_residual[i % len(with_residual)]
+        r = rng.integers(-8, 8, (n, k)).astype(np.int8) if has else np.zeros((n, k), np.int8)
+        ws = rng.uniform(1e-3, 3e-2, n).astype(np.float32)
+        bias = None
+        if i % 2:
+            bias = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(DEV).to(bias_dtype)
+        out.append(dict(q=q, nested=O.nested_r4_codes(q, r), scale=ws, w=torch.from_numpy(O.pack_kmajor(q, 4)).to(DEV),
+                        r=torch.from_numpy(O.pack_kmajor(r, 4)).to(DEV) if has else None,
+                        ws=torch.from_numpy(ws).to(DEV), bias=bias,
+                        out=torch.full((m, n), 5.0, device=DEV, dtype=torch.bfloat16)))
+    return out
+
+
+def _r4_oracle(a_codes, a_scales, t, cols=None):
+    sel = slice(None) if cols is None else cols
+    b = None if t["bias"] is None else t["bias"].float().cpu().numpy()[sel]
+    acc = O.tw_dots(a_codes, t["nested"][sel])
+    return O.round_out(O.tw_epilogue(acc, a_scales, t["scale"][sel] / np.float32(16), b, 0), "bf16")
+
+
+@pytest.mark.parametrize("m,n,k,count", [(1, 4096, 4096, 3), (1, 11008, 4096, 2), (1, 4096, 11008, 1),
+                                         (8, 512, 2048, 2), (32, 256, 1024, 4), (3, 96, 160, 1), (17, 48, 64, 2)])
+@pytest.mark.parametrize("source", ["codes", "x"])
+def test_w4r4_multi_against_oracle(m, n, k, count, source):
+    """actune_tokenwise_linear_multi in the W4R4 layout, residuals present on
+    some projections and absent on others: every output equals the oracle
+    (int8 codes 16 q4 + r4 with the reference's wrap, epilogue scale ws / 16)
+    on sampled columns, from activation codes or from rows quantized in the
+    launch (M <= 8); K = 160 ends in a half K-step."""
+    if source == "x" and m > 8:
+        pytest.skip("rows are quantized in the launch up to M = 8")
+    x, _, _ = seeded_inputs(m, k, 1, seed=m * 7 + n + k)
+    xd = x.to(DEV)
+    tg = _r4_targets(n, k, count, seed=n + k + count, m=m, with_residual=(True, False))
+    wl = _native.TW_KMAJOR_W4R4
+    need = count * _native.tokenwise_workspace_bytes(m, n, k, wl, _native.TW_ACT_A8)
+    work = torch.full((max(need, 1),), 0x5A, dtype=torch.uint8, device=DEV) if need else None
+    targets = [(t["w"], t["ws"], t["bias"], t["out"]) for t in tg]
+    residuals = [t["r"] for t in tg]
+    if source == "codes":
+        act, s = _native.tokenwise_quantize(xd, 8)
+        _native.tokenwise_linear_multi(targets, wl, n, k, _native.TW_EPI_A8, s, codes=act, workspace=work,
+                                       residuals=residuals)
+    else:
+        s = torch.full((m,), -1.0, device=DEV)
+        _native.tokenwise_linear_multi(targets, wl, n, k, _native.TW_EPI_A8, s, x=xd, workspace=work,
+                                       residuals=residuals)
+    torch.cuda.synchronize()
+    a_codes, a_scales = O.tw_quantize_rows(bits(x), 8)
+    np.testing.assert_array_equal(s.cpu().numpy(), a_scales)
+    cols = None if n <= 512 else np.sort(np.random.default_rng(k + 1).choice(n, size=96, replace=False))
+    for i, t in enumerate(tg):
+        got = bits(t["out"]) if cols is None else bits(t["out"])[:, cols]
+        np.testing.assert_array_equal(got, _r4_oracle(a_codes, a_scales, t, cols), err_msg=f"projection {i}")
+
+
+def test_w4r4_without_residual_equals_w4():
+    """A W4R4 launch whose projection has no residual gives the plain
+    KMAJOR_W4 call's result bit for bit (codes 16 q4, scale ws / 16)."""
+    m, n, k = 4, 1024, 4096
+    x = torch.randn(m, k, device=DEV).to(torch.bfloat16)
+    act, s = _native.tokenwise_quantize(x, 8)
+    (t,) = _r4_targets(n, k, 1, seed=4, m=m, with_residual=(False,))
+    need = _native.tokenwise_workspace_bytes(m, n, k, _native.TW_KMAJOR_W4, _native.TW_ACT_A8)
+    want = torch.empty(m, n, device=DEV, dtype=torch.bfloat16)
+    _native.tokenwise_linear(act, _native.TW_ACT_A8, s, t["w"], _native.TW_KMAJOR_W4, t["ws"], None, n, k,
+                             _native.TW_EPI_A8, want,
+                             workspace=torch.empty(need, dtype=torch.uint8, device=DEV) if need else None)
+    need4 = _native.tokenwise_workspace_bytes(m, n, k, _native.TW_KMAJOR_W4R4, _native.TW_ACT_A8)
+    _native.tokenwise_linear_multi([(t["w"], t["ws"], None, t["out"])], _native.TW_KMAJOR_W4R4, n, k,
+                                   _native.TW_EPI_A8, s, codes=act, residuals=[None],
+                                   workspace=torch.empty(need4, dtype=torch.uint8, device=DEV) if need4 else None)
+    assert torch.equal(t["out"], want)
+
+
+def test_w4r4_decode_surface_mixed_group():
+    """The decode API with residuals (decode_w4a8_triton.py:113-239, 312-425):
+    a mixed W4/R4 q/k/v group through launch_decode_group on caller buffers
+    and through a DecodeGraphPlan (three replays), decode_linear and
+    launch_decode on one residual projection: all equal the oracle."""
+    n, k = 4096, 4096
+    tg = _r4_targets(n, k, 3, seed=12, with_residual=(True, False, True), bias_dtype=torch.bfloat16)
+    x, _, _ = seeded_inputs(1, k, 1, seed=12)
+    xd = x.to(DEV)
+    a_codes, a_scales = O.tw_quantize_rows(bits(x), 8)
+    want = [_r4_oracle(a_codes, a_scales, t) for t in tg]
+    act, s = _native.tokenwise_quantize(xd, 8)
+    weights, residuals = [t["w"] for t in tg], [t["r"] for t in tg]
+    scales, biases = [t["ws"] for t in tg], [t["bias"] for t in tg]
+    outs = [torch.empty(1, n, device=DEV, dtype=torch.bfloat16) for _ in tg]
+    partial = torch.full((3 * 32, n), 7, dtype=torch.int32, device=DEV)
+    T.launch_decode_group(act, weights, residuals, s, scales, biases, outs, partial)
+    for i, o in enumerate(outs):
+        np.testing.assert_array_equal(bits(o), want[i], err_msg=f"group projection {i}")
+    plan = T.DecodeGraphPlan(xd, weights, residuals, scales, biases)
+    with T.decode_optimization_scope() as stats:
+        for _ in range(3):
+            got = plan.run(xd)
+            torch.cuda.synchronize()
+            for i in range(3):
+                np.testing.assert_array_equal(bits(got[i:i + 1]), want[i], err_msg=f"plan projection {i}")
+    assert stats.graph_replays == 3 and stats.projection_calls_fused == 9
+    one = torch.empty(1, n, device=DEV, dtype=torch.bfloat16)
+    with T.decode_optimization_scope() as stats:
+        T.decode_linear(act, tg[0]["w"], tg[0]["r"], s, tg[0]["ws"], tg[0]["bias"], one)
+    assert stats.split_k_calls == 1
+    np.testing.assert_array_equal(bits(one), want[0])
+    one.fill_(0)
+    T.launch_decode(act, tg[2]["w"], tg[2]["r"], s, tg[2]["ws"], tg[2]["bias"], one, partial)
+    np.testing.assert_array_equal(bits(one), want[2])
+
+
+def test_w4r4_rejects_bad_calls():
+    m, n, k = 1, 64, 256
+    x = torch.randn(m, k, device=DEV).to(torch.bfloat16)
+    act, s = _native.tokenwise_quantize(x, 8)
+    (t,) = _r4_targets(n, k, 1, seed=2, m=m)
+    tgt = [(t["w"], t["ws"], None, t["out"])]
+    with pytest.raises(ValueError, match="actune_tokenwise_linear_multi"):
+        _native.tokenwise_linear(act, _native.TW_ACT_A8, s, t["w"], _native.TW_KMAJOR_W4R4, t["ws"], None, n, k,
+                                 _native.TW_EPI_A8, t["out"])
+    with pytest.raises(ValueError, match="W4R4 layout only"):
+        _native.tokenwise_linear_multi(tgt, _native.TW_KMAJOR_W4, n, k, 0, s, codes=act, residuals=[t["r"]])
+    with pytest.raises(ValueError, match="one residual"):
+        _native.tokenwise_linear_multi(tgt, _native.TW_KMAJOR_W4R4, n, k, 0, s, codes=act, residuals=[t["r"]] * 2)
+    with pytest.raises(RuntimeError, match="residual shape"):
+        _native.tokenwise_linear_multi(tgt, _native.TW_KMAJOR_W4R4, n, k, 0, s, codes=act, residuals=[t["r"][:-1]])
+    big = torch.zeros(33, k, dtype=torch.int8, device=DEV)
+    with pytest.raises(ValueError, match="up to 32 rows"):
+        _native.tokenwise_linear_multi([(t["w"], t["ws"], None, torch.empty(33, n, device=DEV))],
+                                       _native.TW_KMAJOR_W4R4, n, k, 0, torch.ones(33, device=DEV), codes=big,
+                                       residuals=[t["r"]])

@@ -192,3 +192,41 @@ def test_epilogue_orders_exact_rational():
     # the fused form is observable: unfused rounding gives another value here
     t = rn32(F(np.float32(3)) * F(as_[0]))
     assert rn32(F(t) * F(ws[0]) + F(bias[0])) != rn32(F(rn32(F(t) * F(ws[0]))) + F(bias[0]))
+
+
+def test_nested_r4_codes_hand_derived_and_wrap():
+    """W4R4 codes: hand-derived values, including the wrapped (-8, r < 0)
+    pairs; r = 0 is exactly 16 q; every non-wrapping pair dequantizes to
+    q + r / 16 (the two-level grid the residual refines)."""
+    pairs = {(0, 0): 0, (7, 7): 119, (-8, 0): -128, (-8, -1): 127, (-8, -8): 120, (7, -8): 104,
+             (-1, -1): -17, (1, -8): 8, (-7, -8): -120, (3, 5): 53}
+    q = np.array([p[0] for p in pairs], np.int8)
+    r = np.array([p[1] for p in pairs], np.int8)
+    np.testing.assert_array_equal(O.nested_r4_codes(q, r), np.array(list(pairs.values()), np.int8))
+    grid = np.arange(-8, 8, dtype=np.int8)
+    qq, rr = np.meshgrid(grid, grid, indexing="ij")
+    codes = O.nested_r4_codes(qq, rr)
+    np.testing.assert_array_equal(O.nested_r4_codes(grid, np.zeros(16, np.int8)), grid.astype(np.int16) * 16)
+    wrap = (qq == -8) & (rr < 0)
+    assert wrap.sum() == 8 and (codes[wrap] >= 120).all()
+    for qv, rv, c in zip(qq[~wrap], rr[~wrap], codes[~wrap]):
+        assert Fraction(int(c), 16) == qv + Fraction(int(rv), 16)
+    # all 256 codes reached exactly once: the map is a bijection onto int8
+    assert len(np.unique(codes)) == 256
+    with pytest.raises(ValueError):
+        O.nested_r4_codes(np.array([8], np.int8), np.array([0], np.int8))
+
+
+def test_nested_r4_epilogue_with_zero_residual_is_w4():
+    """With r = 0 the W4R4 result (codes 16 q, scale ws / 16) equals the
+    plain W4 result bit for bit: the factor 16 is exact in int32 and fp32."""
+    rng = np.random.default_rng(3)
+    a = rng.integers(-127, 128, (5, 256)).astype(np.int8)
+    q = rng.integers(-8, 8, (48, 256)).astype(np.int8)
+    as_ = rng.uniform(1e-3, 1e-1, 5).astype(np.float32)
+    ws = rng.uniform(1e-3, 1e-1, 48).astype(np.float32)
+    bias = rng.standard_normal(48).astype(np.float32)
+    w4 = O.tw_epilogue(O.tw_dots(a, q), as_, ws, bias, 0)
+    nested = O.nested_r4_codes(q, np.zeros_like(q))
+    r4 = O.tw_epilogue(O.tw_dots(a, nested), as_, ws / np.float32(16), bias, 0)
+    np.testing.assert_array_equal(r4.view(np.uint32), w4.view(np.uint32))
