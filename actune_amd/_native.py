@@ -29,7 +29,7 @@ MAX_TARGETS = 4
 
 class _Target(ctypes.Structure):
     """actune_linear_target"""
-    _fields_ = [("w", _P), ("w_scale", _P), ("bias", _P), ("out", _P), ("N", _I64)]
+    _fields_ = [("w", _P), ("w_scale", _P), ("bias", _P), ("out", _P), ("N", _I64), ("W", ctypes.c_int32)]
 
 
 class _TwTarget(ctypes.Structure):
@@ -317,10 +317,13 @@ def grouped_forward_multi(flat, targets, W, A, input_scale=None, config=CONFIG_A
                           scales=None):
     """Quantize + GEMM of one [M, K] input against up to 4 linears in one
     launch. targets: sequence of (w, ws, bias, out) with out [M, N_t] (None
-    to allocate). Returns the list of outputs."""
+    to allocate), or (w, ws, bias, out, W_t) for a target whose weight width
+    W_t differs from W (the call then runs the widths in one decode launch
+    where the kernel takes them, else one launch per width on one
+    quantization). Returns the list of outputs."""
     if not 1 <= len(targets) <= MAX_TARGETS:
         raise ValueError("between 1 and 4 targets required")
-    _require_cuda(flat, input_scale, packed, scales, *[t for tgt in targets for t in tgt])
+    _require_cuda(flat, input_scale, packed, scales, *[t for tgt in targets for t in tgt[:4]])
     _check_widths(W, A)
     _check_flat(flat)
     m, k = flat.shape
@@ -332,13 +335,17 @@ def grouped_forward_multi(flat, targets, W, A, input_scale=None, config=CONFIG_A
     bias_dt = _bias_code(biases[0])
     arr = (_Target * len(targets))()
     outs = []
-    for j, (w, ws, bias, out) in enumerate(targets):
-        n = _check_weights(w, ws, bias, k, W)
+    for j, tgt in enumerate(targets):
+        w, ws, bias, out = tgt[:4]
+        wt = tgt[4] if len(tgt) > 4 else W
+        _check_widths(wt, A)
+        n = _check_weights(w, ws, bias, k, wt)
         if out is None:
             out = torch.empty((m, n), device=flat.device, dtype=flat.dtype)
         _check_buffer(out, f"out[{j}]", (m, n), flat.dtype, flat.device)
         outs.append(out)
-        arr[j] = _Target(w.data_ptr(), ws.data_ptr(), None if bias is None else bias.data_ptr(), out.data_ptr(), n)
+        arr[j] = _Target(w.data_ptr(), ws.data_ptr(), None if bias is None else bias.data_ptr(), out.data_ptr(), n,
+                         wt)
     packed, scales = _act_buffers(packed, scales, m, k, A, flat.device)
     _check(lib().actune_grouped_forward_multi(_ptr(flat), _dtype_code(flat), _ptr(input_scale), _ptr(packed),
                                               _ptr(scales), arr, len(targets), bias_dt, m, k, W, A, config,

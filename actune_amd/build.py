@@ -19,7 +19,7 @@ OBJ = PKG / "_build"
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libactune_hip.so"
 SOURCES = ["api.hip", "quantize.hip", "gemm_smallm.hip", "gemm_tiled.hip", "gemm_stream.hip", "gemm_prefill.hip", "gemm_decode.hip",
-           "noalloc.hip", "tokenwise.hip"]
+           "gemm_decode_mixed.hip", "noalloc.hip", "tokenwise.hip"]
 # diagnostic library of register-resident compute ceilings, timed by bench.py
 CEILING_SOURCE = "ceiling.hip"
 CEILING_LIB = LIB_DIR / "libactune_ceiling.so"

@@ -125,9 +125,9 @@ int resolve(int config, int64_t M, int64_t N, int64_t K, int W, int A, bool has_
 }
 
 // Fill the problem table of a launch; returns the number of 16-row tiles.
-int add_problem(LinearArgs& g, const uint8_t* w, const float* ws, const void* bias, void* out, int64_t N) {
+int add_problem(LinearArgs& g, const uint8_t* w, const float* ws, const void* bias, void* out, int64_t N, int W) {
   Problem& p = g.prob[g.nprob++];
-  p = Problem{w, ws, bias, out, (int)N, g.tiles};
+  p = Problem{w, ws, bias, out, (int)N, g.tiles, W};
   g.tiles += (int)((N + 15) / 16);
   return g.tiles;
 }
@@ -377,10 +377,61 @@ int actune_grouped_linear(const uint8_t* a, const float* a_scales, const uint8_t
   LinearArgs g = base_args(M, K, bias_dtype, out_dtype);
   g.a = a;
   g.as = a_scales;
-  add_problem(g, w, w_scale, bias, out, N);
+  add_problem(g, w, w_scale, bias, out, N, W);
   run_gemm(W, A, config, kModePacked, g, (hipStream_t)stream);
   return check_launch();
 }
+
+namespace {
+// Targets of different weight widths (one A). The decode kernel runs them in
+// one launch where its config takes every width: x quantized in the launch
+// where the widest width's launch would quantize it, else on the quantizer's
+// codes. Otherwise x is quantized once and each width runs its own launch on
+// the codes (its own default config under ACTUNE_CONFIG_AUTO). Either way
+// every output equals the single-width call.
+int forward_mixed(LinearArgs& g, int config, bool auto_config, int64_t n_total, const void* x, int x_dtype,
+                  const void* input_scale, uint8_t* a_buf, float* scale_buf, int A, hipStream_t st) {
+  int wmax = 2;
+  for (int q = 0; q < g.nprob; ++q) wmax = std::max(wmax, g.prob[q].W);
+  if (config >= kDecodeFirst) {
+    const int nw = kSmallMWaves[config - kDecodeFirst];
+    const bool fused = decode_fits(g.K, g.M, wmax, nw, false, x_dtype) && decode_light(g.M, n_total, g.K, wmax, nw);
+    bool fits = true;
+    for (int q = 0; q < g.nprob; ++q) fits = fits && decode_fits(g.K, g.M, g.prob[q].W, nw, !fused, x_dtype);
+    if (fits) {
+      if (fused) {
+        g.x = x;
+        g.xscale = input_scale;
+        g.x_dt = x_dtype;
+      } else {
+        launch_quantize(x, x_dtype, input_scale, g.M, g.K, A, a_buf, scale_buf, st);
+        g.a = a_buf;
+        g.as = scale_buf;
+      }
+      launch_decode_mixed(A, nw, !fused, g, st);
+      return check_launch();
+    }
+  }
+  launch_quantize(x, x_dtype, input_scale, g.M, g.K, A, a_buf, scale_buf, st);
+  bool done[kMaxProblems] = {};
+  for (int q = 0; q < g.nprob; ++q) {
+    if (done[q]) continue;
+    const int w = g.prob[q].W;
+    LinearArgs one = base_args(g.M, g.K, g.bias_dt, g.out_dt);
+    one.a = a_buf;
+    one.as = scale_buf;
+    int64_t n_w = 0;
+    for (int r = q; r < g.nprob; ++r)
+      if (!done[r] && g.prob[r].W == w) {
+        add_problem(one, g.prob[r].w, g.prob[r].ws, g.prob[r].bias, g.prob[r].out, g.prob[r].N, w);
+        n_w += g.prob[r].N;
+        done[r] = true;
+      }
+    run_gemm(w, A, auto_config ? packed_default(g.M, n_w, g.K, w, A) : config, kModePacked, one, st);
+  }
+  return check_launch();
+}
+}  // namespace
 
 int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_scale, uint8_t* a_buf,
                                  float* scale_buf, const actune_linear_target* targets, int ntargets,
@@ -389,19 +440,32 @@ int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_s
   g_err[0] = 0;
   if (ntargets < 1 || ntargets > ACTUNE_MAX_TARGETS || !targets)
     return fail(ACTUNE_ERR_INVALID, "between 1 and 4 targets required");
+  // each target's width: its own W field, or the call's W where that is 0
+  int widths[ACTUNE_MAX_TARGETS];
+  bool mixed = false;
+  for (int t = 0; t < ntargets; ++t) {
+    widths[t] = targets[t].W ? targets[t].W : W;
+    if (!width_ok(widths[t])) return fail(ACTUNE_ERR_INVALID, "Unsupported integer width");
+    mixed = mixed || widths[t] != widths[0];
+  }
+  // the widest width sizes the launch (its weight ring is the tightest)
+  W = *std::max_element(widths, widths + ntargets);
   int64_t n_total = 0;
   for (int t = 0; t < ntargets; ++t) n_total += targets[t].N;
+  const bool auto_config = config == ACTUNE_CONFIG_AUTO;
   config = resolve(config, M, n_total, K, W, A, true);
   int rc = check_shape(M, K, W, A, x_dtype, bias_dtype, config);
   if (!rc) rc = check_quantize(x, x_dtype, input_scale, M, K, A, a_buf, scale_buf);
   for (int t = 0; t < ntargets && !rc; ++t)
-    rc = check_target(targets[t].w, targets[t].w_scale, targets[t].out, targets[t].N, M, K, W);
+    rc = check_target(targets[t].w, targets[t].w_scale, targets[t].out, targets[t].N, M, K, widths[t]);
   if (!rc && n_total / 16 >= INT_MAX / 2) rc = fail(ACTUNE_ERR_INVALID, "dimensions too large");
   if (rc || M == 0) return rc;
   hipStream_t st = (hipStream_t)stream;
   LinearArgs g = base_args(M, K, bias_dtype, x_dtype);
   for (int t = 0; t < ntargets; ++t)
-    add_problem(g, targets[t].w, targets[t].w_scale, targets[t].bias, targets[t].out, targets[t].N);
+    add_problem(g, targets[t].w, targets[t].w_scale, targets[t].bias, targets[t].out, targets[t].N, widths[t]);
+  if (mixed)
+    return forward_mixed(g, config, auto_config, n_total, x, x_dtype, input_scale, a_buf, scale_buf, A, st);
   const bool fused = forward_fuses(config, M, n_total, K, W, x_dtype);
   if (fused) {
     g.x = x;
@@ -439,7 +503,7 @@ int actune_grouped_dots_i32(const uint8_t* a, const uint8_t* w, int64_t M, int64
   LinearArgs g = base_args(M, K, kF32, kF32);
   g.a = a;
   g.dots = dots;
-  add_problem(g, w, nullptr, nullptr, nullptr, N);
+  add_problem(g, w, nullptr, nullptr, nullptr, N, W);
   run_gemm(W, A, config, kModeDots, g, (hipStream_t)stream);
   return check_launch();
 }

@@ -16,7 +16,8 @@ constexpr int kDecodeMaxGroupRows = 256;
 constexpr size_t kStreamLdsMax = 144 * 1024;
 
 // One linear of a launch: all problems of a launch share the activation
-// (x or its packed codes), K, W and A.
+// (x or its packed codes), K and A, and all but the mixed-width decode
+// launch (launch_decode_mixed) share W.
 struct Problem {
   const uint8_t* w;     // packed weights [N, K*W/8]
   const float* ws;      // weight scale [N]
@@ -24,6 +25,7 @@ struct Problem {
   void* out;            // [M, N] in out_dt
   int N;
   int tile0;            // first 16-row tile of this problem in the launch grid
+  int W;                // weight width of this problem
 };
 
 enum { kModePacked = 0, kModeFused = 1, kModeDots = 2 };
@@ -69,6 +71,7 @@ __device__ __forceinline__ Problem select_problem(const LinearArgs& args, int ti
     pr.out = s ? pp[q].out : pr.out;
     pr.N = s ? pp[q].N : pr.N;
     pr.tile0 = s ? pp[q].tile0 : pr.tile0;
+    pr.W = s ? pp[q].W : pr.W;
   }
   return pr;
 }
@@ -100,6 +103,9 @@ void launch_prefill(int W, int A, int shape, bool dots, const LinearArgs& g, hip
 // packed: the activations are codes + scales from the quantizer launch
 // (g.a, g.as); otherwise bf16 x is quantized inside the launch (g.x)
 void launch_decode(int W, int A, int nw, bool packed, const LinearArgs& g, hipStream_t st);
+// The decode kernel over problems of different widths (Problem::W, each in
+// {2, 4, 8}), one launch; every width must pass decode_fits
+void launch_decode_mixed(int A, int nw, bool packed, const LinearArgs& g, hipStream_t st);
 size_t decode_lds_bytes(int K, int M, int nw, int tr);
 // true when the decode kernel with nw waves takes an M x K problem of width W
 // in the given activation mode (every wave's loads fit its register ring and

@@ -303,10 +303,11 @@ def grouped_sibling_forward(x, modules):
     input x — sibling projections such as q/k/v or gate/up — and return their
     outputs in order.
 
-    When every module's active backend has the same (W, A), K, padding, bias
-    dtype and input scale, all of them run in ONE quantize + GEMM launch
-    (actune_grouped_forward_multi, up to 4 targets); otherwise each module
-    runs on its own. Either way the outputs are bit-identical to calling the
+    When every module's active backend has the same A, K, padding, bias
+    dtype and input scale, all of them run in one actune_grouped_forward_multi
+    call (up to 4 targets): one quantize + GEMM launch, also where their
+    weight widths differ (q/k/v of a mixed-precision bank) and the decode
+    kernel takes every width; otherwise each module runs on its own. Either way the outputs are bit-identical to calling the
     modules one by one, and each module's calls / input_elements counters
     advance exactly as for a separate call (BankRuntime.audit relies on them).
     """
@@ -320,7 +321,7 @@ def grouped_sibling_forward(x, modules):
         x.is_cuda and 1 < len(modules) <= _native.MAX_TARGETS
         and all(getattr(b.forward, "__func__", None) is GroupedLinear.forward for b in backends)
         and all(m.in_features == first.in_features and m.padding == first.padding for m in modules)
-        and all((b.w, b.a) == (fb.w, fb.a) for b in backends)
+        and all(b.a == fb.a for b in backends)
         and len({None if b.bias is None else b.bias.dtype for b in backends}) == 1
         and all(getattr(m, "input_scale", None) is scale for m in modules)
         and (scale is None or scale.dtype == x.dtype)
@@ -335,6 +336,6 @@ def grouped_sibling_forward(x, modules):
         if scale is not None:
             scale = torch.nn.functional.pad(scale, (0, first.padding), value=1.0)
     flat = x.reshape(-1, fb.in_features).contiguous()
-    targets = [(b.packed_weight, b.weight_scale, b.bias, None) for b in backends]
+    targets = [(b.packed_weight, b.weight_scale, b.bias, None, b.w) for b in backends]
     outs = _native.grouped_forward_multi(flat, targets, fb.w, fb.a, input_scale=scale, config=fb.config)
     return [o.reshape(*x.shape[:-1], m.out_features) for o, m in zip(outs, modules)]

@@ -67,6 +67,8 @@ def parse():
     p.add_argument("--config", type=int, default=-1, help="kernel config for --only (default: automatic)")
     p.add_argument("--tokenwise-only", action="store_true",
                    help="only run the tokenwise-family section and print it as one JSON line")
+    p.add_argument("--expert-only", action="store_true",
+                   help="only run the C5 action-expert section (--steps timed loops) as one JSON line")
     return p.parse_args()
 
 
@@ -643,7 +645,7 @@ EXPERT = {"q": (1024, 1024), "k": (256, 1024), "v": (256, 1024), "o": (1024, 102
 EXPERT_LAYERS = 18  # Gemma-300M (the pi0 action expert): 18 blocks of width 1024
 
 
-def bench_expert(torch, steps):
+def bench_expert(torch, steps, siblings=True):
     """C5: a Gemma-300M-shaped action expert, 18 blocks of width 1024 (q
     1024x1024, k / v 256x1024, o 1024x1024, MLP 1024->4096->1024), installed
     with install_bank as a W4A4 shared bank: every block holds fixed W4A4,
@@ -651,10 +653,13 @@ def bench_expert(torch, steps):
     two binary switchable matrices realising q00/q01/q11/q10, so W2/W4/W8
     versions are all resident in HBM. One denoise step runs the 18 blocks on
     a 50-token chunk; 10 steps follow a seeded q00/q01/q11/q10 schedule, each
-    step one GraphReplay replay of the active configuration's graph; inside
-    it linears that read the same tensor at the same activation width share
-    one quantizer launch (q/k/v on the block input, gate/up on the
-    post-attention residual)."""
+    step one GraphReplay replay of the active configuration's graph. The
+    linears that read the same tensor (q/k/v on the block input, gate/up on
+    the post-attention residual) run as sibling calls (grouped_sibling_forward:
+    one launch over their widths, W4/W8/W4 for q/k/v, where they share the
+    activation width), or with siblings=False as separate module calls that
+    share one quantizer launch per input."""
+    from actune_amd.kernels.grouped import grouped_sibling_forward
     from actune_amd.graph import GraphReplay
     from actune_amd.layers import install_bank
     from actune_amd.precision import CONFIGURATIONS, SharedBank, precision_profile
@@ -671,9 +676,13 @@ def bench_expert(torch, steps):
             # not modelled: only the linears and the block's residual path;
             # the MLP reads the post-attention residual h, as a real block's
             # does, so only q/k/v (on x) and gate/up (on h) share inputs
-            q, _k, _v = self.q(x), self.k(x), self.v(x)
+            if siblings:
+                q, _k, _v = grouped_sibling_forward(x, [self.q, self.k, self.v])
+            else:
+                q, _k, _v = self.q(x), self.k(x), self.v(x)
             h = x + self.o(q * 0.5)
-            return h + self.down(torch.nn.functional.silu(self.gate(h)) * self.up(h))
+            gate, up = grouped_sibling_forward(h, [self.gate, self.up]) if siblings else (self.gate(h), self.up(h))
+            return h + self.down(torch.nn.functional.silu(gate) * up)
 
     class Expert(torch.nn.Module):
         def __init__(self):
@@ -748,7 +757,7 @@ def bench_expert(torch, steps):
     # packed weight + scale bytes each denoise step reads, averaged over the schedule
     active = sum(sum(sizes[nm][configs[q][nm]] for nm in names) for q in schedule) / len(schedule)
     gpu_us = gms * 100
-    return dict(schedule=schedule, layers=EXPERT_LAYERS, linears_per_step=len(names),
+    return dict(schedule=schedule, sibling_calls=siblings, layers=EXPERT_LAYERS, linears_per_step=len(names),
                 ms_per_10_steps=round(ms, 4), us_per_denoise_step=round(ms * 100, 2),
                 gpu_us_per_denoise_step=round(gpu_us, 2),
                 gpu_us_per_linear=round(gpu_us / len(names), 3),
@@ -788,6 +797,12 @@ def main():
         return 0
     if args.tokenwise_only:
         print(json.dumps(dict(tokenwise=bench_tokenwise(torch, _native, args.steps, args.warmup))), flush=True)
+        return 0
+    if args.expert_only:
+        c5 = bench_expert(torch, args.steps)
+        c5["separate_calls"] = {k: v for k, v in bench_expert(torch, args.steps, siblings=False).items()
+                                if k.endswith("per_denoise_step")}
+        print(json.dumps(dict(C5_expert_switching=c5)), flush=True)
         return 0
 
     W, A = args.W, args.A
@@ -882,6 +897,8 @@ def main():
         line["detail"]["C4_gemma_W4A4"] = bench_gemma(torch, _native, 20, 5)
         line["detail"]["C4_gemma_W4A4"]["bank"] = bench_gemma_bank(torch, 20, 3)
         line["detail"]["C5_expert_switching"] = bench_expert(torch, 20)
+        line["detail"]["C5_expert_switching"]["separate_calls"] = {
+            k: v for k, v in bench_expert(torch, 20, siblings=False).items() if k.endswith("per_denoise_step")}
         line["detail"]["tokenwise_family"] = bench_tokenwise(torch, _native, 10, 3)
         line["detail"]["ceilings"] = bench_ceilings(torch)
     if not args.no_cpu_baseline:

@@ -27,13 +27,14 @@ extern "C" {
 enum { ACTUNE_OK = 0, ACTUNE_ERR_INVALID = 1, ACTUNE_ERR_DEVICE = 2 };
 #define ACTUNE_MAX_TARGETS 4
 
-/* One linear of a multi-target call (all targets share x, K, W and A). */
+/* One linear of a multi-target call (all targets share x, K and A). */
 typedef struct actune_linear_target {
   const uint8_t* w;      /* packed weights [N, K*W/8] */
   const float* w_scale;  /* [N] */
   const void* bias;      /* [N] in the call's bias dtype, or NULL */
   void* out;             /* [M, N] in x's dtype */
   int64_t N;
+  int32_t W;             /* this target's weight width (2, 4, 8), or 0 for the call's W */
 } actune_linear_target;
 enum { ACTUNE_DTYPE_BF16 = 0, ACTUNE_DTYPE_F16 = 1, ACTUNE_DTYPE_F32 = 2 };
 #define ACTUNE_CONFIG_AUTO (-1)
@@ -94,6 +95,10 @@ int actune_grouped_forward(const void* x, int x_dtype, const void* input_scale, 
  * decode configs, for bf16 x wherever the decode kernel's activation passes
  * cover a wave's K-range; otherwise a_buf / scale_buf receive the packed
  * activations and scales.
+ * Targets may differ in weight width (actune_linear_target.W; W sizes the
+ * call, the widest width when they differ): one decode launch over every
+ * width where the decode config takes each of them (in-launch quantization
+ * as above), else one quantization and one launch per width on its codes.
  */
 int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_scale, uint8_t* a_buf,
                                  float* scale_buf, const actune_linear_target* targets, int ntargets,

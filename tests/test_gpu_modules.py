@@ -483,7 +483,7 @@ def test_sibling_forward_equals_separate_calls(m):
             sep = [model.k(x), model.v(x), model.gate(x), model.up(x), model.q(x)]
             sep_counts = {n: (mod.calls, mod.input_elements) for n, mod in runtime.modules.items()}
             runtime.before()
-            kv = grouped_sibling_forward(x, [model.k, model.v])  # w8a4 + w4a4: separate launches
+            kv = grouped_sibling_forward(x, [model.k, model.v])  # w8a4 + w4a4: one launch over both widths
             gu = grouped_sibling_forward(x, [model.gate, model.up])  # fused when (W, A) agree
             qq = grouped_sibling_forward(x, [model.q])
             counts = {n: (mod.calls, mod.input_elements) for n, mod in runtime.modules.items()}

@@ -276,6 +276,69 @@ def test_multi_target_equals_separate_calls(m, W, A):
         assert torch.equal(out, _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A))
 
 
+# widths of q/k/v-like sibling targets, output widths, K
+MIXED = [((4, 8, 4), (1024, 256, 256), 1024), ((2, 4), (96, 200), 512), ((8, 2, 4, 8), (64, 48, 160, 32), 4096),
+         ((4, 8), (4096, 4096), 4096)]
+
+
+@pytest.mark.parametrize("m", [1, 3, 8, 13, 50, 100])
+@pytest.mark.parametrize("A", [4, 8, 2])
+@pytest.mark.parametrize("case", range(len(MIXED)))
+def test_mixed_width_multi_against_oracle(m, A, case):
+    """Sibling targets of different weight widths at one A in one call (one
+    decode launch where the kernel takes every width, else one quantization
+    and a launch per width): every output equals its own single-width
+    forward bit for bit and the oracle in the canonical order, with and
+    without the channel scale."""
+    widths, ns, k = MIXED[case]
+    if m == 100 and k == 4096 and max(ns) == 4096:
+        pytest.skip("covered at the smaller M (oracle time)")
+    x, _, _ = seeded_inputs(m, k, 1, seed=m * 13 + A + case)
+    scale = torch.linspace(0.5, 2.0, k).to(torch.bfloat16)
+    xd = x.to(DEV)
+    targets, oracle_side = [], []
+    for j, (W, n) in enumerate(zip(widths, ns)):
+        _, w, b = seeded_inputs(1, k, n, seed=900 + 10 * case + j, bias=j % 2 == 1)
+        codes, wscale, w_dev, ws_dev = _packed_weight(w, W, A)
+        targets.append((w_dev, ws_dev, None if b is None else b.to(DEV), None, W))
+        oracle_side.append((codes, wscale, b))
+    biases = {t[2] is None for t in targets}
+    if len(biases) > 1:  # one bias dtype (or none) per call: give every target a bias
+        targets = [(t[0], t[1], torch.zeros(t[0].shape[0], device=DEV).to(torch.bfloat16) if t[2] is None else t[2],
+                    None, t[4]) for t in targets]
+    cols_all = max(ns) <= 1024
+    for sd in (None, scale.to(DEV)):
+        outs = _native.grouped_forward_multi(xd, targets, widths[0], A, input_scale=sd)
+        _, a_scales, a_codes = oracle_activation(x, A, None if sd is None else scale)
+        for (w_dev, ws_dev, bd, _, W), (codes, wscale, _), out in zip(targets, oracle_side, outs):
+            single = _native.grouped_forward(xd, w_dev, ws_dev, bd, W, A, input_scale=sd)
+            assert torch.equal(out, single), (W, sd is None)
+            n = w_dev.shape[0]
+            cols = None if cols_all else np.sort(np.random.default_rng(n + m).choice(n, size=64, replace=False))
+            bias = None if bd is None else bd.float().cpu().numpy()
+            want = O.linear(a_codes, a_scales, codes, wscale, bias, bounds=canonical_bounds(k // 64), cols=cols)
+            got = bits(out) if cols is None else bits(out)[:, cols]
+            np.testing.assert_array_equal(got, O.round_out(want, "bf16"), err_msg=f"W{W} n={n}")
+
+
+@pytest.mark.parametrize("config", [-1, 14, 15, 16, 0, 7, 10])
+def test_mixed_width_multi_explicit_configs(config):
+    """Mixed widths under explicit configs: the decode configs (one launch
+    where each width fits, else per-width launches), the small-M, streaming
+    and prefill configs (per-width launches on one quantization): outputs
+    equal the single-width calls with the same config."""
+    m, k, A = 8, 1024, 4
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(config + 50)).to(torch.bfloat16).to(DEV)
+    targets = []
+    for j, (W, n) in enumerate(zip((4, 8, 2), (256, 64, 128))):
+        _, w, _ = seeded_inputs(1, k, n, seed=950 + j)
+        _, _, w_dev, ws_dev = _packed_weight(w, W, A)
+        targets.append((w_dev, ws_dev, None, None, W))
+    outs = _native.grouped_forward_multi(x, targets, 4, A, config=config)
+    for (w_dev, ws_dev, _, _, W), out in zip(targets, outs):
+        assert torch.equal(out, _native.grouped_forward(x, w_dev, ws_dev, None, W, A, config=config)), W
+
+
 @pytest.mark.parametrize("m", [1, 8])
 @pytest.mark.parametrize("n,k,count", [(4096, 4096, 3), (11008, 4096, 2)])
 def test_full_size_sibling_launches_against_oracle(m, n, k, count):
