@@ -49,6 +49,7 @@ def lib():
         so.actune_version.restype = ctypes.c_char_p
         so.actune_last_error.restype = ctypes.c_char_p
         so.actune_quantize_groups.argtypes = [_P, _I, _P, _I64, _I64, _I, _P, _P, _P]
+        so.actune_quantize_gated.argtypes = [_P, _P, _I, _I, _P, _I64, _I64, _I, _P, _P, _P]
         so.actune_grouped_linear.argtypes = [_P, _P, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I, _I, _I, _P]
         so.actune_grouped_forward.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _I64, _I64,
                                               _I, _I, _I, _P]
@@ -238,6 +239,31 @@ def quantize_groups(x: torch.Tensor, a: int, input_scale: torch.Tensor | None = 
     packed, scales = _act_buffers(packed, scales, m, k, a, x.device)
     _check(lib().actune_quantize_groups(_ptr(x), _dtype_code(x), _ptr(input_scale), m, k, a,
                                         _ptr(packed), _ptr(scales), _stream(x.device)))
+    return packed, scales
+
+
+ACT_SILU, ACT_GELU_TANH = 0, 1
+
+
+def quantize_gated(gate: torch.Tensor, up: torch.Tensor, act: int, a: int, input_scale: torch.Tensor | None = None,
+                   packed: torch.Tensor | None = None, scales: torch.Tensor | None = None):
+    """Group-64 codes of p = act(gate) * up (ACT_SILU or ACT_GELU_TANH, p
+    formed in the inputs' dtype as torch forms it) through
+    actune_quantize_gated: equal to quantize_groups on a tensor holding p.
+    gate, up: contiguous [M, K] of one dtype. Returns (packed, scales)."""
+    _require_cuda(gate, up, input_scale, packed, scales)
+    _check_widths(8, a)
+    _check_flat(gate)
+    if up.shape != gate.shape or up.dtype != gate.dtype or not up.is_contiguous():
+        raise RuntimeError("up must match gate (contiguous [M, K], same dtype)")
+    if act not in (ACT_SILU, ACT_GELU_TANH):
+        raise ValueError("unknown gate activation")
+    m, k = gate.shape
+    _check_input_scale(input_scale, gate)
+    gate, up, input_scale = _aligned16(gate), _aligned16(up), _aligned16(input_scale)
+    packed, scales = _act_buffers(packed, scales, m, k, a, gate.device)
+    _check(lib().actune_quantize_gated(_ptr(gate), _ptr(up), _dtype_code(gate), act, _ptr(input_scale), m, k, a,
+                                       _ptr(packed), _ptr(scales), _stream(gate.device)))
     return packed, scales
 
 

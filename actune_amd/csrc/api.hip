@@ -363,6 +363,17 @@ int actune_quantize_groups(const void* x, int x_dtype, const void* input_scale, 
   return check_launch();
 }
 
+int actune_quantize_gated(const void* gate, const void* up, int x_dtype, int act, const void* input_scale,
+                          int64_t M, int64_t K, int A, uint8_t* packed, float* scales, void* stream) {
+  g_err[0] = 0;
+  if (act != ACTUNE_ACT_SILU && act != ACTUNE_ACT_GELU_TANH) return fail(ACTUNE_ERR_INVALID, "unknown gate activation");
+  int rc = check_quantize(gate, x_dtype, input_scale, M, K, A, packed, scales);
+  if (!rc && M > 0 && (!up || !aligned(up, 16))) rc = fail(ACTUNE_ERR_INVALID, "null or misaligned up operand");
+  if (rc || M == 0) return rc;
+  launch_quantize_gated(gate, up, x_dtype, act, input_scale, M, K, A, packed, scales, (hipStream_t)stream);
+  return check_launch();
+}
+
 int actune_grouped_linear(const uint8_t* a, const float* a_scales, const uint8_t* w,
                           const float* w_scale, const void* bias, int bias_dtype, void* out,
                           int out_dtype, int64_t M, int64_t N, int64_t K, int W, int A, int config,

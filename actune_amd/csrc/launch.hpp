@@ -96,6 +96,8 @@ void set_last_error(const char* msg);
 
 void launch_quantize(const void* x, int dt, const void* sc, long M, long K, int A, uint8_t* packed,
                      float* scales, hipStream_t stream);
+void launch_quantize_gated(const void* gate, const void* up, int dt, int act, const void* sc, long M, long K, int A,
+                           uint8_t* packed, float* scales, hipStream_t stream);
 void launch_smallm(int W, int A, int nw, int mode, const LinearArgs& g, hipStream_t st);
 void launch_tiled(int W, int A, int shape, bool dots, const LinearArgs& g, hipStream_t st);
 void launch_stream(int W, int A, int nw, int mode, const LinearArgs& g, hipStream_t st);

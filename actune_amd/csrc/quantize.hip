@@ -14,27 +14,22 @@
 // groups (1 KiB of bf16), and the group absmax is a 3-step DPP reduction
 // inside the 8-lane segment. Stores are contiguous per wave:
 // A8 writes 8 B/lane, A4 4 B/lane, A2 2 B/lane.
+#include <math.h>
+
+#include "../../include/actune_hip.h"
 #include "common.hpp"
 #include "launch.hpp"
 #include "operands.hpp"
 
 namespace actune {
 
+// One lane's 8 values v of group gi (segment seg, columns k0..k0+7): the
+// channel-scale division when SCALE, the group's codes packed and stored,
+// and the scale stored by segment 0.
 template <int A, int DT, bool SCALE>
-__global__ __launch_bounds__(256) void quantize_groups_kernel(const void* __restrict__ x,
-                                                              const void* __restrict__ input_scale,
-                                                              long groups, int G,
-                                                              uint8_t* __restrict__ packed,
-                                                              float* __restrict__ scales) {
-  const long gi = (long)blockIdx.x * 32 + (threadIdx.x >> 3);  // global group index m*G + g
-  const int seg = threadIdx.x & 7;                               // 8-element segment in the group
-  const bool live = gi < groups;
-  const long gsafe = live ? gi : groups - 1;
-  const long e0 = gsafe * kGroup + seg * 8;                      // first element of this lane
-  const int k0 = (int)(gsafe % G) * kGroup + seg * 8;            // its column (for input_scale)
-
-  float v[8];
-  load8<DT>(x, e0, v);
+__device__ __forceinline__ void quantize_lane(float (&v)[8], const void* __restrict__ input_scale, int k0,
+                                              bool live, long gi, int seg, uint8_t* __restrict__ packed,
+                                              float* __restrict__ scales) {
   if constexpr (SCALE) {
     float d[8];
     load8<DT>(input_scale, k0, d);
@@ -62,6 +57,80 @@ __global__ __launch_bounds__(256) void quantize_groups_kernel(const void* __rest
   if (seg == 0) scales[gi] = s;
 }
 
+// Lane geometry shared by the quantizers: 8 lanes per group, 32 groups per
+// 256-thread workgroup; a lane past the last group works on the last group
+// and stores nothing.
+struct LaneGroup {
+  long gi, e0;
+  int seg, k0;
+  bool live;
+  __device__ LaneGroup(long groups, int G) {
+    gi = (long)blockIdx.x * 32 + (threadIdx.x >> 3);  // global group index m*G + g
+    seg = threadIdx.x & 7;                             // 8-element segment in the group
+    live = gi < groups;
+    const long gsafe = live ? gi : groups - 1;
+    e0 = gsafe * kGroup + seg * 8;                     // first element of this lane
+    k0 = (int)(gsafe % G) * kGroup + seg * 8;          // its column (for input_scale)
+  }
+};
+
+template <int A, int DT, bool SCALE>
+__global__ __launch_bounds__(256) void quantize_groups_kernel(const void* __restrict__ x,
+                                                              const void* __restrict__ input_scale,
+                                                              long groups, int G,
+                                                              uint8_t* __restrict__ packed,
+                                                              float* __restrict__ scales) {
+  const LaneGroup lg(groups, G);
+  float v[8];
+  load8<DT>(x, lg.e0, v);
+  quantize_lane<A, DT, SCALE>(v, input_scale, lg.k0, lg.live, lg.gi, lg.seg, packed, scales);
+}
+
+// Gate activation of a gated MLP in fp32, as torch's GPU kernels compute it
+// for torch.nn.functional.silu and gelu(approximate="tanh") (opmath float):
+// SiLU x / (1 + e^-x); GELU 0.5 x (1 + tanh(b fma(k, x^3, x))) with
+// b = sqrt(2) * 2/sqrt(pi) * 0.5 and k = 0.044715 rounded to fp32, the
+// inner multiply-add fused as torch's build fuses it (checked against
+// torch on MI355X for every fp32 value of an f16 input). The fp32 result is
+// pinned in a register so that the rounding to f16 that follows stays a
+// separate step: a multiply folded into the conversion (v_fma_mix) would
+// round once from the exact product where torch rounds twice.
+template <int ACT>
+__device__ __forceinline__ float gate_act(float x) {
+  float y;
+  if constexpr (ACT == ACTUNE_ACT_SILU) {
+    y = x / (1.0f + expf(-x));
+  } else {
+    constexpr float kBeta = (float)(M_SQRT2 * M_2_SQRTPI * 0.5);
+    constexpr float kKappa = 0.044715f;
+    const float cube = x * x * x;
+    const float inner = kBeta * __builtin_fmaf(kKappa, cube, x);
+    y = 0.5f * x * (1.0f + tanhf(inner));
+  }
+  asm volatile("" : "+v"(y));
+  return y;
+}
+
+// Quantizer of the down projection's input p = act(gate) * up of a gated MLP:
+// p is formed in the inputs' dtype as torch forms it (act rounded to the
+// dtype, then the product rounded), then quantized exactly as
+// quantize_groups_kernel quantizes a tensor holding p.
+template <int A, int DT, int ACT, bool SCALE>
+__global__ __launch_bounds__(256) void quantize_gated_kernel(const void* __restrict__ gate,
+                                                             const void* __restrict__ up,
+                                                             const void* __restrict__ input_scale,
+                                                             long groups, int G,
+                                                             uint8_t* __restrict__ packed,
+                                                             float* __restrict__ scales) {
+  const LaneGroup lg(groups, G);
+  float v[8], u[8];
+  load8<DT>(gate, lg.e0, v);
+  load8<DT>(up, lg.e0, u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = round_to_dtype<DT>(round_to_dtype<DT>(gate_act<ACT>(v[e])) * u[e]);
+  quantize_lane<A, DT, SCALE>(v, input_scale, lg.k0, lg.live, lg.gi, lg.seg, packed, scales);
+}
+
 template <int A, int DT>
 static void launch_quantize_dt(const void* x, const void* sc, long M, long K, uint8_t* packed,
                                float* scales, hipStream_t stream) {
@@ -86,6 +155,39 @@ void launch_quantize(const void* x, int dt, const void* sc, long M, long K, int 
   if (A == 8) launch_quantize_a<8>(x, dt, sc, M, K, packed, scales, stream);
   else if (A == 4) launch_quantize_a<4>(x, dt, sc, M, K, packed, scales, stream);
   else launch_quantize_a<2>(x, dt, sc, M, K, packed, scales, stream);
+}
+
+template <int A, int DT, int ACT>
+static void launch_gated_t(const void* gate, const void* up, const void* sc, long M, long K, uint8_t* packed,
+                           float* scales, hipStream_t stream) {
+  const long groups = M * (K / kGroup);
+  const dim3 grid((unsigned)((groups + 31) / 32));
+  if (sc)
+    quantize_gated_kernel<A, DT, ACT, true><<<grid, 256, 0, stream>>>(gate, up, sc, groups, (int)(K / kGroup), packed, scales);
+  else
+    quantize_gated_kernel<A, DT, ACT, false><<<grid, 256, 0, stream>>>(gate, up, sc, groups, (int)(K / kGroup), packed, scales);
+}
+
+template <int A, int DT>
+static void launch_gated_dt(const void* gate, const void* up, int act, const void* sc, long M, long K,
+                            uint8_t* packed, float* scales, hipStream_t stream) {
+  if (act == ACTUNE_ACT_SILU) launch_gated_t<A, DT, ACTUNE_ACT_SILU>(gate, up, sc, M, K, packed, scales, stream);
+  else launch_gated_t<A, DT, ACTUNE_ACT_GELU_TANH>(gate, up, sc, M, K, packed, scales, stream);
+}
+
+template <int A>
+static void launch_gated_a(const void* gate, const void* up, int dt, int act, const void* sc, long M, long K,
+                           uint8_t* packed, float* scales, hipStream_t stream) {
+  if (dt == kBF16) launch_gated_dt<A, kBF16>(gate, up, act, sc, M, K, packed, scales, stream);
+  else if (dt == kF16) launch_gated_dt<A, kF16>(gate, up, act, sc, M, K, packed, scales, stream);
+  else launch_gated_dt<A, kF32>(gate, up, act, sc, M, K, packed, scales, stream);
+}
+
+void launch_quantize_gated(const void* gate, const void* up, int dt, int act, const void* sc, long M, long K, int A,
+                           uint8_t* packed, float* scales, hipStream_t stream) {
+  if (A == 8) launch_gated_a<8>(gate, up, dt, act, sc, M, K, packed, scales, stream);
+  else if (A == 4) launch_gated_a<4>(gate, up, dt, act, sc, M, K, packed, scales, stream);
+  else launch_gated_a<2>(gate, up, dt, act, sc, M, K, packed, scales, stream);
 }
 
 }  // namespace actune

@@ -13,6 +13,8 @@ passes one) and the packed GEMM, both launched on the current HIP stream.
 """
 from __future__ import annotations
 
+import functools
+
 from contextlib import contextmanager
 from contextvars import ContextVar
 from types import MethodType
@@ -268,11 +270,62 @@ def _zero_padded(linear, padded):
     return fc
 
 
+def _gate_kind(act_fn):
+    """The gated quantizer's code for an activation whose torch form it
+    reproduces (SiLU; GELU with the tanh approximation, Gemma's
+    gelu_pytorch_tanh), else None."""
+    silu = (torch.nn.functional.silu, torch.nn.SiLU)
+    if act_fn is silu[0] or type(act_fn) is silu[1] or type(act_fn).__name__ == "SiLUActivation":
+        return _native.ACT_SILU
+    if type(act_fn) is torch.nn.GELU and act_fn.approximate == "tanh":
+        return _native.ACT_GELU_TANH
+    inner = getattr(act_fn, "act", None)  # transformers' GELUTanh holds partial(gelu, approximate="tanh")
+    if (type(act_fn).__name__ in ("GELUTanh", "PytorchGELUTanh") and isinstance(inner, functools.partial)
+            and inner.func is torch.nn.functional.gelu and inner.keywords == {"approximate": "tanh"}):
+        return _native.ACT_GELU_TANH
+    return None
+
+
+def gated_down_forward(down, gate, up, act_fn):
+    """down(act_fn(gate) * up) for a gated MLP, the product formed in gate's
+    dtype as torch forms it (act_fn(gate), then gate.mul_(up), grouped.py:
+    22-25). Where down is a GroupedPaddedLinear (or ResidentLinear) without
+    K padding whose active version is a GroupedLinear, and act_fn is one the
+    gated quantizer knows, the activation and the product are formed inside
+    down's quantizer launch (actune_quantize_gated: one launch in place of
+    three) and down runs on its codes; the output is bit-identical to the
+    unfused calls and down's calls / input_elements advance as for one call.
+    Otherwise the unfused calls run."""
+    kind = _gate_kind(act_fn)
+    backend = down.active_backend() if isinstance(down, GroupedPaddedLinear) else None
+    scale = getattr(down, "input_scale", None)
+    fused = (kind is not None and backend is not None and not down.padding and gate.is_cuda
+             and getattr(backend.forward, "__func__", None) is GroupedLinear.forward
+             and gate.shape == up.shape and gate.dtype == up.dtype and gate.shape[-1] == down.in_features
+             and gate.dtype in (torch.bfloat16, torch.float16, torch.float32)
+             and (scale is None or scale.dtype == gate.dtype) and gate.numel() > 0)
+    if not fused:
+        product = act_fn(gate)
+        product.mul_(up)
+        return down(product)
+    down.calls += 1
+    down.input_elements += gate.numel()
+    flat_gate = gate.reshape(-1, down.in_features).contiguous()
+    flat_up = up.reshape(-1, down.in_features).contiguous()
+    packed, scales = _native.quantize_gated(flat_gate, flat_up, kind, backend.a, input_scale=scale)
+    out = _native.grouped_linear(packed, scales, backend.packed_weight, backend.weight_scale, backend.bias,
+                                 flat_gate, backend.w, backend.a, backend.config)
+    return out.reshape(*gate.shape[:-1], down.out_features)
+
+
 def _inference_mlp(self, x):
-    """GemmaMLP forward that reuses the gate activation as the product's
-    buffer (grouped.py:18-25); gate/up run as sibling projections (one
-    launch when their active versions match, else shared codes inside a
-    shared_activation_scope), bit-identical to the separate calls."""
+    """GemmaMLP forward of the reference's patch (grouped.py:18-25): gate/up
+    run as sibling projections (one launch when their activation widths
+    match, else shared codes inside a shared_activation_scope), and the
+    activation times up feeds the down projection through
+    gated_down_forward (formed inside down's quantizer where it can be, else
+    in the gate buffer as the reference reuses it); bit-identical to the
+    unpatched forward."""
     if torch.is_grad_enabled():
         return self._group64_original_forward(x)
     gate_proj, up_proj = self.gate_proj, self.up_proj
@@ -280,9 +333,7 @@ def _inference_mlp(self, x):
         gate, up = grouped_sibling_forward(x, [gate_proj, up_proj])
     else:
         gate, up = gate_proj(x), up_proj(x)
-    gate = self.act_fn(gate)
-    gate.mul_(up)
-    return self.down_proj(gate)
+    return gated_down_forward(self.down_proj, gate, up, self.act_fn)
 
 
 def reuse_mlp_temporary(model):
@@ -307,8 +358,8 @@ def grouped_sibling_forward(x, modules):
     dtype and input scale, all of them run in one actune_grouped_forward_multi
     call (up to 4 targets): one quantize + GEMM launch, also where their
     weight widths differ (q/k/v of a mixed-precision bank) and the decode
-    kernel takes every width; otherwise each module runs on its own. Either way the outputs are bit-identical to calling the
-    modules one by one, and each module's calls / input_elements counters
+    kernel takes every width; otherwise each module runs on its own. Either
+    way the outputs are bit-identical to calling the modules one by one, and each module's calls / input_elements counters
     advance exactly as for a separate call (BankRuntime.audit relies on them).
     """
     modules = list(modules)

@@ -658,8 +658,11 @@ def bench_expert(torch, steps, siblings=True):
     the post-attention residual) run as sibling calls (grouped_sibling_forward:
     one launch over their widths, W4/W8/W4 for q/k/v, where they share the
     activation width), or with siblings=False as separate module calls that
-    share one quantizer launch per input."""
-    from actune_amd.kernels.grouped import grouped_sibling_forward
+    share one quantizer launch per input. The MLP is Gemma's gated form,
+    down(gelu_tanh(gate) * up); with siblings the activation and the product
+    are formed inside down's quantizer (gated_down_forward)."""
+    from actune_amd.kernels.grouped import gated_down_forward, grouped_sibling_forward
+    gelu = torch.nn.GELU(approximate="tanh")  # Gemma's gelu_pytorch_tanh
     from actune_amd.graph import GraphReplay
     from actune_amd.layers import install_bank
     from actune_amd.precision import CONFIGURATIONS, SharedBank, precision_profile
@@ -681,8 +684,10 @@ def bench_expert(torch, steps, siblings=True):
             else:
                 q, _k, _v = self.q(x), self.k(x), self.v(x)
             h = x + self.o(q * 0.5)
-            gate, up = grouped_sibling_forward(h, [self.gate, self.up]) if siblings else (self.gate(h), self.up(h))
-            return h + self.down(torch.nn.functional.silu(gate) * up)
+            if not siblings:
+                return h + self.down(gelu(self.gate(h)) * self.up(h))
+            gate, up = grouped_sibling_forward(h, [self.gate, self.up])
+            return h + gated_down_forward(self.down, gate, up, gelu)
 
     class Expert(torch.nn.Module):
         def __init__(self):

@@ -57,6 +57,23 @@ int actune_quantize_groups(const void* x, int x_dtype, const void* input_scale, 
                            int A, uint8_t* packed, float* scales, void* stream);
 
 /*
+ * Group-64 quantizer of a gated MLP's down-projection input p = act(gate) *
+ * up: the product is formed in x_dtype as torch forms it (the activation in
+ * fp32, rounded to x_dtype, times up, rounded to x_dtype), optionally divided
+ * by input_scale as actune_quantize_groups divides, and quantized exactly as
+ * actune_quantize_groups would quantize a tensor holding p. gate and up:
+ * [M, K], 16-byte aligned. act: ACTUNE_ACT_SILU (torch.nn.functional.silu)
+ * or ACTUNE_ACT_GELU_TANH (gelu(approximate="tanh"), Gemma's
+ * gelu_pytorch_tanh). No reference counterpart: it folds the activation and
+ * the product of the reference's patched MLP forward
+ * (actune/kernels/grouped.py:18-25) into the down projection's quantizer
+ * launch (grouped.py:132-133), three launches into one.
+ */
+enum { ACTUNE_ACT_SILU = 0, ACTUNE_ACT_GELU_TANH = 1 };
+int actune_quantize_gated(const void* gate, const void* up, int x_dtype, int act, const void* input_scale,
+                          int64_t M, int64_t K, int A, uint8_t* packed, float* scales, void* stream);
+
+/*
  * Packed grouped linear. Replaces the native op `linear(a, as, w, ws, bias,
  * source, W, A[, config])` of actune/kernels/grouped_native.cu:90-115 and
  * grouped_big_m.cu:92-135, and the _group_gemm Triton launch of
