@@ -19,10 +19,17 @@ size_t decode_lds_bytes(int K, int M, int nw, int tr) {
 // on MI355X, W4A8 M=8: 256 row tiles run best one per workgroup, 688-1376
 // with four).
 constexpr int kDecodeMinGroups = 160;
+constexpr size_t kCuLds = 160 * 1024;  // LDS of one gfx950 CU
 
 // Row tiles per workgroup for M > 1: the most (up to 4) whose weight slots
 // still fit the ring, keeping at least kDecodeMinGroups workgroups over the
-// nprob problems of `tiles` row tiles each.
+// nprob problems of `tiles` row tiles each. With 16-token tiles, four row
+// tiles' chunk partials (64 KiB) can leave room for one workgroup per CU;
+// where two row tiles still fit two workgroups per CU and their grid fills
+// two per CU, two are taken (measured on MI355X, W4A4 gate/up 2 x 4096 x 1024
+// at M = 50, four waves: 13.2 -> 10.6 us; at M = 24, 11008 x 4096, where two
+// tiles also leave one workgroup per CU, four stay faster: 19.1 against
+// 28.2 us for one).
 int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob) {
   if (M < 2) return 1;
   const int slots = (decode_groups_per_wave(K, nw) + 8 / W - 1) / (8 / W);
@@ -31,6 +38,9 @@ int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob) {
     if (slots * c <= decode_ring(W) && (tiles + c - 1) / c * nprob >= kDecodeMinGroups &&
         decode_lds_bytes(K, M, nw, c) <= kStreamLdsMax)
       tr = c;
+  if (tr == 4 && M > 8 && 2 * decode_lds_bytes(K, M, nw, 4) > kCuLds && 2 * decode_lds_bytes(K, M, nw, 2) <= kCuLds &&
+      (tiles + 1) / 2 * nprob >= 2 * 256)
+    tr = 2;
   return tr;
 }
 

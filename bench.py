@@ -620,12 +620,55 @@ def bench_tokenwise(torch, _native, steps, warmup):
             row["us_quantizer_fused"] = round(us_f, 2)
         return row
 
+    def siblings(count, n, k, residual):
+        """One decode row of `count` sibling projections (W4A8, the row
+        quantized inside the launch): ONE multi-target GEMM launch + one
+        reduce, against one split GEMM + reduce per projection; with
+        residual, the signed-R4 layout (every projection carries r4)."""
+        wl = _native.TW_KMAJOR_W4R4 if residual else _native.TW_KMAJOR_W4
+        nbytes = n * k // 2 * (2 if residual else 1)
+        copies = max(4, (300 << 20) // (count * nbytes))
+        groups = [[(torch.randint(0, 256, (k // 2, n), generator=g, device="cuda", dtype=torch.uint8),
+                    torch.rand(n, generator=g, device="cuda") * 0.01 + 0.005,
+                    torch.randint(0, 256, (k // 2, n), generator=g, device="cuda", dtype=torch.uint8)
+                    if residual else None) for _ in range(count)] for _ in range(copies)]
+        x = torch.randn(1, k, generator=g, device="cuda").to(torch.bfloat16)
+        sc = torch.empty(1, device="cuda")
+        outs = [torch.empty(1, n, device="cuda", dtype=torch.bfloat16) for _ in range(count)]
+        need = _native.tokenwise_workspace_bytes(1, n, k, wl, _native.TW_ACT_A8)
+        work = torch.zeros(max(count * need, 256), dtype=torch.uint8, device="cuda")
+
+        def grouped():
+            for grp in groups:
+                _native.tokenwise_linear_multi([(w, s, None, o) for (w, s, _), o in zip(grp, outs)], wl, n, k,
+                                               _native.TW_EPI_A8, sc, x=x, workspace=work if need else None,
+                                               residuals=[r for _, _, r in grp] if residual else None)
+
+        def separate():
+            for grp in groups:
+                for (w, s, r), o in zip(grp, outs):
+                    if residual:
+                        _native.tokenwise_linear_multi([(w, s, None, o)], wl, n, k, _native.TW_EPI_A8, sc, x=x,
+                                                       workspace=work if need else None, residuals=[r])
+                    else:
+                        _native.tokenwise_linear_x(x, sc, w, wl, s, None, n, k, _native.TW_EPI_A8, o,
+                                                   workspace=work if need else None)
+
+        us_g = time_launches(torch, grouped, steps, warmup) / copies
+        us_s = time_launches(torch, separate, steps, warmup) / copies
+        return dict(us_group=round(us_g, 2), us_per_linear=round(us_g / count, 2), us_separate=round(us_s, 2),
+                    launches_group=2 if need else 1, launches_separate=count * (2 if need else 1),
+                    weight_GBps=round(count * nbytes / us_g / 1e3, 1))
+
     for m in (1, 8):
         row = {}
         for _, n, k in (SHAPES[0], SHAPES[4], SHAPES[6]):
             copies = max(12, (300 << 20) // (n * k // 2))
             row[f"{n}x{k}"] = run("W4A8", 4, 8, m, n, k, copies)
         out[f"W4A8_M={m}"] = row
+    out["W4A8_M=1_siblings"] = {"qkv_3x4096x4096": siblings(3, 4096, 4096, False),
+                                "gate_up_2x11008x4096": siblings(2, 11008, 4096, False),
+                                "qkv_W4R4_3x4096x4096": siblings(3, 4096, 4096, True)}
     row = {}  # M = 256: half a workgroup per CU at N = 4096, where the GEMM splits K in two
     for _, n, k in (SHAPES[0], SHAPES[4], SHAPES[6]):
         row[f"{n}x{k}"] = run("W4A8", 4, 8, 256, n, k, 4)
