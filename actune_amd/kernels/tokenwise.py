@@ -239,12 +239,38 @@ def _require_cuda(value, what):
         raise ValueError(f"{what} requires a CUDA input")
 
 
-_KMAJOR_WIDTH_MSG = "K-major tokenwise weights need out_features divisible by 16 on this backend"
+def _kernel_operands(module, weight, bias):
+    """(weight, weight_scale, bias, N) as a K-major GEMM launch takes them.
+    The kernels read 16 output columns per 16-byte chunk of a K-major row, so
+    a layer whose out_features is not a multiple of 16 (the reference takes
+    any width, w4a8_triton.py:57-158) runs on copies of its weights, scale
+    and bias zero-padded to the next multiple of 16; the caller keeps the
+    first out_features columns of the result. The copies are made once per
+    version of the buffers and held outside the module's buffers, so state
+    dicts and storage counts stay the reference's."""
+    n = module.out_features
+    if n % 16 == 0:
+        return weight, module.weight_scale, bias, n
+    key = tuple(None if t is None else (t.data_ptr(), t._version) for t in (weight, module.weight_scale, bias))
+    cached = module.__dict__.get("_padded_operands")
+    if cached is None or cached[0] != key:
+        n16 = -(-n // 16) * 16
+
+        def padded(t):
+            if t is None:
+                return None
+            out = t.new_zeros(*t.shape[:-1], n16)
+            out[..., :n] = t
+            return out
+
+        cached = (key, (padded(weight), padded(module.weight_scale), padded(bias), n16))
+        module.__dict__["_padded_operands"] = cached
+    return cached[1]
 
 
-def _kmajor_width_ok(out_features):
-    if out_features % 16:
-        raise ValueError(_KMAJOR_WIDTH_MSG)
+def _first_columns(out, n):
+    """out [M, N'] cut to its first n columns (contiguous)."""
+    return out if out.shape[1] == n else out[:, :n].contiguous()
 
 
 # ---------------------------------------------------------------- shared per-row codes
@@ -393,21 +419,20 @@ class _TokenwiseA8(torch.nn.Module):
         original_shape = value.shape[:-1]
         flat = value.reshape(-1, self.in_features)
         m = flat.shape[0]
-        weight = getattr(self, self._weight_name)
+        weight, wscale, bias, n = _kernel_operands(self, getattr(self, self._weight_name), self.bias)
         if self._fuses_rows(flat):
-            out = torch.empty((m, self.out_features), device=flat.device, dtype=value.dtype)
+            out = torch.empty((m, n), device=flat.device, dtype=value.dtype)
             scale = torch.empty(m, device=flat.device, dtype=torch.float32)
-            ws = _split_workspace(m, self.out_features, self.in_features, self._layout, _native.TW_ACT_A8,
-                                  flat.device)
-            _native.tokenwise_linear_x(flat.contiguous(), scale, weight, self._layout, self.weight_scale, self.bias,
-                                       self.out_features, self.in_features, _native.TW_EPI_A8, out, workspace=ws)
-            return out.reshape(*original_shape, self.out_features)
+            ws = _split_workspace(m, n, self.in_features, self._layout, _native.TW_ACT_A8, flat.device)
+            _native.tokenwise_linear_x(flat.contiguous(), scale, weight, self._layout, wscale, bias, n,
+                                       self.in_features, _native.TW_EPI_A8, out, workspace=ws)
+            return _first_columns(out, self.out_features).reshape(*original_shape, self.out_features)
         activation, scale = self._quantize(flat, source=value)
         if self._layout == _native.TW_KMAJOR_W4 and decode_eligible(flat, k=self.in_features, n=self.out_features):
             _count_split_decode(1, self.out_features, self.in_features)
-        output = _gemm(activation, _native.TW_ACT_A8, scale, weight, self._layout, self.weight_scale, self.bias,
-                       self.out_features, self.in_features, _native.TW_EPI_A8, value.dtype)
-        return output.reshape(*original_shape, self.out_features)
+        output = _gemm(activation, _native.TW_ACT_A8, scale, weight, self._layout, wscale, bias, n,
+                       self.in_features, _native.TW_EPI_A8, value.dtype)
+        return _first_columns(output, self.out_features).reshape(*original_shape, self.out_features)
 
 
 class W4A8TritonLinear(_TokenwiseA8):
@@ -424,7 +449,6 @@ class W4A8TritonLinear(_TokenwiseA8):
         super().__init__()
         if linear.in_features % 32:
             raise ValueError("in_features must be divisible by 32")
-        _kmajor_width_ok(linear.out_features)
         self.in_features = linear.in_features
         self.out_features = linear.out_features
         self.fused_quantization = fused_quantization
@@ -456,7 +480,6 @@ class W8A8TritonLinear(_TokenwiseA8):
         super().__init__()
         if linear.in_features % 128:
             raise ValueError("in_features must be divisible by 128")
-        _kmajor_width_ok(linear.out_features)
         self.in_features = linear.in_features
         self.out_features = linear.out_features
         self.fused_quantization = fused_quantization
@@ -481,7 +504,6 @@ class W2A8TritonLinear(_TokenwiseA8):
         super().__init__()
         if linear.in_features % 128:
             raise ValueError("in_features must be divisible by 128")
-        _kmajor_width_ok(linear.out_features)
         self.in_features = linear.in_features
         self.out_features = linear.out_features
         self.fused_quantization = fused_quantization
@@ -595,7 +617,6 @@ class W8A4NativeLinear(torch.nn.Module):
         super().__init__()
         if linear.in_features % 128:
             raise ValueError("W8A4 S8 MMA requires in_features divisible by 128")
-        _kmajor_width_ok(linear.out_features)
         self.in_features = linear.in_features
         self.out_features = linear.out_features
         with torch.no_grad():
@@ -622,10 +643,10 @@ class W8A4NativeLinear(torch.nn.Module):
         original_shape = value.shape[:-1]
         flat = value.reshape(-1, self.in_features)
         packed, activation_scale = _quantize_a4_shared(value, flat, in_features=self.in_features)
-        output = _gemm(packed, _native.TW_ACT_A4, activation_scale, self.weight_int8, _native.TW_KMAJOR_W8,
-                       self.weight_scale, self.bias if self.bias.numel() else None, self.out_features,
+        weight, wscale, bias, n = _kernel_operands(self, self.weight_int8, self.bias if self.bias.numel() else None)
+        output = _gemm(packed, _native.TW_ACT_A4, activation_scale, weight, _native.TW_KMAJOR_W8, wscale, bias, n,
                        self.in_features, _native.TW_EPI_A8, value.dtype)
-        return output.reshape(*original_shape, self.out_features)
+        return _first_columns(output, self.out_features).reshape(*original_shape, self.out_features)
 
 
 # ---------------------------------------------------------------- exact split-K decode

@@ -436,8 +436,10 @@ def bench_gemma_bank(torch, steps, warmup):
     with install_bank as a W4A4 SharedBank whose two binary switchable
     matrices (q and gate) run W4A8 in q01 / q11 / q10, balanced by W4A2
     k / v / o / up (the bank rules of precision.py:54-62). Each
-    configuration's block forward (7 linears and the block's elementwise ops)
-    is one GraphReplay graph; us per block at M = 256 and M = 1."""
+    configuration's block forward (7 linears, k / v and gate / up as sibling
+    calls, the gated MLP product inside down's quantizer, and the block's
+    residual adds) is one GraphReplay graph; us per block at M = 256 and
+    M = 1."""
     from actune_amd.graph import GraphReplay
     from actune_amd.layers import install_bank
     from actune_amd.precision import CONFIGURATIONS, SharedBank, precision_profile
@@ -450,10 +452,17 @@ def bench_gemma_bank(torch, steps, warmup):
                 setattr(self, name, torch.nn.Linear(k, n, bias=False, dtype=torch.bfloat16, device="cuda"))
 
         def forward(self, x):
-            q, _k, _v = self.q(x), self.k(x), self.v(x)
+            # k / v (both W4A2) run as one sibling launch; q reads x at its
+            # own activation width. The MLP is Gemma's gated form with the
+            # tanh GELU, its product formed inside down's quantizer.
+            q = self.q(x)
+            _k, _v = grouped_sibling_forward(x, [self.k, self.v])
             h = x + self.o(q)
-            return h + self.down(torch.nn.functional.silu(self.gate(h)) * self.up(h))
+            gate, up = grouped_sibling_forward(h, [self.gate, self.up])
+            return h + gated_down_forward(self.down, gate, up, gelu)
 
+    from actune_amd.kernels.grouped import gated_down_forward, grouped_sibling_forward
+    gelu = torch.nn.GELU(approximate="tanh")  # Gemma's gelu_pytorch_tanh
     configs = {q: dict(GEMMA_FIXED, q=qm, gate=gm) for q, (qm, gm) in GEMMA_SWITCH.items()}
     modes = [f"w{w}a{a}" for w in (2, 4, 8) for a in (2, 4, 8)]
     sizes = {name: {md: n * k * int(md[1]) // 8 + 4 * n for md in modes} for name, (n, k) in GEMMA_BLOCK.items()}

@@ -88,7 +88,9 @@ def _oracle_out(x, lin, W, A, mode, dtype):
 
 @pytest.mark.parametrize("cls,W,A,mode", FAMILY)
 @pytest.mark.parametrize("m,k,n", [(1, 256, 48), (3, 512, 80), (16, 1024, 128), (17, 384, 16),
-                                   (40, 256, 96), (130, 512, 144), (200, 128, 32), (1, 4096, 256)])
+                                   (40, 256, 96), (130, 512, 144), (200, 128, 32), (1, 4096, 256),
+                                   # out_features not a multiple of 16 (padded K-major operands)
+                                   (5, 256, 100), (1, 512, 40), (9, 1024, 1000), (2, 256, 8), (64, 512, 24)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_modules_bit_exact(cls, W, A, mode, m, k, n, bias):
     if k % (128 if cls in (T.W8A8TritonLinear, T.W2A8TritonLinear, T.W8A4NativeLinear) else 64):
@@ -671,3 +673,21 @@ def test_w4r4_rejects_bad_calls():
         _native.tokenwise_linear_multi([(t["w"], t["ws"], None, torch.empty(33, n, device=DEV))],
                                        _native.TW_KMAJOR_W4R4, n, k, 0, torch.ones(33, device=DEV), codes=big,
                                        residuals=[t["r"]])
+
+
+def test_ragged_width_operands_follow_buffer_updates():
+    """A K-major module of out_features 100 runs on padded copies of its
+    buffers; an in-place update of the buffers (load_state_dict) is seen by
+    the next call, and the state dict keeps the reference's shapes."""
+    torch.manual_seed(21)
+    lin_a = torch.nn.Linear(256, 100, bias=True, dtype=torch.bfloat16, device=DEV)
+    lin_b = torch.nn.Linear(256, 100, bias=True, dtype=torch.bfloat16, device=DEV)
+    mod, other = T.W4A8TritonLinear(lin_a), T.W4A8TritonLinear(lin_b)
+    assert mod.packed_weight.shape == (128, 100) and mod.weight_scale.shape == (100,)
+    x = torch.randn(3, 256, device=DEV).to(torch.bfloat16)
+    with torch.inference_mode():
+        first = mod(x)
+        mod.load_state_dict(other.state_dict())
+        second = mod(x)
+        want = other(x)
+    assert torch.equal(second, want) and not torch.equal(first, second)

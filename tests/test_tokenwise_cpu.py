@@ -123,13 +123,24 @@ def test_shared_cache_scope_and_counters():
 
 
 def test_replace_is_all_or_nothing():
-    """A selected layer the backend cannot take (out_features not a multiple
-    of 16 for the K-major layouts) makes the helper raise before anything is
-    replaced."""
-    model = torch.nn.Sequential(torch.nn.Linear(128, 32), torch.nn.Linear(128, 24))
-    with pytest.raises(ValueError, match="divisible by 16"):
+    """A selected layer the backend cannot take (in_features not a multiple
+    of 32 for W4A8) makes the helper raise before anything is replaced."""
+    model = torch.nn.Sequential(torch.nn.Linear(128, 32), torch.nn.Linear(100, 24))
+    with pytest.raises(ValueError, match="divisible by 32"):
         T.replace_with_w4a8_triton_(model, lambda child, name: isinstance(child, torch.nn.Linear))
     assert all(type(m) is torch.nn.Linear for m in model)
+
+
+def test_k_major_modules_take_any_output_width():
+    """out_features need not be a multiple of 16 (the reference takes any):
+    the buffers keep the reference's shapes; the kernels run on padded
+    copies made at the first call."""
+    model = torch.nn.Sequential(torch.nn.Linear(128, 32), torch.nn.Linear(128, 24))
+    assert T.replace_with_w4a8_triton_(model, lambda child, name: isinstance(child, torch.nn.Linear)) == 2
+    assert model[1].packed_weight.shape == (64, 24) and model[1].weight_scale.shape == (24,)
+    for cls in (T.W8A8TritonLinear, T.W2A8TritonLinear, T.W8A4NativeLinear):
+        mod = cls(torch.nn.Linear(128, 40))
+        assert mod.out_features == 40 and mod.weight_scale.shape == (40,)
 
 
 def test_decode_eligibility():
