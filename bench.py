@@ -72,10 +72,13 @@ def parse():
     return p.parse_args()
 
 
-# --only: (M, [(N, K) per target], kernel config) — M=1 decode launches of the C2 step and one C3 prefill
+# --only: (M, [(N, K) per target], kernel config) — the decode launches of the C2 steps and one C3 prefill
 ONLY_SHAPES = {
     "q": (1, [(4096, 4096)], -1), "gate": (1, [(11008, 4096)], -1), "down": (1, [(4096, 11008)], -1),
     "qkv": (1, [(4096, 4096)] * 3, -1), "gateup": (1, [(11008, 4096)] * 2, -1),
+    # the M=8 step's launches (x quantized in the launch, or the quantizer launch first, as chosen)
+    "o8": (8, [(4096, 4096)], -1), "qkv8": (8, [(4096, 4096)] * 3, -1), "gateup8": (8, [(11008, 4096)] * 2, -1),
+    "down8": (8, [(4096, 11008)], -1),
     "prefill512": (512, [(4096, 4096)], -1),
     # the tokenwise W4A8 GEMM (K-major nibble pairs) on its per-row A8 codes
     "tw512": (512, [(4096, 4096)], "tokenwise"),
