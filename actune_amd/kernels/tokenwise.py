@@ -247,13 +247,17 @@ def _kernel_operands(module, weight, bias):
     and bias zero-padded to the next multiple of 16; the caller keeps the
     first out_features columns of the result. The copies are made once per
     version of the buffers and held outside the module's buffers, so state
-    dicts and storage counts stay the reference's."""
+    dicts and storage counts stay the reference's (buffers that are
+    inference tensors have no version counter, so theirs are remade on every
+    call)."""
     n = module.out_features
     if n % 16 == 0:
         return weight, module.weight_scale, bias, n
-    key = tuple(None if t is None else (t.data_ptr(), t._version) for t in (weight, module.weight_scale, bias))
+    key = tuple(None if t is None else (t.data_ptr(), _version_of(t)) for t in (weight, module.weight_scale, bias))
+    # inference tensors carry no version counter: their copies are remade on every call
+    trackable = all(k is None or k[1] is not None for k in key)
     cached = module.__dict__.get("_padded_operands")
-    if cached is None or cached[0] != key:
+    if cached is None or cached[0] != key or not trackable:
         n16 = -(-n // 16) * 16
 
         def padded(t):
