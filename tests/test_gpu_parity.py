@@ -110,6 +110,35 @@ def test_output_bit_exact_in_canonical_order(W, A, shape, with_bias):
     assert all(torch.equal(first, o) for o in outs.values())  # every config bit-identical
 
 
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,offset", [(96, 0), (42, 0), (96, 1)])
+def test_prefill_epilogue_store_forms(out_dtype, n, offset):
+    """The prefill kernel stores a lane's four consecutive outputs in one
+    vector store when N % 4 == 0 and the output pointer is aligned to four
+    elements, and one element at a time otherwise (N = 42; an output view one
+    element into its storage): every config valid at M = 70 matches the
+    oracle bit for bit in each form."""
+    m, k = 70, 320
+    W, A = 4, 8
+    x, w, b = seeded_inputs(m, k, n, seed=n + offset, bias=True)
+    a_packed, a_scales, ac = oracle_activation(x, A)
+    wc, wsc, w_dev, ws_dev = _packed_weight(w, W, A)
+    a_dev = torch.from_numpy(a_packed).to(DEV)
+    s_dev = torch.from_numpy(a_scales).to(DEV)
+    want = O.round_out(O.linear(ac, a_scales, wc, wsc, b.float().numpy(), bounds=canonical_bounds(k // 64)),
+                       dtype_name(out_dtype))
+    for config in range(_native.num_configs()):
+        if not _native.config_valid(config, m):
+            continue
+        store = torch.full((m * n + offset,), float("nan"), device=DEV, dtype=out_dtype)
+        out = store[offset:].view(m, n)
+        _native.grouped_linear(a_dev, s_dev, w_dev, ws_dev, b.to(DEV), (m, k), W, A, config, out=out,
+                               out_dtype=out_dtype)
+        np.testing.assert_array_equal(bits(out), want, err_msg=f"config {config}")
+        if offset:
+            assert torch.isnan(store[:offset]).all()  # nothing written before the view
+
+
 @pytest.mark.parametrize("W,A", PAIRS)
 @pytest.mark.parametrize("shape", [(1, 64, 32), (17, 128, 96)])
 def test_reference_float_criterion(W, A, shape):
