@@ -116,11 +116,21 @@ bool forward_fuses(int config, int64_t M, int64_t n_total, int64_t K, int W, int
   return M <= kFusedMaxM && (config < kSmallMConfigs || (config >= kStreamFirst && config < kPrefillFirst));
 }
 
+// Arguments some call can take: the config selection reasons only about
+// these (its arithmetic divides by the widths and casts the dimensions).
+bool selectable(int64_t M, int64_t N, int64_t K, int W, int A) {
+  return width_ok(W) && width_ok(A) && M >= 0 && M <= INT_MAX && N > 0 && N <= INT_MAX / 2 && K > 0 &&
+         K % kGroup == 0 && K <= INT_MAX / 8;
+}
+
 // ACTUNE_CONFIG_AUTO: calls that hand over x (and may fuse the quantizer) use
 // actune_default_config; calls on packed activations use packed_default (the
-// same choice without the in-launch quantization).
+// same choice without the in-launch quantization). Arguments no call takes
+// resolve to the first prefill config, valid at every M, so that the call's
+// own checks name what is wrong.
 int resolve(int config, int64_t M, int64_t N, int64_t K, int W, int A, bool has_x) {
   if (config != ACTUNE_CONFIG_AUTO) return config;
+  if (!selectable(M, N, K, W, A)) return kPrefillFirst;
   return has_x ? actune_default_config(M, N, K, W, A) : packed_default(M, N, K, W, A);
 }
 
@@ -224,6 +234,7 @@ bool decode_waves_useful(int64_t K, int nw) {
 }  // namespace
 
 int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
+  if (!selectable(M, N, K, W, A)) return ACTUNE_CONFIG_AUTO;
   // Decode (M <= 64, measured on MI355X at Llama/Gemma shapes): the decode
   // kernel beats the small-M and streaming kernels wherever a wave's K-range
   // fits its load ring. Calls that hand over bf16 x first try to quantize it
@@ -462,7 +473,10 @@ int actune_grouped_forward_multi(const void* x, int x_dtype, const void* input_s
   // the widest width sizes the launch (its weight ring is the tightest)
   W = *std::max_element(widths, widths + ntargets);
   int64_t n_total = 0;
-  for (int t = 0; t < ntargets; ++t) n_total += targets[t].N;
+  for (int t = 0; t < ntargets; ++t) {
+    if (targets[t].N <= 0 || targets[t].N > INT_MAX / 2) return fail(ACTUNE_ERR_INVALID, "invalid dimensions");
+    n_total += targets[t].N;
+  }
   const bool auto_config = config == ACTUNE_CONFIG_AUTO;
   config = resolve(config, M, n_total, K, W, A, true);
   int rc = check_shape(M, K, W, A, x_dtype, bias_dtype, config);

@@ -176,7 +176,9 @@ int actune_grouped_dots_i32(const uint8_t* a, const uint8_t* w, int64_t M, int64
  *   actune_grouped_forward(_multi). actune_grouped_linear and
  *   actune_grouped_dots_i32 (packed activations) resolve AUTO to the same
  *   kernels without the in-launch quantization (a decode config where the
- *   decode kernel fits the codes).
+ *   decode kernel fits the codes). For a width or dimension that no call
+ *   takes it returns ACTUNE_CONFIG_AUTO (-1); a call with such arguments
+ *   returns ACTUNE_ERR_INVALID naming them, whatever its config.
  */
 int actune_num_configs(void);
 int actune_config_valid(int config, int64_t M);

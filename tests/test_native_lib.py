@@ -3,6 +3,8 @@ symbol include/actune_hip.h declares, passes its host layout self-test and
 rejects bad arguments before launching anything."""
 import ctypes
 import re
+import subprocess
+import sys
 from pathlib import Path
 
 import pytest
@@ -168,6 +170,29 @@ def test_linear_rejects_bad_arguments(args, msg):
     rc = _native.lib().actune_grouped_linear(None, None, None, None, None, 2, None, p["out_dt"],
                                              p["M"], p["N"], p["K"], p["W"], p["A"], p["config"], None)
     assert rc == 1 and msg in _err()
+
+
+def test_auto_config_with_invalid_arguments_reports_them():
+    """ACTUNE_CONFIG_AUTO with a width or dimension no call takes used to run
+    the config selection on it first (a division by the weight width: the
+    process died of SIGFPE); the call now names the bad argument."""
+    lib = _native.lib()
+    for W in (0, 16):
+        rc = lib.actune_grouped_linear(None, None, None, None, None, 2, None, 0, 4, 32, 128, W, 8, -1, None)
+        assert rc == 1 and "Unsupported integer width" in _err()
+    rc = lib.actune_grouped_forward(None, 0, None, None, None, None, None, None, 2, None, 4, 0, 128, 4, 8, -1, None)
+    assert rc == 1 and "invalid dimensions" in _err()
+    assert _native.default_config(4, 4096, 4096, 0, 8) == -1
+    assert _native.default_config(4, 4096, 100, 4, 8) == -1
+
+
+def test_entry_points_survive_argument_fuzz():
+    """tests/abi_fuzz.py in a child process: every entry point, NULL buffers,
+    edge-case and invalid arguments; each call returns a status (OK only for
+    an empty call) and none crashes."""
+    res = subprocess.run([sys.executable, str(ROOT / "tests" / "abi_fuzz.py"), str(_native.LIB_PATH), "3000"],
+                         capture_output=True, text=True, timeout=600)
+    assert res.returncode == 0, (res.returncode, res.stdout[-2000:], res.stderr[-2000:])
 
 
 def test_zero_rows_is_a_no_op_without_a_gpu():
