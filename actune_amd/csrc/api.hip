@@ -53,7 +53,9 @@ int check_quantize(const void* x, int dt, const void* sc, int64_t M, int64_t K, 
   if (!width_ok(A)) return fail(ACTUNE_ERR_INVALID, "Unsupported integer width");
   if (!dtype_ok(dt)) return fail(ACTUNE_ERR_INVALID, "unsupported activation dtype");
   if (M < 0 || K <= 0 || K % 64) return fail(ACTUNE_ERR_INVALID, "Grouped backend requires K divisible by 64");
-  if (M * (K / 64) / 32 >= INT_MAX || K > INT_MAX / 8) return fail(ACTUNE_ERR_INVALID, "activation too large");
+  // (bounds on M and K first, so that the group count cannot overflow)
+  if (M > INT_MAX || K > INT_MAX / 8 || M * (K / 64) / 32 >= INT_MAX)
+    return fail(ACTUNE_ERR_INVALID, "activation too large");
   if (M == 0) return ACTUNE_OK;
   if (!x || !packed || !scales) return fail(ACTUNE_ERR_INVALID, "null pointer");
   if (!aligned(x, 16) || (sc && !aligned(sc, 16)) || !aligned(packed, 8) || !aligned(scales, 4))
