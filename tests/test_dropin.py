@@ -87,7 +87,7 @@ def _run(tmp_path, prologue, layers, grouped):
 
 
 def test_alias_recipe_serves_reference_import_paths(tmp_path):
-    """The INTEGRATION.md recipe: install() first, then the reference's own
+    """The drop-in recipe: dropin.install() first, then the reference's own
     import order; actune.precision, actune.layers and actune.kernels.grouped
     are this package's modules and the Controller's precision_profile drives
     dispatch."""
