@@ -297,10 +297,15 @@ __device__ __forceinline__ void decode_tile(const LinearArgs& args, int GW, uint
     if ((FULL && ONE && !PACKED) || p < npass) {
       const float sf = convert_x(p, early[p]);
       if constexpr (FAST) {
+        // a group past the wave's range (the tail of its last slot, whose
+        // weights are the next row's bytes and whose slab row is unwritten
+        // LDS) gets scale 0 and adds fma(d, 0, p) = p exactly
 #pragma unroll
         for (int j = 0; j < PR; ++j)
           if (p * PR + j < RING * GS)
-            gsc[p * PR + j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sf), (64 / PR) * j));
+            gsc[p * PR + j] = p * PR + j < ng
+                                  ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sf), (64 / PR) * j))
+                                  : 0.0f;
       }
     }
   }
@@ -332,8 +337,9 @@ __device__ __forceinline__ void decode_tile(const LinearArgs& args, int GW, uint
     // M == 1: lanes of token 0 (i == 0) read the wave's slab, the others the
     // zero region, both with stride 64 per group, so every token operand
     // read is one LDS load at a constant offset (reads past the wave's range
-    // stay inside LDS and are never used); the rescale takes its scale from
-    // a scalar register. Same pipeline and order as the general loop below.
+    // stay inside LDS; their groups have scale 0); the rescale takes its
+    // scale from a scalar register. Same pipeline and order as the general
+    // loop below.
     constexpr int RA = 3;
     const uint8_t* tbase = (i == 0 ? slab : zero_row) + smallm_slot_k<W>(kb);
     v4u bq[RING][GS];

@@ -139,6 +139,53 @@ def test_prefill_epilogue_store_forms(out_dtype, n, offset):
             assert torch.isnan(store[:offset]).all()  # nothing written before the view
 
 
+@pytest.mark.parametrize("W", [2, 4, 8])
+@pytest.mark.parametrize("m", [1, 2, 3])
+def test_decode_ragged_tail_adds_nothing(W, m):
+    """The decode kernel's last weight slot of the wave whose K-range ends at
+    G also spans up to 3 groups past G (4 groups per slot at W2, 2 at W4).
+    Their weights are the next row's bytes and their slab rows unwritten
+    LDS, so each such group must get scale 0. The one-token path with x
+    quantized in the launch once gave them the quantizer's 1e-8 floor scale
+    instead (x reads past K are zeros): a run-dependent error of about 1e-8
+    per output, below a bf16 ulp unless the output is 0 or near a rounding
+    boundary. Here every output is exactly 0 (group 4 of x repeats group 0;
+    each weight row holds codes c in group 0 and -c in group 4, in two
+    canonical chunks, and zeros elsewhere), so any such term shows. G = 5..11
+    and 21 under every decode config, each call after a launch that leaves
+    nonzero codes in LDS."""
+    A, n = 4, 48
+    bf16 = torch.bfloat16
+    junk_x = torch.full((m, 4096), 30.0, dtype=bf16, device=DEV)
+    _, junk_w, _ = seeded_inputs(1, 4096, 64, seed=3)
+    _, _, junk_dev, junk_ws = _packed_weight(junk_w, W, A)
+    configs = [c for c in range(14, _native.num_configs()) if _native.config_valid(c, m)]
+    q = (1 << (W - 1)) - 1  # symmetric code range, so -c is a code too
+    fused = 0
+    for G in list(range(5, 12)) + [21]:
+        k = 64 * G
+        gen = torch.Generator().manual_seed(100 * G + W + m)
+        x = torch.randn(m, k, generator=gen)
+        x[:, 256:320] = x[:, 0:64]
+        x = x.to(bf16)
+        wc = np.zeros((n, k), np.int8)
+        c = torch.randint(-q, q + 1, (n, 64), generator=gen).numpy().astype(np.int8)
+        wc[:, 0:64], wc[:, 256:320] = c, -c
+        wsc = (torch.rand(n, generator=gen) * 0.05 + 0.01).numpy().astype(np.float32)
+        w_dev = torch.from_numpy(O.pack_rows(wc, W)).to(DEV)
+        ws_dev = torch.from_numpy(wsc).to(DEV)
+        _, a_scales, ac = oracle_activation(x, A)
+        want = O.round_out(O.linear(ac, a_scales, wc, wsc, None, bounds=canonical_bounds(G)), "bf16")
+        assert not want.any()  # every output +0
+        x_dev = x.to(DEV)
+        for config in configs:
+            fused += _native.forward_fuses_quantizer(m, n, k, W, A, bf16, config)
+            _native.grouped_forward(junk_x, junk_dev, junk_ws, None, W, A, config=config)
+            got = _native.grouped_forward(x_dev, w_dev, ws_dev, None, W, A, config=config)
+            np.testing.assert_array_equal(bits(got), want, err_msg=f"G={G} config {config}")
+    assert fused > 0  # the in-launch quantization ran
+
+
 @pytest.mark.parametrize("W,A", PAIRS)
 @pytest.mark.parametrize("shape", [(1, 64, 32), (17, 128, 96)])
 def test_reference_float_criterion(W, A, shape):

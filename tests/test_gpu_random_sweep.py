@@ -1,0 +1,100 @@
+"""Seeded random sweep of the group-64 path on the GPU against the oracle.
+
+Each case draws M (1-300), N (1-699), K (64-3072), the (W, A) pair, the
+input dtype (= output dtype), a bias and its dtype, a channel scale and a
+kernel config (AUTO or any config valid at M) from its own seed, runs the
+forward through the C ABI, and checks every output bit against the oracle in
+the canonical chunked fp32 order. The multi-target cases give each of one
+to four targets its own N and weight width. The hand-picked shapes of the
+other parity tests cover the known edges; this sweep covers combinations
+of them that no one picked.
+"""
+import numpy as np
+import pytest
+import torch
+
+from actune_amd import _native
+from oracle import oracle as O
+from tests.helpers import PAIRS, bits, canonical_bounds, dtype_name, oracle_weight, seeded_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+MS = (1, 2, 3, 5, 8, 13, 16, 17, 31, 50, 64, 65, 96, 130, 257, 300)
+
+
+def _draw(rng):
+    m = int(rng.choice(MS))
+    k = 64 * int(rng.integers(1, 49))
+    A = int(rng.choice((2, 4, 8)))
+    dtype = DTYPES[int(rng.integers(3))]
+    bias_dtype = DTYPES[int(rng.integers(3))] if rng.random() < 0.5 else None
+    scale = rng.random() < 0.3
+    valid = [c for c in range(_native.num_configs()) if _native.config_valid(c, m)]
+    config = _native.CONFIG_AUTO if rng.random() < 0.4 else int(rng.choice(valid))
+    return m, k, A, dtype, bias_dtype, scale, config
+
+
+def _target(rng, seed, m, k, n, W, A, dtype, bias_dtype):
+    """Weights from seeded_inputs (CPU), their oracle codes and device buffers."""
+    _, w, _ = seeded_inputs(1, k, n, seed=seed, dtype=dtype)
+    wc, wsc = oracle_weight(w, W, A)
+    bias = None
+    if bias_dtype is not None:
+        g = torch.Generator().manual_seed(seed + 1)
+        bias = (torch.randn(n, generator=g) * 0.1).to(bias_dtype)
+    dev = (torch.from_numpy(O.pack_rows(wc, W)).to(DEV), torch.from_numpy(wsc).to(DEV),
+           None if bias is None else bias.to(DEV))
+    return wc, wsc, bias, dev
+
+
+def _inputs(seed, m, k, dtype, scale):
+    x, _, _ = seeded_inputs(m, k, 1, seed=seed, dtype=dtype)
+    s = None
+    if scale:
+        g = torch.Generator().manual_seed(seed + 2)
+        s = (torch.rand(k, generator=g) * 1.5 + 0.25).to(dtype)
+    return x, s
+
+
+def _want(x, s, A, wc, wsc, bias, dtype, k):
+    _, asc, ac = O.quantize_groups(bits(x), A, dtype_name(dtype), None if s is None else bits(s))
+    y = O.linear(ac, asc, wc, wsc, None if bias is None else bias.float().numpy(), bounds=canonical_bounds(k // 64))
+    return O.round_out(y, dtype_name(dtype))
+
+
+@pytest.mark.parametrize("case", range(48))
+def test_random_forward_against_oracle(case):
+    rng = np.random.default_rng(7000 + case)
+    m, k, A, dtype, bias_dtype, scale, config = _draw(rng)
+    W = int(rng.choice((2, 4, 8)))
+    n = int(rng.integers(1, 700))
+    wc, wsc, bias, (w_dev, ws_dev, b_dev) = _target(rng, 100 * case, m, k, n, W, A, dtype, bias_dtype)
+    x, s = _inputs(100 * case + 50, m, k, dtype, scale)
+    out = _native.grouped_forward(x.to(DEV), w_dev, ws_dev, b_dev, W, A,
+                                  input_scale=None if s is None else s.to(DEV), config=config)
+    np.testing.assert_array_equal(bits(out), _want(x, s, A, wc, wsc, bias, dtype, k),
+                                  err_msg=f"M={m} N={n} K={k} W{W}A{A} {dtype} bias={bias_dtype} "
+                                          f"scale={scale} config={config}")
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_random_multi_target_forward_against_oracle(case):
+    rng = np.random.default_rng(9000 + case)
+    m, k, A, dtype, bias_dtype, scale, config = _draw(rng)
+    count = int(rng.integers(1, _native.MAX_TARGETS + 1))
+    widths = [int(rng.choice((2, 4, 8))) for _ in range(count)]
+    ns = [int(rng.integers(1, 400)) for _ in range(count)]
+    targets, expect = [], []
+    x, s = _inputs(100 * case + 77, m, k, dtype, scale)
+    for j, (W, n) in enumerate(zip(widths, ns)):
+        wc, wsc, bias, (w_dev, ws_dev, b_dev) = _target(rng, 100 * case + 10 * j, m, k, n, W, A, dtype, bias_dtype)
+        targets.append((w_dev, ws_dev, b_dev, None, W))
+        expect.append(_want(x, s, A, wc, wsc, bias, dtype, k))
+    outs = _native.grouped_forward_multi(x.to(DEV), targets, widths[0], A,
+                                         input_scale=None if s is None else s.to(DEV), config=config)
+    for j, (out, want) in enumerate(zip(outs, expect)):
+        np.testing.assert_array_equal(bits(out), want,
+                                      err_msg=f"target {j}: M={m} N={ns} K={k} W={widths} A{A} {dtype} "
+                                              f"bias={bias_dtype} scale={scale} config={config}")
