@@ -7,7 +7,9 @@ forward through the C ABI, and checks every output bit against the oracle in
 the canonical chunked fp32 order. The multi-target cases give each of one
 to four targets its own N and weight width. The hand-picked shapes of the
 other parity tests cover the known edges; this sweep covers combinations
-of them that no one picked.
+of them that no one picked. The exact-zero test builds outputs that are 0
+in the canonical order under every config, where a leaked term of any size
+shows.
 """
 import numpy as np
 import pytest
@@ -98,3 +100,48 @@ def test_random_multi_target_forward_against_oracle(case):
         np.testing.assert_array_equal(bits(out), want,
                                       err_msg=f"target {j}: M={m} N={ns} K={k} W={widths} A{A} {dtype} "
                                               f"bias={bias_dtype} scale={scale} config={config}")
+
+
+@pytest.mark.parametrize("W,A", PAIRS)
+@pytest.mark.parametrize("m", [1, 2, 4, 17, 65])
+def test_exact_zero_outputs_every_config(W, A, m):
+    """Outputs that are exactly 0 in the canonical order stay exactly 0 under
+    every config, on the forward (x quantized in the launch where the config
+    does so, with and without a channel scale) and on packed codes: group 4
+    of x (and of the channel scale) repeats group 0, each weight row holds
+    codes c in group 0 and -c in group 4 (two canonical chunks) and zeros
+    elsewhere. A term leaked into a partial sum (a group past K, a stale LDS
+    row, a scale from outside the range) would show as a nonzero output,
+    however small. Ragged G (5, 9, 21: tails of 1, 1 and 1 groups in the last
+    quad), each call after a launch that leaves nonzero codes in LDS."""
+    n = 40
+    q = (1 << (W - 1)) - 1
+    junk_x = torch.full((m, 4096), 30.0, dtype=torch.bfloat16, device=DEV)
+    junk_w = torch.full((64, 4096 * W // 8), 0x5A, dtype=torch.uint8, device=DEV)
+    junk_ws = torch.ones(64, device=DEV)
+    configs = [_native.CONFIG_AUTO] + [c for c in range(_native.num_configs()) if _native.config_valid(c, m)]
+    for G in (5, 9, 21):
+        k = 64 * G
+        gen = torch.Generator().manual_seed(100 * G + 10 * W + A + 1000 * m)
+        x = torch.randn(m, k, generator=gen)
+        x[:, 256:320] = x[:, 0:64]
+        x = x.to(torch.bfloat16)
+        scale = torch.rand(k, generator=gen) + 0.5
+        scale[256:320] = scale[0:64]
+        scale = scale.to(torch.bfloat16)
+        wc = np.zeros((n, k), np.int8)
+        c = torch.randint(-q, q + 1, (n, 64), generator=gen).numpy().astype(np.int8)
+        wc[:, 0:64], wc[:, 256:320] = c, -c
+        wsc = (torch.rand(n, generator=gen) * 0.05 + 0.01).numpy().astype(np.float32)
+        w_dev = torch.from_numpy(O.pack_rows(wc, W)).to(DEV)
+        ws_dev = torch.from_numpy(wsc).to(DEV)
+        packed, a_scales, _ = O.quantize_groups(bits(x), A, "bf16")
+        a_dev, s_dev = torch.from_numpy(packed).to(DEV), torch.from_numpy(a_scales).to(DEV)
+        zero = np.zeros((m, n), np.uint16)
+        for config in configs:
+            for sc in (None, scale.to(DEV)):
+                _native.grouped_forward(junk_x, junk_w, junk_ws, None, W, A, config=config)
+                got = _native.grouped_forward(x.to(DEV), w_dev, ws_dev, None, W, A, input_scale=sc, config=config)
+                np.testing.assert_array_equal(bits(got), zero, err_msg=f"G={G} config {config} scale={sc is not None}")
+            got = _native.grouped_linear(a_dev, s_dev, w_dev, ws_dev, None, (m, k), W, A, config)
+            np.testing.assert_array_equal(bits(got), zero, err_msg=f"G={G} config {config} (packed)")
