@@ -267,6 +267,32 @@ def test_full_size_sampled_parity(m, n, k, W, A):
     np.testing.assert_array_equal(got, O.round_out(want, "bf16"))
 
 
+@pytest.mark.parametrize("m,n,k,W,A", [
+    (1, 65536, 8192, 4, 8), (8, 8192, 65536, 4, 8), (3, 131072, 4096, 8, 8), (64, 100003, 1024, 2, 4),
+    (1024, 4096, 65536, 8, 8), (1, 16, 262144, 4, 8),
+])
+def test_extreme_shapes_sampled_every_config(m, n, k, W, A):
+    """Shapes far from the BASELINE ones, up to the buffer limits' order of
+    magnitude (512 MiB of weights, K = 262144 = 4096 groups, N = 131072 and a
+    ragged 100003): every config valid at M against the oracle on sampled
+    columns and rows, the first and last of each included."""
+    g = torch.Generator().manual_seed(m + n + k)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    codes, scale = O.weight_codes((torch.randn(n, k, generator=g) * 0.02).numpy(), W, A)
+    w_dev = torch.from_numpy(O.pack_rows(codes, W)).to(DEV)
+    ws_dev = torch.from_numpy(scale).to(DEV)
+    rng = np.random.default_rng(0)
+    cols = np.unique(np.concatenate([rng.choice(n, size=min(60, n), replace=False), [0, n - 1]]))
+    rows = np.arange(m) if m <= 64 else np.unique(np.concatenate([rng.choice(m, size=60, replace=False), [0, m - 1]]))
+    _, a_scales, a_codes = oracle_activation(x, A)
+    want = O.round_out(O.linear(a_codes, a_scales, codes, scale, None, bounds=canonical_bounds(k // 64),
+                                rows=rows, cols=cols), "bf16")
+    xd = x.to(DEV)
+    for config in [_native.CONFIG_AUTO] + [c for c in range(_native.num_configs()) if _native.config_valid(c, m)]:
+        out = _native.grouped_forward(xd, w_dev, ws_dev, None, W, A, config=config)
+        np.testing.assert_array_equal(bits(out)[rows][:, cols], want, err_msg=f"config {config}")
+
+
 # ---------------------------------------------------------------- fused / siblings
 @pytest.mark.parametrize("W,A", PAIRS)
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 12, 16])
