@@ -299,11 +299,12 @@ __device__ __forceinline__ void decode_tile(const LinearArgs& args, int GW, uint
       if constexpr (FAST) {
         // a group past the wave's range (the tail of its last slot, whose
         // weights are the next row's bytes and whose slab row is unwritten
-        // LDS) gets scale 0 and adds fma(d, 0, p) = p exactly
+        // LDS) gets scale 0 and adds fma(d, 0, p) = p exactly; a FULL
+        // launch has none (every wave holds RING * GS groups)
 #pragma unroll
         for (int j = 0; j < PR; ++j)
           if (p * PR + j < RING * GS)
-            gsc[p * PR + j] = p * PR + j < ng
+            gsc[p * PR + j] = FULL || p * PR + j < ng
                                   ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sf), (64 / PR) * j))
                                   : 0.0f;
       }
