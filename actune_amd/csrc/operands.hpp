@@ -147,16 +147,59 @@ __device__ __forceinline__ void load8(const void* p, long i, float v[8]) {
   }
 }
 
-// Maximum of non-negative floats over an aligned 8-lane segment, in every
-// lane of the segment: DPP moves (quad xor 1, quad xor 2, then the mirror
-// inside each 8-lane half row) and integer max on the bit patterns, which
-// orders non-negative floats like their values; no LDS round trip. All 64
-// lanes must execute it.
-__device__ __forceinline__ float seg8_max(float a) {
+// E consecutive elements starting at element i (i % E == 0) as fp32: load8
+// for E = 8, one 4-, 8- or 16-byte load for E = 2 or 4.
+template <int DT, int E>
+__device__ __forceinline__ void load_n(const void* p, long i, float v[E]) {
+  if constexpr (E == 8) {
+    load8<DT>(p, i, v);
+  } else {
+    static_assert(E == 2 || E == 4, "2, 4 or 8 elements per lane");
+    constexpr int ES = DT == kF32 ? 4 : 2;  // element bytes
+    constexpr int NW = E * ES / 4;          // dwords
+    uint32_t w[NW];
+    const char* src = reinterpret_cast<const char*>(p) + i * ES;
+    if constexpr (NW == 4) {
+      const v4u q = *reinterpret_cast<const v4u*>(src);
+      w[0] = q[0]; w[1] = q[1]; w[2] = q[2]; w[3] = q[3];
+    } else if constexpr (NW == 2) {
+      const v2u q = *reinterpret_cast<const v2u*>(src);
+      w[0] = q[0]; w[1] = q[1];
+    } else {
+      w[0] = *reinterpret_cast<const uint32_t*>(src);
+    }
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      if constexpr (DT == kF32) {
+        v[j] = __uint_as_float(w[j]);
+      } else {
+        const uint16_t lo = (uint16_t)(w[j] & 0xffffu), hi = (uint16_t)(w[j] >> 16);
+        if constexpr (DT == kBF16) { v[2 * j] = bf16_to_f32(lo); v[2 * j + 1] = bf16_to_f32(hi); }
+        else { v[2 * j] = f16_to_f32(lo); v[2 * j + 1] = f16_to_f32(hi); }
+      }
+    }
+  }
+}
+
+// Maximum of non-negative floats over an aligned L-lane segment (L = 8, 16
+// or 32), in every lane of the segment: DPP moves (quad xor 1, quad xor 2,
+// the mirror inside each 8-lane half row, then the mirror of the 16-lane
+// row), for 32 lanes a swap of odd and even rows, and integer max on the
+// bit patterns, which orders non-negative floats like their values; no LDS
+// round trip. All 64 lanes must execute it.
+template <int L>
+__device__ __forceinline__ float seg_max(float a) {
+  static_assert(L == 8 || L == 16 || L == 32, "8, 16 or 32 lanes");
   uint32_t u = __float_as_uint(a);
   u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0xB1, 0xF, 0xF, false));   // [1,0,3,2]
   u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x4E, 0xF, 0xF, false));   // [2,3,0,1]
   u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x141, 0xF, 0xF, false));  // half-row mirror
+  if constexpr (L >= 16) u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x140, 0xF, 0xF, false));  // row mirror
+  if constexpr (L >= 32) {
+    // rows 0/1 (and 2/3) exchanged: each lane sees its own row and the other
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    u = max((uint32_t)r[0], (uint32_t)r[1]);
+  }
   return __uint_as_float(u);
 }
 
@@ -165,8 +208,8 @@ __device__ __forceinline__ float seg8_max(float a) {
 // sum's bit pattern is then that integer in two's complement.
 constexpr float kRoundMagic = 12582912.0f;
 
-// Group-64 codes of 8 elements held by one lane of an 8-lane segment group:
-// amax over the group, s = fl(max(amax, 1e-8) / P) and c = clamp(rint(fl(v /
+// Group-64 codes of E elements held by one lane of a (64 / E)-lane segment
+// group (8 elements and 8 lanes unless E says otherwise): amax over the group, s = fl(max(amax, 1e-8) / P) and c = clamp(rint(fl(v /
 // s)), -P-1, P). For 16-bit inputs the quotient is x * y with y = fl(1/s)
 // plus one FMA correction (Markstein), which gives the IEEE codes for every
 // bf16 and f16 input (proved exhaustively by tests/exhaustive_division.c);
@@ -174,13 +217,13 @@ constexpr float kRoundMagic = 12582912.0f;
 // (the bounds are integers, so clamp and round commute) and rounded by the
 // magic add; cb[e] holds the sum's bits, whose low byte is code e. All 64
 // lanes of the wave must call this together.
-template <int A, int DT>
-__device__ __forceinline__ float group_code_bits(const float v[8], uint32_t cb[8]) {
+template <int A, int DT, int E = 8>
+__device__ __forceinline__ float group_code_bits(const float v[E], uint32_t cb[E]) {
   constexpr int P = (1 << (A - 1)) - 1;
   float amax = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
-  amax = fmaxf(seg8_max(amax), 1e-8f);
+  for (int e = 0; e < E; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  amax = fmaxf(seg_max<64 / E>(amax), 1e-8f);
   float s;
   if constexpr (DT == kF32 || P == 1) {
     s = amax / (float)P;
@@ -197,7 +240,7 @@ __device__ __forceinline__ float group_code_bits(const float v[8], uint32_t cb[8
   }
   const float y = 1.0f / s;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < E; ++e) {
     float q;
     if constexpr (DT == kF32) {
       q = v[e] / s;
@@ -213,12 +256,12 @@ __device__ __forceinline__ float group_code_bits(const float v[8], uint32_t cb[8
 }
 
 // Same codes as integers.
-template <int A, int DT>
-__device__ __forceinline__ float group_codes(const float v[8], int c[8]) {
-  uint32_t cb[8];
-  const float s = group_code_bits<A, DT>(v, cb);
+template <int A, int DT, int E = 8>
+__device__ __forceinline__ float group_codes(const float v[E], int c[E]) {
+  uint32_t cb[E];
+  const float s = group_code_bits<A, DT, E>(v, cb);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) c[e] = (int)(int8_t)(cb[e] & 0xffu);
+  for (int e = 0; e < E; ++e) c[e] = (int)(int8_t)(cb[e] & 0xffu);
   return s;
 }
 

@@ -14,6 +14,16 @@
 // groups (1 KiB of bf16), and the group absmax is a 3-step DPP reduction
 // inside the 8-lane segment. Stores are contiguous per wave:
 // A8 writes 8 B/lane, A4 4 B/lane, A2 2 B/lane.
+//
+// The gated quantizer also has a narrow geometry for small inputs: 2
+// elements per lane (4 for A2, so that a lane still stores whole bytes) and
+// 32 (16) lanes per group. Its per-element work (the activation, two
+// roundings and the product) is several times the plain quantizer's, and
+// below 16384 groups the launch is too small to fill the chip: spreading a
+// group over more lanes shortens each wave's serial work (M=50, K=4096,
+// bf16 A4, in a hipGraph: 2.0 us against 2.9 us per launch). Above that,
+// 8 elements per lane are as fast or faster (M=256, K=16384: 7.0 against
+// 7.6 us with 2 per lane).
 #include <math.h>
 
 #include "../../include/actune_hip.h"
@@ -23,54 +33,62 @@
 
 namespace actune {
 
-// One lane's 8 values v of group gi (segment seg, columns k0..k0+7): the
-// channel-scale division when SCALE, the group's codes packed and stored,
-// and the scale stored by segment 0.
-template <int A, int DT, bool SCALE>
-__device__ __forceinline__ void quantize_lane(float (&v)[8], const void* __restrict__ input_scale, int k0,
+// One lane's E values v of group gi (segment seg, columns k0..k0+E-1): the
+// channel-scale division when SCALE, the group's codes packed and stored
+// (E*A bits at bit E*A*seg of the group's codes), and the scale stored by
+// segment 0.
+template <int A, int DT, bool SCALE, int E = 8>
+__device__ __forceinline__ void quantize_lane(float (&v)[E], const void* __restrict__ input_scale, int k0,
                                               bool live, long gi, int seg, uint8_t* __restrict__ packed,
                                               float* __restrict__ scales) {
+  static_assert(E * A >= 8, "a lane stores whole bytes");
   if constexpr (SCALE) {
-    float d[8];
-    load8<DT>(input_scale, k0, d);
+    float d[E];
+    load_n<DT, E>(input_scale, k0, d);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = round_to_dtype<DT>(v[e] / d[e]);
+    for (int e = 0; e < E; ++e) v[e] = round_to_dtype<DT>(v[e] / d[e]);
   }
-  int c[8];
-  const float s = group_codes<A, DT>(v, c);
+  int c[E];
+  const float s = group_codes<A, DT, E>(v, c);
   uint32_t bits[2] = {0u, 0u};
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < E; ++e) {
     const uint32_t field = (uint32_t)c[e] & ((1u << A) - 1u);
-    const int bit = e * A;  // bit position inside this lane's 8*A-bit run
+    const int bit = e * A;  // bit position inside this lane's E*A-bit run
     bits[bit >> 5] |= field << (bit & 31);
   }
   if (!live) return;
-  uint8_t* dst = packed + gi * (kGroup * A / 8) + seg * A;
-  if constexpr (A == 8) {
+  constexpr int B = E * A / 8;  // bytes per lane
+  uint8_t* dst = packed + gi * (kGroup * A / 8) + seg * B;
+  if constexpr (B == 8) {
     *reinterpret_cast<v2u*>(dst) = v2u{bits[0], bits[1]};
-  } else if constexpr (A == 4) {
+  } else if constexpr (B == 4) {
     *reinterpret_cast<uint32_t*>(dst) = bits[0];
-  } else {
+  } else if constexpr (B == 2) {
     *reinterpret_cast<uint16_t*>(dst) = (uint16_t)bits[0];
+  } else {
+    *dst = (uint8_t)bits[0];
   }
   if (seg == 0) scales[gi] = s;
 }
 
-// Lane geometry shared by the quantizers: 8 lanes per group, 32 groups per
-// 256-thread workgroup; a lane past the last group works on the last group
-// and stores nothing.
+// Lane geometry shared by the quantizers: E elements per lane, 64 / E lanes
+// per group, 4 E groups per 256-thread workgroup; a lane past the last group
+// works on the last group and stores nothing.
+template <int E = 8>
 struct LaneGroup {
+  static constexpr int kLanes = kGroup / E;              // lanes per group
+  static constexpr int kGroupsPerBlock = 256 / kLanes;
   long gi, e0;
   int seg, k0;
   bool live;
   __device__ LaneGroup(long groups, int G) {
-    gi = (long)blockIdx.x * 32 + (threadIdx.x >> 3);  // global group index m*G + g
-    seg = threadIdx.x & 7;                             // 8-element segment in the group
+    gi = (long)blockIdx.x * kGroupsPerBlock + threadIdx.x / kLanes;  // global group index m*G + g
+    seg = threadIdx.x % kLanes;                                       // E-element segment in the group
     live = gi < groups;
     const long gsafe = live ? gi : groups - 1;
-    e0 = gsafe * kGroup + seg * 8;                     // first element of this lane
-    k0 = (int)(gsafe % G) * kGroup + seg * 8;          // its column (for input_scale)
+    e0 = gsafe * kGroup + seg * E;                                    // first element of this lane
+    k0 = (int)(gsafe % G) * kGroup + seg * E;                         // its column (for input_scale)
   }
 };
 
@@ -80,7 +98,7 @@ __global__ __launch_bounds__(256) void quantize_groups_kernel(const void* __rest
                                                               long groups, int G,
                                                               uint8_t* __restrict__ packed,
                                                               float* __restrict__ scales) {
-  const LaneGroup lg(groups, G);
+  const LaneGroup<> lg(groups, G);
   float v[8];
   load8<DT>(x, lg.e0, v);
   quantize_lane<A, DT, SCALE>(v, input_scale, lg.k0, lg.live, lg.gi, lg.seg, packed, scales);
@@ -114,22 +132,26 @@ __device__ __forceinline__ float gate_act(float x) {
 // Quantizer of the down projection's input p = act(gate) * up of a gated MLP:
 // p is formed in the inputs' dtype as torch forms it (act rounded to the
 // dtype, then the product rounded), then quantized exactly as
-// quantize_groups_kernel quantizes a tensor holding p.
-template <int A, int DT, int ACT, bool SCALE>
+// quantize_groups_kernel quantizes a tensor holding p. E elements per lane.
+template <int A, int DT, int ACT, bool SCALE, int E>
 __global__ __launch_bounds__(256) void quantize_gated_kernel(const void* __restrict__ gate,
                                                              const void* __restrict__ up,
                                                              const void* __restrict__ input_scale,
                                                              long groups, int G,
                                                              uint8_t* __restrict__ packed,
                                                              float* __restrict__ scales) {
-  const LaneGroup lg(groups, G);
-  float v[8], u[8];
-  load8<DT>(gate, lg.e0, v);
-  load8<DT>(up, lg.e0, u);
+  const LaneGroup<E> lg(groups, G);
+  float v[E], u[E];
+  load_n<DT, E>(gate, lg.e0, v);
+  load_n<DT, E>(up, lg.e0, u);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = round_to_dtype<DT>(round_to_dtype<DT>(gate_act<ACT>(v[e])) * u[e]);
-  quantize_lane<A, DT, SCALE>(v, input_scale, lg.k0, lg.live, lg.gi, lg.seg, packed, scales);
+  for (int e = 0; e < E; ++e) v[e] = round_to_dtype<DT>(round_to_dtype<DT>(gate_act<ACT>(v[e])) * u[e]);
+  quantize_lane<A, DT, SCALE, E>(v, input_scale, lg.k0, lg.live, lg.gi, lg.seg, packed, scales);
 }
+
+// Elements per lane of the gated quantizer: the narrow geometry up to 16384
+// groups, 8 above.
+constexpr long kGatedNarrowMaxGroups = 16384;
 
 template <int A, int DT>
 static void launch_quantize_dt(const void* x, const void* sc, long M, long K, uint8_t* packed,
@@ -157,15 +179,26 @@ void launch_quantize(const void* x, int dt, const void* sc, long M, long K, int 
   else launch_quantize_a<2>(x, dt, sc, M, K, packed, scales, stream);
 }
 
+template <int A, int DT, int ACT, int E>
+static void launch_gated_e(const void* gate, const void* up, const void* sc, long groups, int G, uint8_t* packed,
+                           float* scales, hipStream_t stream) {
+  constexpr long per_block = LaneGroup<E>::kGroupsPerBlock;
+  const dim3 grid((unsigned)((groups + per_block - 1) / per_block));
+  if (sc)
+    quantize_gated_kernel<A, DT, ACT, true, E><<<grid, 256, 0, stream>>>(gate, up, sc, groups, G, packed, scales);
+  else
+    quantize_gated_kernel<A, DT, ACT, false, E><<<grid, 256, 0, stream>>>(gate, up, sc, groups, G, packed, scales);
+}
+
 template <int A, int DT, int ACT>
 static void launch_gated_t(const void* gate, const void* up, const void* sc, long M, long K, uint8_t* packed,
                            float* scales, hipStream_t stream) {
   const long groups = M * (K / kGroup);
-  const dim3 grid((unsigned)((groups + 31) / 32));
-  if (sc)
-    quantize_gated_kernel<A, DT, ACT, true><<<grid, 256, 0, stream>>>(gate, up, sc, groups, (int)(K / kGroup), packed, scales);
+  const int G = (int)(K / kGroup);
+  if (groups <= kGatedNarrowMaxGroups)
+    launch_gated_e<A, DT, ACT, A == 2 ? 4 : 2>(gate, up, sc, groups, G, packed, scales, stream);
   else
-    quantize_gated_kernel<A, DT, ACT, false><<<grid, 256, 0, stream>>>(gate, up, sc, groups, (int)(K / kGroup), packed, scales);
+    launch_gated_e<A, DT, ACT, 8>(gate, up, sc, groups, G, packed, scales, stream);
 }
 
 template <int A, int DT>

@@ -36,18 +36,30 @@ def _every_finite(dtype):
     return values[torch.isfinite(values)]
 
 
+def _gated_in_calls(gate, up, act, A, rows):
+    """quantize_gated over row slices of `rows` rows (all at once for None):
+    at most 16384 groups per call take the quantizer's narrow geometry (2 or
+    4 elements per lane), more take 8 per lane."""
+    if rows is None:
+        return _native.quantize_gated(gate, up, act, A)
+    parts = [_native.quantize_gated(gate[i:i + rows], up[i:i + rows], act, A) for i in range(0, gate.shape[0], rows)]
+    return torch.cat([p for p, _ in parts]), torch.cat([s for _, s in parts])
+
+
+@pytest.mark.parametrize("rows", [None, 16384], ids=["wide", "narrow"])
 @pytest.mark.parametrize("act", [_native.ACT_SILU, _native.ACT_GELU_TANH])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_every_gate_value_in_a_group_of_its_own(act, dtype):
+def test_every_gate_value_in_a_group_of_its_own(act, dtype, rows):
     """One group per finite gate value g = [g, 0 x 63] with up = 1: the scale
     of that group equals torch's for every value, so act(g) rounded to the
     dtype is torch's bit for bit wherever |act(g)| >= 127e-8 (below, the
-    1e-8 floor of the scale hides it and the code is compared)."""
+    1e-8 floor of the scale hides it and the code is compared). In one call
+    (8 elements per lane) and in calls of 16384 groups (2 per lane)."""
     values = _every_finite(dtype).to(DEV)
     gate = torch.zeros(values.numel(), 64, device=DEV, dtype=dtype)
     gate[:, 0] = values
     up = torch.ones_like(gate)
-    got_p, got_s = _native.quantize_gated(gate, up, act, 8)
+    got_p, got_s = _gated_in_calls(gate, up, act, 8, rows)
     want_p, want_s = _torch_codes(gate, up, act, 8)
     assert torch.equal(got_s, want_s)
     assert torch.equal(got_p, want_p)
@@ -69,8 +81,11 @@ def test_fp32_gate_values_sampled(act):
 @pytest.mark.parametrize("act", [_native.ACT_SILU, _native.ACT_GELU_TANH])
 @pytest.mark.parametrize("A", [8, 4, 2])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("m,k", [(1, 1024), (50, 4096), (300, 16384), (7, 64)])
+@pytest.mark.parametrize("m,k", [(1, 1024), (50, 4096), (300, 16384), (7, 64), (3, 192), (16, 65536), (16385, 64)])
 def test_products_equal_torch_then_quantizer(act, A, dtype, m, k):
+    """Both lane geometries (narrow up to 16384 groups: the first, second,
+    fourth to sixth shapes; 8 elements per lane above), ragged group counts
+    (7, 9 and 16385 groups) and the channel-scale division."""
     g = torch.Generator().manual_seed(m + k + A)
     gate = (torch.randn(m, k, generator=g) * 3).to(dtype).to(DEV)
     up = torch.randn(m, k, generator=g).to(dtype).to(DEV)
