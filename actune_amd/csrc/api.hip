@@ -94,12 +94,16 @@ int packed_default(int64_t M, int64_t N, int64_t K, int W, int A);
 // (row tiles / tiles per workgroup) x groups x tokens; measured on MI355X
 // (W4A8, M = 1..8, N = 2048..22016), past about 180 (4-token tiles) or 160
 // (8-token tiles) group-rows per SIMD (1024 SIMDs) the quantizer launch
-// followed by the GEMM on its codes is faster. Where the codes path cannot
+// followed by the GEMM on its codes is faster. With 16-token blocks (M > 16)
+// the limit is 200: at M = 50 every launch measured at 200 was faster fused
+// (W4A4 4096x1024 8.9 -> 8.5 us, 8192x1024 and 2 x 4096x1024 12.3 -> 11.5
+// and 12.6 -> 12.0 us, 2048x2048 8.2 -> 7.7 us), at 256 some were slower
+// (8192x1024 at M = 64: 13.0 against 13.4 us). Where the codes path cannot
 // run the decode kernel (M <= 4), the fused small-M kernel runs instead.
 bool decode_light(int64_t M, int64_t n_total, int64_t K, int W, int nw) {
   const int64_t tiles = (n_total + 15) / 16;
   const int tr = decode_row_tiles((int)K, (int)M, W, nw, (int)std::min<int64_t>(tiles, INT_MAX), 1);
-  const int64_t limit = (M <= kFusedMaxM ? 180 : 160) * 1024;
+  const int64_t limit = (M <= kFusedMaxM ? 180 : M > 16 ? 200 : 160) * 1024;
   return (tiles + tr - 1) / tr * (K / kGroup) * M <= limit;
 }
 
@@ -253,9 +257,14 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
     // (decode_row_tiles); 16 waves, whose short K-ranges allow four tiles,
     // below 1024 row tiles, 8 waves from there on. Two tokens below 1024 row
     // tiles: one tile per 4-wave workgroup, as for M = 1 (measured W4A8
-    // 11008x4096 8.9 -> 7.8 us, 12288x4096 9.1 -> 8.2 us).
+    // 11008x4096 8.9 -> 7.8 us, 12288x4096 9.1 -> 8.2 us). Where K gives
+    // that many waves no work (decode_waves_useful), the most waves that all
+    // get work: at K = 1024, 4 waves against 16 for 8192 rows (W4A4 and
+    // W2A4, also as 2 x 4096) are 12-35% faster at M = 4..32 (M = 17: 7.5
+    // against 11.5 us).
     if (M == 2 && tiles < 1024 && fused_at(0)) return kDecodeFirst;
-    const int pref = tiles >= 1024 ? 1 : 2;
+    int pref = tiles >= 1024 ? 1 : 2;
+    while (pref > 0 && !decode_waves_useful(K, kSmallMWaves[pref])) --pref;
     if (fused_at(pref)) return kDecodeFirst + pref;
   } else if (M > kFusedMaxM && M <= kDecodeAutoMax) {
     // narrow N, 8- and 16-token tiles: the most waves that get work quantize
@@ -297,14 +306,20 @@ namespace {
 // at M = 24 / 32, 21.3 / 22.5 against 22.7 / 23.6 us) below 1024 row tiles
 // and 8 waves from there on;
 // narrow N above 4 tokens, the fewest waves that fit, except 16 waves for
-// 256 row tiles with K >= 4096 at W8 or above 32 tokens.
+// 256 row tiles with K >= 4096 at W8 or above 32 tokens. From 1024 row tiles
+// above 16 tokens: 16 waves first for K >= 4096 (W4A8 22016x4096 and 2 x
+// 11008x4096, W8A8 2 x 11008x4096, M = 17..64: 7-15% faster than 8 waves,
+// e.g. W4A8 2 x 11008x4096 at M = 32 33.2 against 38.4 us), 4 waves first
+// below (W4A4 16384x2048 alone, 2 x 8192x2048 and 2 x 16384x2048: 3-9%).
 int decode_packed_config(int64_t M, int64_t N, int64_t K, int W) {
   if (M < 1 || M > kDecodeAutoMax) return -1;
   const int64_t tiles = (N + 15) / 16;
   auto packed_at = [&](int c) { return decode_fits((int)K, (int)M, W, kSmallMWaves[c], true, kBF16); };
   int order[3] = {0, 1, 2};
   if (tiles > 256 && M >= 2) {
-    if (tiles >= 1024) { order[0] = 1; order[1] = M > 8 ? 2 : 0; order[2] = M > 8 ? 0 : 2; }
+    if (tiles >= 1024 && M > 16) {
+      if (K >= 4096) { order[0] = 2; order[1] = 1; order[2] = 0; }
+    } else if (tiles >= 1024) { order[0] = 1; order[1] = M > 8 ? 2 : 0; order[2] = M > 8 ? 0 : 2; }
     else if (M > 16 && M <= 32) { order[0] = 1; order[1] = 2; order[2] = 0; }  // two 16-token blocks
     else if (M > 8) { order[0] = 2; order[1] = 1; order[2] = 0; }
   } else if (M > 8 && tiles >= 256 && K >= 4096 && (W == 8 || M > 32)) {

@@ -121,6 +121,21 @@ def test_config_table():
     assert _native.default_config(50, 4096, 1024, 4, 4) == 14
     assert _native.default_config(50, 1024, 4096, 8, 4) == 15
     assert _native.default_config(50, 4096, 4096, 4, 4) == 16
+    # wide N at K = 1024 (4 quads): 4 waves, where 16 would leave 12 idle
+    assert _native.default_config(17, 8192, 1024, 4, 4) == 14
+    assert _native.default_config(8, 8192, 1024, 2, 4) == 14
+    assert _native.default_config(4, 8192, 1024, 4, 4) == 14
+    # from 1024 row tiles above 16 tokens: 16 waves for K >= 4096, 4 below
+    assert _native.default_config(32, 22016, 4096, 4, 8) == 16
+    assert _native.default_config(50, 22016, 4096, 8, 8) == 16
+    assert _native.default_config(50, 32768, 2048, 4, 4) == 14
+    assert _native.default_config(24, 16384, 2048, 4, 4) == 14
+    # in-launch quantization with 16-token blocks up to 200 group-rows per SIMD
+    import torch
+    bf16 = torch.bfloat16
+    assert _native.forward_fuses_quantizer(50, 8192, 1024, 4, 4, bf16)      # 200
+    assert not _native.forward_fuses_quantizer(64, 8192, 1024, 4, 4, bf16)  # 256
+    assert _native.forward_fuses_quantizer(50, 2048, 2048, 4, 4, bf16, 15)
     assert _native.default_config(65, 4096, 4096, 4, 8) not in (14, 15, 16)  # 192 prefill tiles
     # above 64 tokens, narrow problems (at most 128 tiles of 64x32, K <= 4096)
     # run the decode kernel in 16-token blocks
