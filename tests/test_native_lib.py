@@ -125,13 +125,13 @@ def test_config_table():
     assert _native.default_config(17, 8192, 1024, 4, 4) == 14
     assert _native.default_config(8, 8192, 1024, 2, 4) == 14
     assert _native.default_config(4, 8192, 1024, 4, 4) == 14
+    import torch
     # from 1024 row tiles above 16 tokens: 16 waves for K >= 4096, 4 below
     assert _native.default_config(32, 22016, 4096, 4, 8) == 16
     assert _native.default_config(50, 22016, 4096, 8, 8) == 16
     assert _native.default_config(50, 32768, 2048, 4, 4) == 14
     assert _native.default_config(24, 16384, 2048, 4, 4) == 14
     # in-launch quantization with 16-token blocks up to 200 group-rows per SIMD
-    import torch
     bf16 = torch.bfloat16
     assert _native.forward_fuses_quantizer(50, 8192, 1024, 4, 4, bf16)      # 200
     assert not _native.forward_fuses_quantizer(64, 8192, 1024, 4, 4, bf16)  # 256
