@@ -102,6 +102,40 @@ def test_random_multi_target_forward_against_oracle(case):
                                               f"bias={bias_dtype} scale={scale} config={config}")
 
 
+@pytest.mark.parametrize("case", range(12))
+def test_random_wide_forward_against_oracle(case):
+    """AUTO forwards at 9-64 tokens on wide N (one to three targets of
+    256-16416 rows, same or mixed widths, K up to 11008): the selection's
+    wide-N branches, shared row tiles and x quantized in the launch with
+    16-token blocks. Random codes and scales; 24 sampled columns per target
+    against the oracle."""
+    rng = np.random.default_rng(31000 + case)
+    m = int(rng.integers(9, 65))
+    k = 64 * int(rng.choice([16, 32, 64, 172]))
+    A = int(rng.choice((2, 4, 8)))
+    count = int(rng.integers(1, 4))
+    widths = [int(rng.choice((2, 4, 8))) for _ in range(count)]
+    if case % 2:
+        widths = [widths[0]] * count
+    ns = [int(rng.choice((256, 4096, 8192, 11008, 16384))) + 16 * int(rng.integers(0, 3)) for _ in range(count)]
+    g = torch.Generator().manual_seed(case)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    _, asc, ac = O.quantize_groups(bits(x), A, "bf16")
+    targets, expect = [], []
+    for W, n in zip(widths, ns):
+        q = (1 << (W - 1)) - 1
+        wc = rng.integers(-q - 1, q + 1, size=(n, k), dtype=np.int8)
+        wsc = (rng.random(n) * 0.02 + 0.001).astype(np.float32)
+        cols = np.sort(rng.choice(n, size=24, replace=False))
+        want = O.round_out(O.linear(ac, asc, wc, wsc, None, bounds=canonical_bounds(k // 64), cols=cols), "bf16")
+        targets.append((torch.from_numpy(O.pack_rows(wc, W)).to(DEV), torch.from_numpy(wsc).to(DEV), None, None, W))
+        expect.append((cols, want))
+    outs = _native.grouped_forward_multi(x.to(DEV), targets, widths[0], A)
+    for j, (out, (cols, want)) in enumerate(zip(outs, expect)):
+        np.testing.assert_array_equal(bits(out)[:, cols], want,
+                                      err_msg=f"target {j}: M={m} N={ns} K={k} W={widths} A{A}")
+
+
 @pytest.mark.parametrize("W,A", PAIRS)
 @pytest.mark.parametrize("m", [1, 2, 4, 17, 65])
 def test_exact_zero_outputs_every_config(W, A, m):
