@@ -35,6 +35,18 @@ __host__ __device__ inline int chunk_begin(int c, int G) {
   return b < G ? b : G;
 }
 
+// Chunks that hold groups: all kChunks from Q = kChunks quads on; below,
+// each nonempty chunk holds exactly one quad (its bounds differ by at most
+// Q / kChunks < 1 quads), so there are Q of them, in quad order. An empty
+// chunk's partial is +0, and a running sum of partials is never -0 (each
+// partial starts from +0 and an exact cancellation rounds to +0), so adding
+// it changes no bit: a reduction may keep one slot per nonempty chunk (its
+// quad) and skip the rest.
+__host__ __device__ inline int chunk_slots(int G) {
+  const int Q = (G + 3) / 4;
+  return Q < kChunks ? Q : kChunks;
+}
+
 // v_perm_b32: byte i of the result is byte sel.i of the 8-byte pool
 // {lo (bytes 0-3), hi (bytes 4-7)}. The host form emulates it so the layout
 // self-test can run without a GPU.

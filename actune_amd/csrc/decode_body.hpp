@@ -33,8 +33,9 @@
 //    before slot s's results are rescaled. The tokens are the MFMA A operand
 //    (token m of weight row c lands in lane 16*(m/4) + c, register m%4); one
 //    fp32 FMA per (row, token, group) rescales the exact int32 dot.
-//  * Chunk partials meet in LDS [16 chunks][16 * TR rows][MT tokens] and are
-//    added in chunk order after one barrier (wave t finishes tile t).
+//  * Chunk partials meet in LDS [16 chunks][16 * TR rows][MT tokens] (CMP:
+//    one slot per chunk that holds groups) and are added in chunk order after
+//    one barrier (wave t finishes tile t).
 #pragma once
 #include <algorithm>
 
@@ -95,9 +96,13 @@ __device__ __forceinline__ int chunk_begin_u(int c, int G) {
 // runs without bounds tests (and a fused ONE launch issues exactly the x
 // passes of the range). TR: 16-row tiles per workgroup (M > 1): the tiles share
 // the workgroup's activation slab, so x is read and quantized once per TR
-// tiles; RING is then the weight slots per tile.
-template <int W, int A, int NW, int RING, int MT, bool PACKED, bool SCALE, bool ONE, bool FULL, int TR>
+// tiles; RING is then the weight slots per tile. CMP (K below kChunks quads,
+// M > 1): the chunk partials keep one slot per nonempty chunk (chunk_slots),
+// which shrinks the workgroup's LDS where it limits how many are resident.
+template <int W, int A, int NW, int RING, int MT, bool PACKED, bool SCALE, bool ONE, bool FULL, int TR,
+          bool CMP = false>
 __device__ __forceinline__ void decode_tile(const LinearArgs& args, int GW, uint8_t* smem) {
+  static_assert(!CMP || !ONE, "compact partials are for the M > 1 slot loop");
   constexpr int GS = 8 / W;                // groups per 16-byte weight load per lane
   constexpr int CPW = kChunks / NW;        // canonical chunks per wave
   constexpr int T = shift_of(W) + shift_of(A);
@@ -326,10 +331,17 @@ __device__ __forceinline__ void decode_tile(const LinearArgs& args, int GW, uint
   const bool writer = lane < 16 * (MT / 4);
   float* red_lane = red + (size_t)(lane & 15) * MT + 4 * ((lane >> 4) & (MT / 4 - 1));
   auto write_partials = [&](int cc_) {
+    // CMP: the chunk's quad is its slot; a chunk without groups stores
+    // nothing (its partial is +0)
+    int sl = cc_;
+    if constexpr (CMP) {
+      const int b0 = chunk_begin_u(cc_, G), b1 = chunk_begin_u(cc_ + 1, G);
+      sl = b1 > b0 ? b0 >> 2 : -1;
+    }
 #pragma unroll
     for (int t = 0; t < TR; ++t) {
-      if (writer)
-        *reinterpret_cast<v4f*>(red_lane + (size_t)cc_ * RS + 16 * t * MT) = v4f{p[t][0], p[t][1], p[t][2], p[t][3]};
+      if (writer && (!CMP || sl >= 0))
+        *reinterpret_cast<v4f*>(red_lane + (size_t)sl * RS + 16 * t * MT) = v4f{p[t][0], p[t][1], p[t][2], p[t][3]};
 #pragma unroll
       for (int q = 0; q < 4; ++q) p[t][q] = 0.f;
     }
@@ -494,8 +506,20 @@ __device__ __forceinline__ void decode_tile(const LinearArgs& args, int GW, uint
       if (m < M && n < N) {
         const float* rr = red + (size_t)(16 * et + e_row) * MT + m;
         float acc = rr[0];
+        if constexpr (CMP) {
+          // the slots in chunk order, all reads issued together (indices
+          // clamped to the last slot), then added
+          const int ns = chunk_slots(G);
+          float v[kChunks];
 #pragma unroll
-        for (int q = 1; q < kChunks; ++q) acc = acc + rr[(size_t)q * RS];
+          for (int q = 1; q < kChunks; ++q) v[q] = rr[(size_t)(q < ns ? q : ns - 1) * RS];
+#pragma unroll
+          for (int q = 1; q < kChunks; ++q)
+            if (q < ns) acc = acc + v[q];
+        } else {
+#pragma unroll
+          for (int q = 1; q < kChunks; ++q) acc = acc + rr[(size_t)q * RS];
+        }
         const float y = finish_const(acc, cc, pr.bias != nullptr, bias_dt);
         const long o = (long)m * N + n;
         if (out_dt == kBF16) store_out<kBF16>(pr.out, o, y);

@@ -7,12 +7,14 @@ namespace actune {
 
 // Dynamic LDS: per wave a slab [GW groups][M tokens][64 B] and a scale slab
 // [GW][MT] (fp32, 2^-(sW+sA) folded in; entries of absent tokens unused), the
-// zero region, and the chunk partials red[16][16 * tr][MT].
-size_t decode_lds_bytes(int K, int M, int nw, int tr) {
+// zero region, and the chunk partials red[16][16 * tr][MT] (cmp:
+// red[chunk_slots(G)][16 * tr][MT]).
+size_t decode_lds_bytes(int K, int M, int nw, int tr, bool cmp) {
   M = M > 16 ? 16 : M;  // tokens of one 16-token block
   const int gw = decode_groups_per_wave(K, nw), MT = decode_token_tile(M);
+  const int slots = cmp ? chunk_slots(K / kGroup) : kChunks;
   return (size_t)nw * gw * (M * kGroup + MT * sizeof(float)) + kDecodeZeroBytes +
-         sizeof(float) * kChunks * 16 * tr * MT;
+         sizeof(float) * slots * 16 * tr * MT;
 }
 
 // At least this many workgroups when several row tiles share one (measured
@@ -44,6 +46,25 @@ int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob) {
   return tr;
 }
 
+// Workgroups of a decode launch resident at once: the CU's LDS and 16 waves
+// per CU (the M > 1 decode kernels take 100-128 VGPRs, four waves per SIMD),
+// over 256 CUs.
+long decode_resident(int nw, size_t lds) {
+  return 256L * std::min<long>(16 / nw, (long)(kCuLds / lds));
+}
+
+// Compact chunk partials for a 4-wave launch of 16-token blocks with two or
+// four row tiles per workgroup, below kChunks quads: taken where the grid
+// needs more than one round of resident workgroups and the smaller LDS lets
+// more of them be resident (W4A4 2 x 4096 x 1024 at M = 50, two tiles:
+// 50 -> 26 KB, three to four workgroups per CU for 1024 workgroups).
+bool decode_compact(int K, int M, int nw, int tr, long groups) {
+  if (nw != 4 || tr < 2 || M <= 8 || chunk_slots(K / kGroup) >= kChunks) return false;
+  const long full = decode_resident(nw, decode_lds_bytes(K, M, nw, tr)),
+             cmp = decode_resident(nw, decode_lds_bytes(K, M, nw, tr, true));
+  return groups > full && cmp > full;
+}
+
 bool decode_fits(int K, int M, int W, int nw, bool packed, int x_dt) {
   if (!packed && x_dt != kBF16) return false;  // fused mode: bf16 x
   if (M < 1 || M > kDecodeMaxM || (nw != 4 && nw != 8 && nw != 16)) return false;
@@ -58,33 +79,43 @@ bool decode_fits(int K, int M, int W, int nw, bool packed, int x_dt) {
 }
 
 // ---------------------------------------------------------------------------
-template <int W, int A, int NW, int RING, int MT, bool PACKED, bool SCALE, bool ONE, bool FULL, int TR>
+template <int W, int A, int NW, int RING, int MT, bool PACKED, bool SCALE, bool ONE, bool FULL, int TR, bool CMP>
 __global__ __launch_bounds__(NW * 64) void gemm_decode(const LinearArgs args, int GW) {
   extern __shared__ __align__(16) uint8_t smem[];
-  decode_tile<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL, TR>(args, GW, smem);
+  decode_tile<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL, TR, CMP>(args, GW, smem);
 }
 
-template <int W, int A, int NW, int MT, bool PACKED, bool SCALE, bool ONE, bool FULL, int TR = 1>
+template <int W, int A, int NW, int MT, bool PACKED, bool SCALE, bool ONE, bool FULL, int TR = 1, bool CMP = false>
 static void launch_decode_one(const LinearArgs& g, hipStream_t st) {
   constexpr int RING = decode_ring(W) / TR;
-  const size_t lds = decode_lds_bytes(g.K, g.M, NW, TR);
-  auto kern = gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL, TR>;
-  allow_dynamic_lds<gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL, TR>>();
+  const size_t lds = decode_lds_bytes(g.K, g.M, NW, TR, CMP);
+  auto kern = gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL, TR, CMP>;
+  allow_dynamic_lds<gemm_decode<W, A, NW, RING, MT, PACKED, SCALE, ONE, FULL, TR, CMP>>();
   const int groups = (decode_max_tiles(g) + TR - 1) / TR, blocks = MT == 16 ? (g.M + 15) / 16 : 1;
   kern<<<dim3((unsigned)groups, (unsigned)g.nprob, (unsigned)blocks), NW * 64, lds, st>>>(g, decode_groups_per_wave(g.K, NW));
 }
 
-// M > 1: TR row tiles per workgroup (decode_row_tiles)
+// M > 1: TR row tiles per workgroup (decode_row_tiles), compact partials
+// where decode_compact takes them (4 waves, 16-token blocks)
 template <int W, int A, int NW, int MT, bool PACKED, bool SCALE>
 static void launch_decode_tr(const LinearArgs& g, hipStream_t st) {
-  const int tr = decode_row_tiles(g.K, g.M, W, NW, decode_max_tiles(g), g.nprob * (MT == 16 ? (g.M + 15) / 16 : 1));
+  const int blocks = MT == 16 ? (g.M + 15) / 16 : 1;
+  const int tr = decode_row_tiles(g.K, g.M, W, NW, decode_max_tiles(g), g.nprob * blocks);
   const bool full = decode_full(g.K, W, NW, tr);
-#define DEC_TR(TRV)                                                                      \
-  if (full) launch_decode_one<W, A, NW, MT, PACKED, SCALE, false, true, TRV>(g, st);     \
-  else launch_decode_one<W, A, NW, MT, PACKED, SCALE, false, false, TRV>(g, st)
-  if (tr == 4) { DEC_TR(4); }
-  else if (tr == 2) { DEC_TR(2); }
-  else { DEC_TR(1); }
+#define DEC_TR(TRV, CMPV)                                                                      \
+  if (full) launch_decode_one<W, A, NW, MT, PACKED, SCALE, false, true, TRV, CMPV>(g, st);     \
+  else launch_decode_one<W, A, NW, MT, PACKED, SCALE, false, false, TRV, CMPV>(g, st)
+  if constexpr (MT == 16 && NW == 4) {
+    const long groups = (long)((decode_max_tiles(g) + tr - 1) / tr) * g.nprob * blocks;
+    if (tr >= 2 && decode_compact(g.K, g.M, NW, tr, groups)) {
+      if (tr == 4) { DEC_TR(4, true); }
+      else { DEC_TR(2, true); }
+      return;
+    }
+  }
+  if (tr == 4) { DEC_TR(4, false); }
+  else if (tr == 2) { DEC_TR(2, false); }
+  else { DEC_TR(1, false); }
 #undef DEC_TR
 }
 

@@ -108,7 +108,8 @@ void launch_decode(int W, int A, int nw, bool packed, const LinearArgs& g, hipSt
 // The decode kernel over problems of different widths (Problem::W, each in
 // {2, 4, 8}), one launch; every width must pass decode_fits
 void launch_decode_mixed(int A, int nw, bool packed, const LinearArgs& g, hipStream_t st);
-size_t decode_lds_bytes(int K, int M, int nw, int tr);
+// cmp: with compact chunk partials (one slot per nonempty chunk)
+size_t decode_lds_bytes(int K, int M, int nw, int tr, bool cmp = false);
 // true when the decode kernel with nw waves takes an M x K problem of width W
 // in the given activation mode (every wave's loads fit its register ring and
 // activation passes; the fused mode takes bf16 x only)

@@ -136,6 +136,56 @@ def test_random_wide_forward_against_oracle(case):
                                       err_msg=f"target {j}: M={m} N={ns} K={k} W={widths} A{A}")
 
 
+@pytest.mark.parametrize("W,A,ns,k,m", [(4, 4, (4096, 4096), 1024, 50), (4, 8, (16384,), 2048, 24),
+                                         (2, 4, (8192,), 320, 64), (4, 2, (12288,), 576, 40),
+                                         (8, 8, (8192, 8192), 1024, 64)])
+def test_compact_partials_on_large_grids(W, A, ns, k, m):
+    """4-wave launches of 16-token blocks with two row tiles per workgroup
+    whose grid exceeds one round of resident workgroups, below 16 quads
+    (G = 5, 9, 16, 32): the launch keeps one partial slot per nonempty chunk
+    (decode_compact). Forward with x quantized in the launch or not (config
+    14, the library's own choice), the same on the oracle's codes, and the
+    exact-zero construction after a launch that leaves nonzero partials in
+    LDS; sampled columns against the oracle."""
+    rng = np.random.default_rng(k + m + W)
+    g = torch.Generator().manual_seed(k + m)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    packed, asc, ac = O.quantize_groups(bits(x), A, "bf16")
+    targets, expect = [], []
+    for n in ns:
+        q = (1 << (W - 1)) - 1
+        wc = rng.integers(-q - 1, q + 1, size=(n, k), dtype=np.int8)
+        wsc = (rng.random(n) * 0.02 + 0.001).astype(np.float32)
+        cols = np.sort(rng.choice(n, size=32, replace=False))
+        want = O.round_out(O.linear(ac, asc, wc, wsc, None, bounds=canonical_bounds(k // 64), cols=cols), "bf16")
+        targets.append((torch.from_numpy(O.pack_rows(wc, W)).to(DEV), torch.from_numpy(wsc).to(DEV), None, None))
+        expect.append((cols, want))
+    outs = _native.grouped_forward_multi(x.to(DEV), targets, W, A, config=14)
+    for j, (out, (cols, want)) in enumerate(zip(outs, expect)):
+        np.testing.assert_array_equal(bits(out)[:, cols], want, err_msg=f"forward, target {j}")
+    a_dev, s_dev = torch.from_numpy(packed).to(DEV), torch.from_numpy(asc).to(DEV)
+    w_dev, ws_dev, _, _ = targets[0]
+    cols, want = expect[0]
+    got = _native.grouped_linear(a_dev, s_dev, w_dev, ws_dev, None, (m, k), W, A, 14)
+    np.testing.assert_array_equal(bits(got)[:, cols], want, err_msg="on codes")
+    # exact zeros on the same grid: group 4 of x repeats group 0 and every
+    # weight row holds c in group 0, -c in group 4 (quads 0 and 1, so two
+    # chunks below 16 quads) and zeros elsewhere
+    xz = torch.randn(m, k, generator=g)
+    xz[:, 256:320] = xz[:, 0:64]
+    xz = xz.to(torch.bfloat16)
+    q = (1 << (W - 1)) - 1
+    zero_targets = []
+    for (w_dev, ws_dev, _, _), n in zip(targets, ns):
+        wz = np.zeros((n, k), np.int8)
+        c = rng.integers(-q, q + 1, size=(n, 64), dtype=np.int8)
+        wz[:, 0:64], wz[:, 256:320] = c, -c
+        zero_targets.append((torch.from_numpy(O.pack_rows(wz, W)).to(DEV), ws_dev, None, None))
+    _native.grouped_forward_multi(x.to(DEV), targets, W, A, config=14)
+    for j, got in enumerate(_native.grouped_forward_multi(xz.to(DEV), zero_targets, W, A, config=14)):
+        assert not bits(got).any(), f"a term leaked into a zero output, target {j}"
+
+
 @pytest.mark.parametrize("W,A", PAIRS)
 @pytest.mark.parametrize("m", [1, 2, 4, 17, 65])
 def test_exact_zero_outputs_every_config(W, A, m):
