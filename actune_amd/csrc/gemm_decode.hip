@@ -40,9 +40,17 @@ int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob) {
     if (slots * c <= decode_ring(W) && (tiles + c - 1) / c * nprob >= kDecodeMinGroups &&
         decode_lds_bytes(K, M, nw, c) <= kStreamLdsMax)
       tr = c;
-  if (tr == 4 && M > 8 && 2 * decode_lds_bytes(K, M, nw, 4) > kCuLds && 2 * decode_lds_bytes(K, M, nw, 2) <= kCuLds &&
-      (tiles + 1) / 2 * nprob >= 2 * 256)
+  if (tr == 4 && M > 8 && nw == 4 && chunk_slots(K / kGroup) < kChunks) {
+    // a launch that can take compact partials (decode_compact) keeps four
+    // tiles, x quantized once per four, while that grid still gives every
+    // CU two workgroups (W4A4 2 x 4096 x 1024 at M = 50: 10.8 -> 10.2 us;
+    // 16384 x 2048 at M = 24: 15.0 -> 12.3 us; with half that grid, 8192 x
+    // 1024 at M = 17, four tiles were 12% slower than two)
+    if ((tiles + 3) / 4 * nprob < 2 * 256 && (tiles + 1) / 2 * nprob >= 2 * 256) tr = 2;
+  } else if (tr == 4 && M > 8 && 2 * decode_lds_bytes(K, M, nw, 4) > kCuLds &&
+             2 * decode_lds_bytes(K, M, nw, 2) <= kCuLds && (tiles + 1) / 2 * nprob >= 2 * 256) {
     tr = 2;
+  }
   return tr;
 }
 
