@@ -100,9 +100,10 @@ int packed_default(int64_t M, int64_t N, int64_t K, int W, int A);
 // and 12.6 -> 12.0 us, 2048x2048 8.2 -> 7.7 us), at 256 some were slower
 // (8192x1024 at M = 64: 13.0 against 13.4 us). Where the codes path cannot
 // run the decode kernel (M <= 4), the fused small-M kernel runs instead.
-bool decode_light(int64_t M, int64_t n_total, int64_t K, int W, int nw) {
+// compact: as for decode_row_tiles (false for the mixed-width kernel).
+bool decode_light(int64_t M, int64_t n_total, int64_t K, int W, int nw, bool compact = true) {
   const int64_t tiles = (n_total + 15) / 16;
-  const int tr = decode_row_tiles((int)K, (int)M, W, nw, (int)std::min<int64_t>(tiles, INT_MAX), 1);
+  const int tr = decode_row_tiles((int)K, (int)M, W, nw, (int)std::min<int64_t>(tiles, INT_MAX), 1, compact);
   const int64_t limit = (M <= kFusedMaxM ? 180 : M > 16 ? 200 : 160) * 1024;
   return (tiles + tr - 1) / tr * (K / kGroup) * M <= limit;
 }
@@ -434,7 +435,8 @@ int forward_mixed(LinearArgs& g, int config, bool auto_config, int64_t n_total, 
   for (int q = 0; q < g.nprob; ++q) wmax = std::max(wmax, g.prob[q].W);
   if (config >= kDecodeFirst) {
     const int nw = kSmallMWaves[config - kDecodeFirst];
-    const bool fused = decode_fits(g.K, g.M, wmax, nw, false, x_dtype) && decode_light(g.M, n_total, g.K, wmax, nw);
+    const bool fused =
+        decode_fits(g.K, g.M, wmax, nw, false, x_dtype) && decode_light(g.M, n_total, g.K, wmax, nw, false);
     bool fits = true;
     for (int q = 0; q < g.nprob; ++q) fits = fits && decode_fits(g.K, g.M, g.prob[q].W, nw, !fused, x_dtype);
     if (fits) {

@@ -32,7 +32,7 @@ constexpr size_t kCuLds = 160 * 1024;  // LDS of one gfx950 CU
 // at M = 50, four waves: 13.2 -> 10.6 us; at M = 24, 11008 x 4096, where two
 // tiles also leave one workgroup per CU, four stay faster: 19.1 against
 // 28.2 us for one).
-int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob) {
+int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob, bool compact) {
   if (M < 2) return 1;
   const int slots = (decode_groups_per_wave(K, nw) + 8 / W - 1) / (8 / W);
   int tr = 1;
@@ -40,7 +40,7 @@ int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob) {
     if (slots * c <= decode_ring(W) && (tiles + c - 1) / c * nprob >= kDecodeMinGroups &&
         decode_lds_bytes(K, M, nw, c) <= kStreamLdsMax)
       tr = c;
-  if (tr == 4 && M > 8 && nw == 4 && chunk_slots(K / kGroup) < kChunks) {
+  if (tr == 4 && M > 8 && compact && nw == 4 && chunk_slots(K / kGroup) < kChunks) {
     // a launch that can take compact partials (decode_compact) keeps four
     // tiles, x quantized once per four, while that grid still gives every
     // CU two workgroups (W4A4 2 x 4096 x 1024 at M = 50: 10.8 -> 10.2 us;

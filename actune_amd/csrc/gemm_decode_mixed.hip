@@ -38,7 +38,7 @@ void launch_mixed_tr(const LinearArgs& g, hipStream_t st) {
   const int blocks = MT == 16 ? (g.M + 15) / 16 : 1;
   int tr = 4;
   for (int q = 0; q < g.nprob; ++q)
-    tr = std::min(tr, decode_row_tiles(g.K, g.M, g.prob[q].W, NW, decode_max_tiles(g), g.nprob * blocks));
+    tr = std::min(tr, decode_row_tiles(g.K, g.M, g.prob[q].W, NW, decode_max_tiles(g), g.nprob * blocks, false));
   if (tr == 4) launch_mixed_one<A, NW, MT, PACKED, SCALE, false, 4>(g, st);
   else if (tr == 2) launch_mixed_one<A, NW, MT, PACKED, SCALE, false, 2>(g, st);
   else launch_mixed_one<A, NW, MT, PACKED, SCALE, false, 1>(g, st);

@@ -116,7 +116,9 @@ size_t decode_lds_bytes(int K, int M, int nw, int tr, bool cmp = false);
 bool decode_fits(int K, int M, int W, int nw, bool packed, int x_dt);
 // 16-row tiles per workgroup of a decode launch (1, 2 or 4) for nprob
 // problems of `tiles` row tiles each; results do not depend on it
-int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob);
+// compact: the launch can take compact chunk partials (the single-width
+// kernel; the mixed-width kernel cannot)
+int decode_row_tiles(int K, int M, int W, int nw, int tiles, int nprob, bool compact = true);
 size_t stream_lds_bytes(int K, int M, int nw);
 
 }  // namespace actune
