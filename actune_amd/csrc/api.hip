@@ -93,18 +93,23 @@ int packed_default(int64_t M, int64_t N, int64_t K, int W, int A);
 // quantizes the whole activation, so the in-launch work grows as workgroups
 // (row tiles / tiles per workgroup) x groups x tokens; measured on MI355X
 // (W4A8, M = 1..8, N = 2048..22016), past about 180 (4-token tiles) or 160
-// (8-token tiles) group-rows per SIMD (1024 SIMDs) the quantizer launch
-// followed by the GEMM on its codes is faster. With 16-token blocks (M > 16)
-// the limit is 200: at M = 50 every launch measured at 200 was faster fused
-// (W4A4 4096x1024 8.9 -> 8.5 us, 8192x1024 and 2 x 4096x1024 12.3 -> 11.5
-// and 12.6 -> 12.0 us, 2048x2048 8.2 -> 7.7 us), at 256 some were slower
-// (8192x1024 at M = 64: 13.0 against 13.4 us). Where the codes path cannot
-// run the decode kernel (M <= 4), the fused small-M kernel runs instead.
+// (one 16-token block, M = 9..16) group-rows per SIMD (1024 SIMDs) the
+// quantizer launch followed by the GEMM on its codes is faster. With
+// 8-token tiles (M = 5..8) the limit is 300: every launch measured up to 301
+// was faster fused (W4A8 and W2A8 2 x 11008x4096, W4A8 22016x4096, M = 5-7:
+// +0.3 to +9%, e.g. W4A8 2 x 11008x4096 at M = 5 16.3 -> 14.9 us), at 344
+// one was slower (W2A8 2 x 11008x4096 at M = 8: 13.4 against 14.1 us).
+// With 16-token blocks (M > 16) the limit is 200: at M = 50 every launch
+// measured at 200 was faster fused (W4A4 4096x1024 8.9 -> 8.5 us, 8192x1024
+// and 2 x 4096x1024 12.3 -> 11.5 and 12.6 -> 12.0 us, 2048x2048 8.2 -> 7.7
+// us), at 256 some were slower (8192x1024 at M = 64: 13.0 against 13.4 us).
+// Where the codes path cannot run the decode kernel (M <= 4), the fused
+// small-M kernel runs instead.
 // compact: as for decode_row_tiles (false for the mixed-width kernel).
 bool decode_light(int64_t M, int64_t n_total, int64_t K, int W, int nw, bool compact = true) {
   const int64_t tiles = (n_total + 15) / 16;
   const int tr = decode_row_tiles((int)K, (int)M, W, nw, (int)std::min<int64_t>(tiles, INT_MAX), 1, compact);
-  const int64_t limit = (M <= kFusedMaxM ? 180 : M > 16 ? 200 : 160) * 1024;
+  const int64_t limit = (M <= kFusedMaxM ? 180 : M <= 8 ? 300 : M <= 16 ? 160 : 200) * 1024;
   return (tiles + tr - 1) / tr * (K / kGroup) * M <= limit;
 }
 

@@ -131,6 +131,10 @@ def test_config_table():
     assert _native.default_config(50, 22016, 4096, 8, 8) == 16
     assert _native.default_config(50, 32768, 2048, 4, 4) == 14
     assert _native.default_config(24, 16384, 2048, 4, 4) == 14
+    # in-launch quantization with 8-token tiles up to 300 group-rows per SIMD
+    # (W4A8 22016x4096: 215 at M = 5, 344 at M = 8)
+    assert _native.forward_fuses_quantizer(5, 22016, 4096, 4, 8, torch.bfloat16)
+    assert not _native.forward_fuses_quantizer(8, 22016, 4096, 4, 8, torch.bfloat16)
     # in-launch quantization with 16-token blocks up to 200 group-rows per SIMD
     bf16 = torch.bfloat16
     assert _native.forward_fuses_quantizer(50, 8192, 1024, 4, 4, bf16)      # 200
