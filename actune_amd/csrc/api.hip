@@ -277,7 +277,12 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
     // x in the launch where light. Above 12 tokens 16 waves do not: at 1024
     // rows and K = 4096 the 8-wave launch on the quantizer's codes is faster
     // (measured W4A4/W8A4/W2A8, M = 14-24: 7.9-8.4 against 8.2-9.0 us;
-    // M = 9-12: 16 waves in-launch 6.3-7.9 against 7.2-8.1 us)
+    // M = 9-12: 16 waves in-launch 6.3-7.9 against 7.2-8.1 us). W8 with
+    // 8-token tiles: 8 waves where they quantize x in the launch (a full
+    // ring at K = 4096; W8A8/A4/A2, N = 1024-4096, K = 4096: 13-16% faster
+    // than 16 waves at M = 5, 3-5% at M = 8, e.g. W8A8 4096x4096 at M = 5
+    // 6.7 against 7.6 us; W4 keeps 16 waves, faster at M = 8)
+    if (W == 8 && M <= 8 && decode_waves_useful(K, 8) && fused_at(1)) return kDecodeFirst + 1;
     for (int c = 2; c >= 0; --c) {
       if (kSmallMWaves[c] == 16 && M > 12) continue;
       if (decode_waves_useful(K, kSmallMWaves[c]) && fused_at(c)) return kDecodeFirst + c;

@@ -131,6 +131,12 @@ def test_config_table():
     assert _native.default_config(50, 22016, 4096, 8, 8) == 16
     assert _native.default_config(50, 32768, 2048, 4, 4) == 14
     assert _native.default_config(24, 16384, 2048, 4, 4) == 14
+    # narrow W8 at 5-8 tokens: 8 waves with x quantized in the launch; W4 keeps 16
+    assert _native.default_config(5, 4096, 4096, 8, 8) == 15
+    assert _native.default_config(8, 1024, 4096, 8, 4) == 15
+    assert _native.forward_fuses_quantizer(8, 1024, 4096, 8, 4, torch.bfloat16)
+    assert _native.default_config(8, 4096, 4096, 4, 8) == 16
+    assert _native.default_config(8, 4096, 8192, 8, 8) == 16  # 8 waves do not hold K = 8192 of W8
     # in-launch quantization with 8-token tiles up to 300 group-rows per SIMD
     # (W4A8 22016x4096: 215 at M = 5, 344 at M = 8)
     assert _native.forward_fuses_quantizer(5, 22016, 4096, 4, 8, torch.bfloat16)
