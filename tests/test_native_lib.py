@@ -131,6 +131,11 @@ def test_config_table():
     assert _native.default_config(50, 22016, 4096, 8, 8) == 16
     assert _native.default_config(50, 32768, 2048, 4, 4) == 14
     assert _native.default_config(24, 16384, 2048, 4, 4) == 14
+    # W8 4096x4096 at 13-16 tokens: 8 waves on codes; 16 waves in the launch at 9-12, on codes from 17
+    assert _native.default_config(13, 4096, 4096, 8, 4) == 15
+    assert _native.default_config(16, 4096, 4096, 8, 8) == 15
+    assert _native.default_config(10, 4096, 4096, 8, 8) == 16
+    assert _native.default_config(17, 4096, 4096, 8, 8) == 16
     # narrow W8 at 5-8 tokens: 8 waves with x quantized in the launch; W4 keeps 16
     assert _native.default_config(5, 4096, 4096, 8, 8) == 15
     assert _native.default_config(8, 1024, 4096, 8, 4) == 15
