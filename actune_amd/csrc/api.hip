@@ -298,9 +298,12 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
     // narrow N, M <= 4: fewer waves per tile cost less per-workgroup work, so
     // take the smallest wave count that still gives every SIMD a wave (tiles
     // x waves >= 1024, or the most waves that get work) and fits K, with x
-    // quantized in the launch where that pays (decode_light)
+    // quantized in the launch where that pays (decode_light). W8 takes at
+    // most 8 waves: over W8A8/A4/A2 at N = 1024-4096, K = 1024-4096, M = 2-4
+    // 16 waves were never the fastest (W8A4 1024x4096 at M = 2: 8 waves 4.75
+    // against 5.69 us for 16)
     for (int c = 0; c < 3; ++c) {
-      const bool last = c == 2 || !decode_waves_useful(K, kSmallMWaves[c + 1]);
+      const bool last = c == 2 || !decode_waves_useful(K, kSmallMWaves[c + 1]) || (W == 8 && c == 1);
       if (!(tiles * kSmallMWaves[c] >= 1024 || last)) continue;
       if (decode_waves_useful(K, kSmallMWaves[c]) && fused_at(c)) return kDecodeFirst + c;
     }
