@@ -301,7 +301,11 @@ int actune_default_config(int64_t M, int64_t N, int64_t K, int W, int A) {
     // quantized in the launch where that pays (decode_light). W8 takes at
     // most 8 waves: over W8A8/A4/A2 at N = 1024-4096, K = 1024-4096, M = 2-4
     // 16 waves were never the fastest (W8A4 1024x4096 at M = 2: 8 waves 4.75
-    // against 5.69 us for 16)
+    // against 5.69 us for 16). W2 at K >= 4096 takes 16 waves where they
+    // quantize x in the launch (one load slot per wave): 4-11% faster at
+    // 2048x4096 and 4096x4096, M = 2-4, every A (W2A4 4096x4096 at M = 4:
+    // 5.15 against 5.64 us for 8 waves)
+    if (W == 2 && K >= 4096 && decode_waves_useful(K, 16) && fused_at(2)) return kDecodeFirst + 2;
     for (int c = 0; c < 3; ++c) {
       const bool last = c == 2 || !decode_waves_useful(K, kSmallMWaves[c + 1]) || (W == 8 && c == 1);
       if (!(tiles * kSmallMWaves[c] >= 1024 || last)) continue;

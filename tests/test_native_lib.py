@@ -131,10 +131,13 @@ def test_config_table():
     assert _native.default_config(50, 22016, 4096, 8, 8) == 16
     assert _native.default_config(50, 32768, 2048, 4, 4) == 14
     assert _native.default_config(24, 16384, 2048, 4, 4) == 14
-    # W8 at 2-4 tokens takes at most 8 waves; W2 / W4 keep their counts
+    # W8 at 2-4 tokens takes at most 8 waves; W2 at K >= 4096 takes 16
     assert _native.default_config(2, 1024, 4096, 8, 4) == 15
     assert _native.default_config(4, 1024, 1024, 8, 8) == 14
     assert _native.default_config(3, 1024, 4096, 2, 8) == 16
+    assert _native.default_config(2, 4096, 4096, 2, 4) == 16
+    assert _native.default_config(4, 2048, 4096, 2, 2) == 16
+    assert _native.default_config(2, 4096, 2048, 2, 4) == 14
     # W8 4096x4096 at 13-16 tokens: 8 waves on codes; 16 waves in the launch at 9-12, on codes from 17
     assert _native.default_config(13, 4096, 4096, 8, 4) == 15
     assert _native.default_config(16, 4096, 4096, 8, 8) == 15
